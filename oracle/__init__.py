@@ -1,0 +1,11 @@
+"""CPU oracle for the MTP speculative-decoding verify step. TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s `cpu_baseline` leg may import this package, and only as the
+checker (or the timed CPU baseline), never as part of the product path: the HIP library under
+`qwen38-27b-aws_amd/` never calls into it and fails loudly when its own extension is missing.
+
+`oracle.model` restates the reference's CPU path (qwen38_inf2/model.py, generate.py, scheduler.py) in torch CPU ops
+at the same rounding points, with this build's weight format (FP8 e4m3 + E8M0 per 32) in place of the reference's
+e5m2 bytes. Pinning (which check fixes each function) is listed in each function's docstring; a function with no
+such check says "parity unpinned".
+"""

@@ -1,0 +1,444 @@
+"""CPU restatement of the reference's verify-step semantics. TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Every function follows the reference CPU path op for op, in torch CPU, at the same rounding points (dtype bf16 in
+production; float32 for the invariant tests, as the reference's own tests do). The one deliberate difference is the
+weight format: FP8 e4m3 bytes ``[out, in]`` with an E8M0 scale per 32 inputs, dequantized exactly, where the
+reference decodes e5m2 bytes ``[in, out]`` (qwen38_inf2/model.py:221-225, fp4.py:157-166).
+
+Pinning of each function (what fixes it besides this text):
+* tests/golden/verify_tiny.safetensors, written by tests/golden/make_golden.py from the reference's own CPU path
+  (imported in the build container): pins `gdn_verify`, `attention_verify`, `mlp`, `decoder_layer`, `step_verify`,
+  `mtp_forward`, `head_group_maxima`, `chip_next_tokens`, `accept` bit for bit on config 0 shapes.
+* invariants in tests/test_oracle.py: verify with every token accepted equals sequential `gdn_decode`/`attention_decode`
+  steps (reference tests/test_prefill.py:235-263); the textbook recurrence in float64; full-softmax attention by brute
+  force; ChipHead equals HostHead (reference tests/test_model_parity.py:280-309); e4m3 dequantization against its bit
+  fields; e5m2 rounding against an exhaustive bf16 table.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+# Added to the scores of unfilled cache slots (model.py:30-32).
+MASKED_SCORE = -1e4
+# The reference rounds every FP8 projection's input to e5m2 (model.py:85-87, 222-225). Tests that compare two float32
+# forms of the same computation switch it off, as reference tests/test_model_parity.py:255-260 does.
+ROUND_E5M2 = True
+
+
+# ----------------------------------------------------------------------------------------------- elementwise pieces
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """model.py:48-51."""
+    return x * torch.sigmoid(x)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """model.py:54-57: float32 inside, ``(1 + weight)``, result in x's dtype."""
+    h = x.float()
+    h = h * torch.rsqrt((h * h).mean(-1, keepdim=True) + eps)
+    return (h * (1.0 + weight.float())).type_as(x)
+
+
+def l2_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """model.py:60-61."""
+    return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
+
+
+def repeat_interleave(x: torch.Tensor, repeats: int, dim: int) -> torch.Tensor:
+    """model.py:64-67."""
+    expanded = x.unsqueeze(dim + 1).expand(*x.shape[: dim + 1], repeats, *x.shape[dim + 1 :])
+    return expanded.reshape(*x.shape[:dim], x.shape[dim] * repeats, *x.shape[dim + 1 :])
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """model.py:70-72."""
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rotary(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """model.py:75-82: partial RoPE on the first ``cos.shape[-1]`` dims."""
+    cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    rot = cos.shape[-1]
+    q_rot, q_pass = q[..., :rot], q[..., rot:]
+    k_rot, k_pass = k[..., :rot], k[..., rot:]
+    q_out = q_rot * cos + rotate_half(q_rot) * sin
+    k_out = k_rot * cos + rotate_half(k_rot) * sin
+    return torch.cat((q_out, q_pass), dim=-1), torch.cat((k_out, k_pass), dim=-1)
+
+
+def fp8_round(x: torch.Tensor) -> torch.Tensor:
+    """model.py:85-87: round to e5m2 and back."""
+    return x.to(torch.float8_e5m2).to(x.dtype) if ROUND_E5M2 else x
+
+
+def e4m3_to_float(coded: torch.Tensor) -> torch.Tensor:
+    """OCP e4m3fn bytes to float32 from the bit fields: sign, 4 exponent bits (bias 7), 3 mantissa bits, subnormals
+    at exponent 0, and 0x7F/0xFF NaN. Written from the format definition rather than torch's cast, so tests can hold
+    the two against each other."""
+    b = coded.to(torch.int32)
+    exponent, mantissa = (b >> 3) & 15, b & 7
+    magnitude = torch.where(
+        exponent == 0, mantissa.float() * 2.0**-9, (1.0 + mantissa.float() / 8.0) * torch.pow(2.0, exponent.float() - 7.0)
+    )
+    magnitude = torch.where((b & 127) == 127, torch.full_like(magnitude, float("nan")), magnitude)
+    return torch.where(b >= 128, -magnitude, magnitude)
+
+
+class FP8Weight:
+    """One projection's weight: e4m3 bytes ``[out, in]`` and E8M0 bytes ``[out, in/32]``."""
+
+    def __init__(self, coded: torch.Tensor, scales: torch.Tensor):
+        self.coded, self.scales = coded, scales
+        self._dense_t = None
+
+    def dense_t(self) -> torch.Tensor:
+        """float32 ``[in, out]``, contiguous, the layout the reference's weights have (``weight_fp8`` is
+        ``[in, out]``, model.py:214-219), so torch's CPU matmuls see the same strides and sum in the same order.
+        Exact, and exact again in bf16."""
+        if self._dense_t is None:
+            n, k = self.coded.shape
+            values = e4m3_to_float(self.coded).reshape(n, k // 32, 32)
+            scale = torch.pow(2.0, self.scales.float() - 127.0).unsqueeze(-1)
+            self._dense_t = (values * scale).reshape(n, k).T.contiguous()
+        return self._dense_t
+
+    def dense(self) -> torch.Tensor:
+        """float32 ``[out, in]`` (a transposed view)."""
+        return self.dense_t().T
+
+
+def linear_fp8(x: torch.Tensor, weight: FP8Weight) -> torch.Tensor:
+    """`FP8Linear.forward` on CPU (model.py:221-225): e5m2 input, weights in x's dtype, x's dtype out."""
+    x = fp8_round(x)
+    return F.linear(x, weight.dense_t().T.to(x.dtype))
+
+
+def mlp(w: dict, x: torch.Tensor) -> torch.Tensor:
+    """`MLP.forward` on CPU (model.py:250-259), tp 1."""
+    return linear_fp8(silu(linear_fp8(x, w["mlp.gate_proj"])) * linear_fp8(x, w["mlp.up_proj"]), w["mlp.down_proj"])
+
+
+# ----------------------------------------------------------------------------------------------- gated delta net
+
+
+def _gdn_split(cfg, mixed: torch.Tensor):
+    """`GatedDeltaNetStep._split` (model.py:322-331): q, k per value head and v, float32; q scaled by d^-1/2."""
+    tokens = mixed.shape[0]
+    k_head, v_head = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    key_dim = cfg.linear_key_dim
+    query = mixed[:, :key_dim].reshape(tokens, cfg.linear_num_key_heads, k_head)
+    key = mixed[:, key_dim : 2 * key_dim].reshape(tokens, cfg.linear_num_key_heads, k_head)
+    value = mixed[:, 2 * key_dim :].reshape(tokens, cfg.linear_num_value_heads, v_head)
+    query = repeat_interleave(query, cfg.linear_key_repeat, dim=1)
+    key = repeat_interleave(key, cfg.linear_key_repeat, dim=1)
+    return l2_norm(query.float()) / math.sqrt(k_head), l2_norm(key.float()), value.float()
+
+
+def _gdn_gates(w: dict, x: torch.Tensor):
+    """`GatedDeltaNetStep._gates` (model.py:333-337): beta and log decay, float32 ``[tokens, v_heads]``."""
+    beta = F.linear(x, w["linear_attn.in_proj_b"]).sigmoid().float()
+    a = F.linear(x, w["linear_attn.in_proj_a"]).float()
+    return beta, -w["linear_attn.A_log"].float().exp() * F.softplus(a + w["linear_attn.dt_bias"].float())
+
+
+def _gdn_finish(cfg, w: dict, out: torch.Tensor, z: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """`GatedDeltaNetStep._finish` (model.py:339-345): gated RMS norm per value head (weight without 1+), then
+    out_proj. ``out``, ``z`` ``[tokens, v_heads, v_head]``."""
+    h = out.float()
+    h = h * torch.rsqrt((h * h).mean(-1, keepdim=True) + cfg.rms_norm_eps)
+    h = w["linear_attn.norm_weight"] * h.to(dtype)
+    h = (h * silu(z.float())).to(dtype)
+    return linear_fp8(h.reshape(out.shape[0], 1, cfg.linear_value_dim), w["linear_attn.out_proj"])
+
+
+def commit_and_read(state, scale, weighted, deltas, reads):
+    """`_commit_and_read` CPU branch (model.py:262-266): ``S' = (S*scale + W^T D)`` rounded to the state's dtype, and
+    ``R^T float(S')``."""
+    committed = (state.float() * scale + weighted.transpose(1, 2) @ deltas).to(state.dtype)
+    return committed, reads.transpose(1, 2) @ committed.float()
+
+
+def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
+    """`GatedDeltaNetStep.verify` (model.py:376-454), tp 1. ``x`` ``[B, K, H]`` (the input norm's output).
+
+    ``st`` holds ``recurrent_state [B,Hv,d,d]``, ``conv_state [B,C,3]``, ``pending_key_state [B,K,Hv,d]`` (f32),
+    ``pending_delta_state [B,K,Hv,d]`` (f32), ``pending_decay_state [B,K,Hv]`` (f32), ``pending_input_state [B,K,C]``;
+    the entries are replaced by their new values. Returns ``[B, K, H]``.
+    """
+    dtype = x.dtype
+    batch, tokens = x.shape[:2]
+    kernel = cfg.linear_conv_kernel_dim
+    on = (active > 0.5).reshape(batch, 1)
+    keep = torch.where((position.reshape(batch, 1) == 0) & on, 0.0, 1.0)
+    taken = [(accepted.reshape(batch, 1) > s).float() for s in range(st["pending_key_state"].shape[1])]
+    decays = [st["pending_decay_state"][:, s] * taken[s] for s in range(len(taken))]
+    remaining, weighted = sum(decays), []
+    scale = torch.where(on, remaining.exp() * keep, 1.0)
+    for s in range(len(taken)):
+        remaining = remaining - decays[s]
+        weighted.append(st["pending_key_state"][:, s] * (remaining.exp() * taken[s] * keep * on).unsqueeze(-1))
+    window = torch.cat((st["conv_state"], st["pending_input_state"].transpose(1, 2)), dim=-1)
+    index = (accepted.long().reshape(batch, 1, 1) + torch.arange(kernel - 1)).expand(-1, window.shape[1], -1)
+    history = window.gather(2, index) * keep.reshape(batch, 1, 1).to(dtype)
+    history = torch.where(on.reshape(batch, 1, 1), history, st["conv_state"])
+    st["conv_state"] = history
+
+    qkv = linear_fp8(x, w["linear_attn.in_proj_qkv"])
+    window = torch.cat((history, qkv.transpose(1, 2)), dim=-1)
+    conv_weight = w["linear_attn.conv_weight"]
+    mixed = torch.stack([(window[:, :, t : t + kernel] * conv_weight).sum(dim=-1) for t in range(tokens)], dim=1)
+    query, key, value = (
+        part.reshape(batch, tokens, *part.shape[1:]) for part in _gdn_split(cfg, silu(mixed).reshape(batch * tokens, -1))
+    )
+    heads = cfg.linear_num_value_heads
+    z = linear_fp8(x, w["linear_attn.in_proj_z"]).reshape(batch * tokens, heads, -1)
+    beta, log_decay = _gdn_gates(w, x.reshape(batch * tokens, -1))
+    beta = beta.reshape(batch, tokens, -1) * active.reshape(batch, 1, 1)
+    log_decay = log_decay.reshape(batch, tokens, -1) * active.reshape(batch, 1, 1)
+
+    state = st["recurrent_state"]
+    k_head, v_head = state.shape[2:]
+    pairs = batch * heads
+    committed, products = commit_and_read(
+        state.reshape(pairs, k_head, v_head),
+        scale.reshape(pairs, 1, 1).expand(-1, k_head, -1),
+        torch.stack(weighted, dim=2).reshape(pairs, -1, k_head),
+        st["pending_delta_state"].transpose(1, 2).reshape(pairs, -1, v_head),
+        torch.cat((key, query), dim=1).permute(0, 2, 3, 1).reshape(pairs, k_head, 2 * tokens),
+    )
+    st["recurrent_state"] = committed.reshape(batch, heads, k_head, v_head)
+    products = products.reshape(batch, heads, 2 * tokens, v_head).transpose(1, 2)
+    key_state, query_state = products[:, :tokens], products[:, tokens:]
+
+    cumulative = [log_decay[:, 0]]
+    for t in range(1, tokens):
+        cumulative.append(cumulative[-1] + log_decay[:, t])
+    deltas, outs = [], []
+    for t in range(tokens):
+        delta = value[:, t] - cumulative[t].exp().unsqueeze(-1) * key_state[:, t]
+        for s in range(t):
+            coupling = (cumulative[t] - cumulative[s]).exp() * (key[:, t] * key[:, s]).sum(dim=-1)
+            delta = delta - coupling.unsqueeze(-1) * deltas[s]
+        deltas.append(delta * beta[:, t].unsqueeze(-1))
+        out = cumulative[t].exp().unsqueeze(-1) * query_state[:, t]
+        for s in range(t + 1):
+            attend = (cumulative[t] - cumulative[s]).exp() * (query[:, t] * key[:, s]).sum(dim=-1)
+            out = out + attend.unsqueeze(-1) * deltas[s]
+        outs.append(out)
+    delta, out = torch.stack(deltas, dim=1), torch.stack(outs, dim=1)
+    # The reference adds the commit kernel's zero output to order these writes after its reads (model.py:449-452);
+    # adding 0.0 also turns -0.0 into +0.0, which the stored bits show.
+    st["pending_key_state"] = key.float() + 0.0
+    st["pending_delta_state"] = delta
+    st["pending_decay_state"] = log_decay.float() + 0.0
+    st["pending_input_state"] = qkv + torch.zeros((), dtype=qkv.dtype)
+    out = out.reshape(batch * tokens, heads, -1).to(dtype)
+    return _gdn_finish(cfg, w, out, z, dtype).reshape(batch, tokens, -1)
+
+
+def gdn_decode(cfg, w: dict, st: dict, x, position, active):
+    """`GatedDeltaNetStep.forward` (model.py:347-374): one token per row, ``x`` ``[B, 1, H]``. Used only to check the
+    verify form against (reference tests/test_prefill.py:235-263)."""
+    dtype = x.dtype
+    batch = x.shape[0]
+    on = active.reshape(batch, 1, 1) > 0.5
+    keep = torch.where((position == 0) & (active > 0.5), 0.0, 1.0)
+    qkv = linear_fp8(x, w["linear_attn.in_proj_qkv"]).transpose(1, 2)
+    conv_state = st["conv_state"]
+    window = torch.cat((conv_state * keep.reshape(batch, 1, 1).to(dtype), qkv), dim=-1)
+    st["conv_state"] = torch.where(on, window[:, :, 1:], conv_state)
+    query, key, value = _gdn_split(cfg, silu((window * w["linear_attn.conv_weight"]).sum(dim=-1)))
+    heads = cfg.linear_num_value_heads
+    z = linear_fp8(x, w["linear_attn.in_proj_z"]).reshape(batch, heads, -1)
+    beta, log_decay = _gdn_gates(w, x.reshape(batch, -1))
+    beta = (beta * active.unsqueeze(-1)).unsqueeze(-1)
+    log_decay = log_decay * active.unsqueeze(-1)
+    state = st["recurrent_state"].float() * keep.reshape(batch, 1, 1, 1) * log_decay.exp()[..., None, None]
+    delta = (value - (state * key.unsqueeze(-1)).sum(dim=-2)) * beta
+    state = state + key.unsqueeze(-1) * delta.unsqueeze(-2)
+    st["recurrent_state"] = state.to(st["recurrent_state"].dtype)
+    out = (state * query.unsqueeze(-1)).sum(dim=-2).to(dtype)
+    return _gdn_finish(cfg, w, out, z, dtype)
+
+
+# ----------------------------------------------------------------------------------------------- full attention
+
+
+def _attention_project(cfg, w: dict, x, cos, sin):
+    """`FullAttentionStep._project` (model.py:565-577)."""
+    head = cfg.head_dim
+    rows, tokens = x.shape[:2]
+    q_and_gate = linear_fp8(x, w["self_attn.q_proj"]).reshape(rows, tokens, cfg.num_attention_heads, head * 2)
+    query, gate = q_and_gate[..., :head], q_and_gate[..., head:]
+    query = rms_norm(query, w["self_attn.q_norm_weight"], cfg.rms_norm_eps).transpose(1, 2)
+    key = linear_fp8(x, w["self_attn.k_proj"]).reshape(rows, tokens, cfg.num_key_value_heads, head)
+    key = rms_norm(key, w["self_attn.k_norm_weight"], cfg.rms_norm_eps).transpose(1, 2)
+    value = linear_fp8(x, w["self_attn.v_proj"]).reshape(rows, tokens, cfg.num_key_value_heads, head).transpose(1, 2)
+    query, key = apply_rotary(query, key, cos, sin)
+    return query, key, value, gate.reshape(rows, tokens, cfg.num_attention_heads * head)
+
+
+def _write_both(st: dict, key, value, positions):
+    """`FullAttentionStep._write_both` (model.py:603-608) for a bf16 cache."""
+    rows, kv_heads, n, head = key.shape
+    at = positions.reshape(rows, 1, n, 1).expand(-1, kv_heads, -1, head)
+    st["k_cache"] = st["k_cache"].scatter(2, at, key)
+    st["v_cache"] = st["v_cache"].scatter(2, at, value)
+
+
+def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active):
+    """`FullAttentionStep.verify` bf16-cache branch (model.py:641-672), tp 1. ``st`` holds ``k_cache``/``v_cache``
+    ``[B, Hkv, S, hd]``, replaced by the written caches."""
+    head = cfg.head_dim
+    batch, tokens = x.shape[:2]
+    max_seq_len = st["k_cache"].shape[2]
+    query, key, value, gate = _attention_project(cfg, w, x, cos, sin)
+    groups = cfg.num_key_value_groups
+    steps = torch.arange(tokens)
+    where = torch.where(active.unsqueeze(-1) > 0.5, position.long().unsqueeze(-1) + steps, max_seq_len - tokens + steps)
+    grouped = query.reshape(batch, cfg.num_key_value_heads, groups, tokens, head)
+    keys = st["k_cache"].unsqueeze(2)
+    values = st["v_cache"].unsqueeze(2)
+    earlier = torch.arange(max_seq_len) < position.unsqueeze(-1)
+    cached = torch.matmul(grouped, keys.transpose(-1, -2)).float() + torch.where(earlier, 0.0, MASKED_SCORE).reshape(batch, 1, 1, 1, -1)
+    own_key = key.unsqueeze(2)
+    own_value = value.unsqueeze(2)
+    causal = steps.unsqueeze(0) <= steps.unsqueeze(-1)
+    own = torch.matmul(grouped, own_key.transpose(-1, -2)).float() + torch.where(causal, 0.0, MASKED_SCORE)
+    weights = torch.softmax(torch.cat((cached, own), dim=-1) * head**-0.5, dim=-1).to(x.dtype)
+    out = torch.matmul(weights[..., :max_seq_len], values) + torch.matmul(weights[..., max_seq_len:], own_value)
+    out = out.permute(0, 3, 1, 2, 4).reshape(batch, tokens, cfg.num_attention_heads * head)
+    _write_both(st, key, value, where)
+    return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
+
+
+def attention_decode(cfg, w: dict, st: dict, x, cos, sin, position, active):
+    """`FullAttentionStep.forward` bf16-cache branch (model.py:610-639): one token per row."""
+    head = cfg.head_dim
+    batch = x.shape[0]
+    max_seq_len = st["k_cache"].shape[2]
+    query, key, value, gate = _attention_project(cfg, w, x, cos, sin)
+    grouped = query.reshape(batch, cfg.num_key_value_heads, cfg.num_key_value_groups, head)
+    where = torch.where(active > 0.5, position.long(), max_seq_len - 1).unsqueeze(-1)
+    keys, values = st["k_cache"], st["v_cache"]
+    earlier = torch.arange(max_seq_len) < position.unsqueeze(-1)
+    cached = torch.matmul(grouped, keys.transpose(2, 3)).float() + torch.where(earlier, 0.0, MASKED_SCORE).reshape(batch, 1, 1, -1)
+    own = torch.matmul(grouped, key.transpose(2, 3)).float()
+    weights = torch.softmax(torch.cat((cached, own), dim=-1) * head**-0.5, dim=-1).to(x.dtype)
+    out = torch.matmul(weights[..., :-1], values) + weights[..., -1:] * value
+    out = out.reshape(batch, 1, cfg.num_attention_heads * head)
+    _write_both(st, key, value, where)
+    return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
+
+
+# ----------------------------------------------------------------------------------------------- layers and step
+
+
+def decoder_layer(cfg, layer_type: str, w: dict, st: dict, x, cos, sin, position, active, accepted=None):
+    """`DecoderLayer.forward` (model.py:918-930): verify when ``accepted`` is given, else decode."""
+    eps = cfg.rms_norm_eps
+    h = rms_norm(x, w["input_layernorm_weight"], eps)
+    if layer_type == "linear_attention":
+        if accepted is not None:
+            mixer = gdn_verify(cfg, w, st, h, position, active, accepted)
+        else:
+            mixer = gdn_decode(cfg, w, st, h, position, active)
+    else:
+        if accepted is not None:
+            mixer = attention_verify(cfg, w, st, h, cos, sin, position, active)
+        else:
+            mixer = attention_decode(cfg, w, st, h, cos, sin, position, active)
+    x = x + mixer
+    return x + mlp(w, rms_norm(x, w["post_attention_layernorm_weight"], eps))
+
+
+def step_verify(cfg, layers: list, states: list, inputs_embeds, cos, sin, position, active, accepted):
+    """`Qwen38Step.forward` with ``accepted`` (model.py:983-995): all layers, hidden before the final norm."""
+    x = inputs_embeds
+    for layer_type, w, st in zip(cfg.layer_types, layers, states):
+        x = decoder_layer(cfg, layer_type, w, st, x, cos, sin, position, active, accepted)
+    return x
+
+
+def step_decode(cfg, layers: list, states: list, inputs_embeds, cos, sin, position, active):
+    """`Qwen38Step.forward` decode form (model.py:983-995)."""
+    x = inputs_embeds
+    for layer_type, w, st in zip(cfg.layer_types, layers, states):
+        x = decoder_layer(cfg, layer_type, w, st, x, cos, sin, position, active)
+    return x
+
+
+def mtp_forward(cfg, w: dict, st: dict, hidden, inputs_embeds, cos, sin, position, active):
+    """`MTPStep.forward` step form (model.py:843-860), tp 1. ``w`` uses the MTP names (``fc``,
+    ``embedding_norm_weight``, ``hidden_norm_weight``, ``norm_weight``, ``final_norm_weight`` and ``layer.*``)."""
+    eps = cfg.rms_norm_eps
+    embedded = rms_norm(inputs_embeds, w["embedding_norm_weight"], eps)
+    state = rms_norm(rms_norm(hidden, w["final_norm_weight"], eps), w["hidden_norm_weight"], eps)
+    joined = torch.cat((embedded, state), dim=-1)
+    x = linear_fp8(joined, w["fc"])
+    layer_w = {name[len("layer.") :]: t for name, t in w.items() if name.startswith("layer.")}
+    x = decoder_layer(cfg, "full_attention", layer_w, st, x, cos, sin, position, active, accepted=active)
+    out = rms_norm(x, w["norm_weight"], eps)
+    return (out.float() / (1.0 + w["final_norm_weight"].float())).to(x.dtype)
+
+
+# ----------------------------------------------------------------------------------------------- head and acceptance
+
+
+def head_group_maxima(cfg, norm_weight, lm_head: FP8Weight, hidden, group_rows: int = 32):
+    """`HeadStep.forward` CPU branch (model.py:890-895), tp 1: final norm in hidden's dtype, float32 logits, the
+    largest in each group of ``group_rows`` tokens. ``hidden`` ``[R, 1, H]`` -> ``[R, V / group_rows]``."""
+    x = rms_norm(hidden, norm_weight, cfg.rms_norm_eps).reshape(hidden.shape[0], -1)
+    logits = x.float() @ lm_head.dense_t()
+    return torch.stack([g.amax(dim=-1) for g in logits.split(group_rows, dim=-1)], dim=-1)
+
+
+def chip_next_tokens(cfg, norm_weight, lm_head: FP8Weight, hidden, maxima, recheck_groups: int = 4, group_rows: int = 32):
+    """`ChipHead.next_tokens` after the graph (generate.py:194-208): the best ``recheck_groups`` groups by maxima,
+    exact float32 logits inside them from float32-normed hidden, the first strictly larger in top-k order wins."""
+    rows = hidden.shape[0]
+    maxima = maxima[:rows].float()
+    best_groups = maxima.topk(min(recheck_groups, maxima.shape[-1]), dim=-1).indices.tolist()
+    norm = rms_norm(hidden.float(), norm_weight, cfg.rms_norm_eps).squeeze(1)
+    dense = lm_head.dense().contiguous().to(torch.bfloat16)
+    tokens = []
+    for row, groups in enumerate(best_groups):
+        best_token, best_logit = -1, -torch.inf
+        for group in groups:
+            first = group * group_rows
+            logit, index = (dense[first : first + group_rows].float() @ norm[row]).max(dim=0)
+            if logit > best_logit:
+                best_token, best_logit = first + int(index), logit
+        if best_token < 0:
+            raise FloatingPointError(f"row {row}'s logits are not finite, so the graph produced NaN or infinity")
+        tokens.append(best_token)
+    return tokens
+
+
+def host_next_tokens(cfg, norm_weight, lm_head: FP8Weight, hidden):
+    """`HostHead.next_tokens` (generate.py:156-159): argmax over the whole vocabulary in float32."""
+    norm = rms_norm(hidden.float(), norm_weight, cfg.rms_norm_eps).squeeze(1)
+    return torch.argmax(norm @ lm_head.dense_t(), dim=-1).tolist()
+
+
+def accept(picks: list, drafts: list, k: int):
+    """Greedy longest-prefix acceptance (scheduler.py:291-298): leading drafts equal to the model's picks are kept,
+    then the model's own next pick. Returns (match, emitted)."""
+    match = 0
+    while match < k - 1 and drafts[match] == picks[match]:
+        match += 1
+    return match, picks[: match + 1]
+
+
+def top2_gap(cfg, norm_weight, lm_head: FP8Weight, hidden) -> torch.Tensor:
+    """Per row, the gap between the two largest float32 logits: rows under 1e-3 are near-ties, where a pick may
+    legitimately differ between two correct implementations."""
+    norm = rms_norm(hidden.float(), norm_weight, cfg.rms_norm_eps).squeeze(1)
+    top = (norm @ lm_head.dense_t()).topk(2, dim=-1).values
+    return top[:, 0] - top[:, 1]

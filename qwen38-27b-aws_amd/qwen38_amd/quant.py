@@ -1,0 +1,56 @@
+"""FP8 weight format of this build: e4m3 bytes with one E8M0 power-of-two scale per 32 input elements.
+
+The reference stores FP8 e5m2 weights ``[in, out]`` with the FP4 checkpoint's scale folded in
+(qwen38_inf2/fp4.py:118-140, checkpoint.py:177-182). BASELINE's weights are FP8 e4m3 with per-32 power-of-two
+scales, which gfx950's scaled MFMA (`v_mfma_scale_f32_*_f8f6f4`) applies in hardware. Canonical host layout here is
+``[out, in]`` (row per output column, like a torch Linear weight): ``weight_fp8`` uint8 ``[N, K]`` and
+``scale_e8m0`` uint8 ``[N, K/32]``. A dequantized weight ``e4m3 * 2**(scale-127)`` is exact in bf16.
+
+Activations are rounded to FP8 e5m2 at every projection input, as the reference does (model.py:85-87, 222-225).
+
+These are torch ops and run on whichever device the tensor is on; the results are bit-identical on CPU and GPU
+because every step is exact or a correctly rounded cast.
+"""
+
+from __future__ import annotations
+
+import torch
+
+GROUP = 32
+E8M0_BIAS = 127
+E4M3_MAX = 448.0
+
+
+def quantize_e4m3(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize a float ``[N, K]`` matrix to (e4m3 bytes ``[N, K]``, E8M0 bytes ``[N, K/32]``).
+
+    OCP MX recipe: a group's scale is ``2**(floor(log2(amax)) - 8)``, 8 being e4m3's largest exponent, so the group's
+    largest element lands in [256, 512) and saturates at 448.
+    """
+    n, k = weight.shape
+    if k % GROUP:
+        raise ValueError(f"K={k} is not a multiple of {GROUP}")
+    groups = weight.float().reshape(n, k // GROUP, GROUP)
+    amax = groups.abs().amax(dim=-1)
+    _, exponent = torch.frexp(amax)  # amax = m * 2**exponent with m in [0.5, 1), so floor(log2(amax)) = exponent - 1
+    scale_exp = torch.where(amax > 0, exponent - 1 - 8, torch.zeros_like(exponent)).clamp(-126, 126)
+    scaled = groups * pow2(-scale_exp).unsqueeze(-1)
+    coded = scaled.clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+    return coded.reshape(n, k), (scale_exp + E8M0_BIAS).to(torch.uint8)
+
+
+def pow2(exponent: torch.Tensor) -> torch.Tensor:
+    """Exactly ``2**exponent`` as float32 for integer exponents in [-126, 127], built from the bit fields."""
+    return ((exponent.to(torch.int32) + 127) << 23).view(torch.float32)
+
+
+def dequantize_e4m3(coded: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """float32 ``[N, K]`` from e4m3 bytes and E8M0 scale bytes."""
+    n, k = coded.shape
+    values = coded.view(torch.float8_e4m3fn).float().reshape(n, k // GROUP, GROUP)
+    return (values * pow2(scales.to(torch.int32) - E8M0_BIAS).unsqueeze(-1)).reshape(n, k)
+
+
+def round_e5m2(x: torch.Tensor) -> torch.Tensor:
+    """Round to FP8 e5m2 and back, as `model.fp8_round` does (model.py:85-87)."""
+    return x.to(torch.float8_e5m2).to(x.dtype)

@@ -1,0 +1,292 @@
+"""Pin the CPU oracle: against golden vectors from the reference's own CPU path, and against invariants and closed
+forms that a plausible mistake (a dropped term, a wrong index or sign, a transposed operand) breaks."""
+
+from __future__ import annotations
+
+import hashlib
+import math
+
+import pytest
+import torch
+
+from oracle import model as om
+from qwen38_amd import synth
+from qwen38_amd.config import tiny_config, with_layers
+from qwen38_amd.generate import mtp_step_inputs, verify_inputs, batch_step_inputs
+from qwen38_amd.quant import dequantize_e4m3, quantize_e4m3
+from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states
+
+
+def _digest(t):
+    return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = tiny_config(1)
+    meta = golden_meta()
+    values = dict((s.name, v) for s, v in synth.make_all(synth.model_specs(cfg), meta["seed"]))
+    return cfg, meta, values
+
+
+def test_synthetic_weights_are_the_ones_the_golden_vectors_were_made_with(tiny):
+    cfg, meta, values = tiny
+    for name, v in values.items():
+        t = v if isinstance(v, torch.Tensor) else torch.cat([v[0].flatten(), v[1].flatten()])
+        assert _digest(t) == meta["weights_sha256"][name], name
+
+
+def test_oracle_verify_head_and_mtp_match_the_reference_bit_for_bit(tiny):
+    cfg, meta, values = tiny
+    gold = golden_tensors()
+    layers, mtp_w, head_w = oracle_weights(values, cfg)
+    states = tiny_states(cfg, meta, meta["seed"])
+    b, k, s = meta["batch"], meta["tokens"], meta["max_seq_len"]
+    embed = values["embed_tokens"]
+    ids = gold["ids"].long()
+    active = torch.tensor(meta["active"]).float()
+
+    in1 = verify_inputs(cfg, meta["positions_1"], k, s, torch.bfloat16, meta["active"], [0] * b)
+    assert torch.equal(in1["cos"], gold["cos1"]) and torch.equal(in1["sin"], gold["sin1"])
+    h1 = om.step_verify(cfg, layers, states, embed[ids[0]], in1["cos"], in1["sin"], in1["position"], in1["active"], in1["accepted"])
+    assert torch.equal(h1, gold["hidden1"])
+    in2 = verify_inputs(cfg, meta["positions_2"], k, s, torch.bfloat16, meta["active"], meta["accepted_2"])
+    h2 = om.step_verify(cfg, layers, states, embed[ids[1]], in2["cos"], in2["sin"], in2["position"], in2["active"], in2["accepted"])
+    assert torch.equal(h2, gold["hidden2"])
+    for i, (kind, st) in enumerate(zip(cfg.layer_types, states)):
+        owner = "linear_attn" if kind == "linear_attention" else "self_attn"
+        for key, value in st.items():
+            assert _digest(value) == meta["state_sha256"][f"layers.{i}.{owner}.{key}"], (i, key)
+
+    rows = h2.reshape(b * k, 1, -1)
+    maxima = om.head_group_maxima(cfg, head_w["norm_weight"], head_w["lm_head"], rows)
+    assert torch.equal(maxima, gold["maxima"])
+    assert om.chip_next_tokens(cfg, head_w["norm_weight"], head_w["lm_head"], rows, maxima) == gold["picks4"].tolist()
+    assert om.chip_next_tokens(cfg, head_w["norm_weight"], head_w["lm_head"], rows, maxima, 1) == gold["picks1"].tolist()
+
+    mst = synth.kv_states(cfg, b, s, meta["context"], meta["seed"], "mtp")
+    picks = gold["picks4"].long().reshape(b, k)
+    mi = mtp_step_inputs(cfg, meta["positions_2"], k, s, torch.bfloat16, meta["active"])
+    out = om.mtp_forward(cfg, mtp_w, mst, h2, embed[picks], mi["cos"], mi["sin"], mi["position"], mi["active"])
+    assert torch.equal(out, gold["mtp_out"])
+    for key, value in mst.items():
+        assert _digest(value) == meta["mtp_state_sha256"][f"layer.self_attn.{key}"], key
+
+
+# ------------------------------------------------------------------------------------------- invariants
+
+
+def _float32_tiny(num_layers_types, seed=3):
+    cfg = with_layers(tiny_config(1), num_layers_types)
+    values = dict((s.name, v) for s, v in synth.make_all(synth.model_specs(cfg, mtp=False, head=False), seed))
+    layers, _, _ = oracle_weights(values, cfg)
+    for w in layers:
+        for key, v in list(w.items()):
+            if isinstance(v, torch.Tensor):
+                w[key] = v.float()
+    return cfg, layers
+
+
+@pytest.mark.parametrize("kind", ["linear_attention", "full_attention"])
+def test_verify_steps_equal_decoding_the_accepted_tokens_one_by_one(monkeypatch, kind):
+    """Reference tests/test_prefill.py:235-263, on one layer of each kind in float32: after steps that commit
+    2, 4, 1, 3, 1 of the last step's tokens, every accepted position's output equals one-token decode."""
+    monkeypatch.setattr(om, "ROUND_E5M2", False)
+    cfg, layers = _float32_tiny((kind,))
+    k, batch, s = 4, 2, 64
+    g = torch.Generator().manual_seed(5)
+    tokens = torch.randn(16, cfg.hidden_size, generator=g)
+
+    def fresh():
+        if kind == "linear_attention":
+            st = synth.gdn_states(cfg, batch, k, 7, "x")
+            return [{key: v.float() if key != "pending_input_state" and key != "conv_state" else v.float() for key, v in st.items()}]
+        st = synth.kv_states(cfg, batch, s, [20, 0], 7, "x")
+        return [{key: v.float() for key, v in st.items()}]
+
+    plain = fresh()
+    start = 20
+    want = []
+    for i in range(14):
+        inputs = batch_step_inputs(cfg, [start + i, 0], s, torch.float32, [True, False])
+        x = torch.stack([tokens[i], torch.zeros(cfg.hidden_size)]).reshape(2, 1, -1)
+        want.append(om.step_decode(cfg, layers, plain, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"])[0, 0])
+
+    spec = fresh()
+    done, accepted = 0, 0
+    for take in [2, 4, 1, 3, 1]:
+        x = torch.zeros(2, k, cfg.hidden_size)
+        x[0, :take] = tokens[done : done + take]
+        x[0, take:] = tokens[15]
+        inputs = verify_inputs(cfg, [start + done, 0], k, s, torch.float32, [True, False], [accepted, 0])
+        out = om.step_verify(cfg, layers, spec, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"], inputs["accepted"])
+        for j in range(take):
+            assert torch.allclose(out[0, j], want[done + j], atol=1e-4, rtol=1e-4), (done, j, (out[0, j] - want[done + j]).abs().max())
+        done, accepted = done + take, take
+
+
+def test_gated_delta_verify_equals_the_textbook_recurrence_in_float64():
+    """Reference tests/test_prefill.py:18-26's recurrence: S_t = e^{g_t} S_{t-1} + k_t d_t^T,
+    d_t = b_t (v_t - S_{t-1}^T k_t e^{g_t}), o_t = S_t^T q_t, checked against the verify form's commit (pending
+    snapshots from a previous step, any accepted count) and its in-step K x K solve."""
+    torch.manual_seed(0)
+    pairs, k, d = 3, 4, 16
+    q = torch.nn.functional.normalize(torch.randn(pairs, 2 * k, d, dtype=torch.float64), dim=-1) / d**0.5
+    key = torch.nn.functional.normalize(torch.randn(pairs, 2 * k, d, dtype=torch.float64), dim=-1)
+    v = torch.randn(pairs, 2 * k, d, dtype=torch.float64)
+    g = -torch.rand(pairs, 2 * k, dtype=torch.float64)
+    beta = torch.rand(pairs, 2 * k, dtype=torch.float64)
+    s0 = torch.randn(pairs, d, d, dtype=torch.float64)
+
+    def textbook(state, first, n):
+        outs, deltas = [], []
+        for t in range(first, first + n):
+            state_dec = state * g[:, t].exp().reshape(-1, 1, 1)
+            delta = beta[:, t].unsqueeze(-1) * (v[:, t] - (state_dec * key[:, t].unsqueeze(-1)).sum(-2))
+            state = state_dec + key[:, t].unsqueeze(-1) * delta.unsqueeze(-2)
+            outs.append((state * q[:, t].unsqueeze(-1)).sum(-2))
+            deltas.append(delta)
+        if not outs:
+            return state, None, None
+        return state, torch.stack(outs, 1), torch.stack(deltas, 1)
+
+    for accepted in range(k + 1):
+        # Step A runs tokens 0..k-1 from s0; its snapshots are (key, delta, g). Step B commits `accepted` of them
+        # and runs tokens `accepted`..`accepted+k-1` (the rejected ones re-sent).
+        _, _, deltas_a = textbook(s0, 0, k)
+        taken = [float(accepted > s) for s in range(k)]
+        decays = [g[:, s] * taken[s] for s in range(k)]
+        remaining = sum(decays)
+        scale = remaining.exp()
+        weighted = []
+        for s in range(k):
+            remaining = remaining - decays[s]
+            weighted.append(key[:, s] * (remaining.exp() * taken[s]).unsqueeze(-1))
+        committed, products = om.commit_and_read(
+            s0.float(), scale.reshape(pairs, 1, 1).float(), torch.stack(weighted, 1).float(), deltas_a.float(),
+            torch.cat((key[:, accepted : accepted + k], q[:, accepted : accepted + k]), 1).transpose(1, 2).float(),
+        )
+        committed, products = committed.double(), products.double()
+        want_state, want_out, _ = textbook(s0, 0, accepted)
+        assert torch.allclose(committed, want_state, atol=1e-5)
+        # In-step solve of step B, written as gdn_verify runs it.
+        gb, bb = g[:, accepted : accepted + k], beta[:, accepted : accepted + k]
+        kb, qb, vb = key[:, accepted : accepted + k], q[:, accepted : accepted + k], v[:, accepted : accepted + k]
+        key_state, query_state = products[:, :k], products[:, k:]
+        cum = gb.cumsum(-1)
+        ds, outs = [], []
+        for t in range(k):
+            delta = vb[:, t] - cum[:, t].exp().unsqueeze(-1) * key_state[:, t]
+            for s in range(t):
+                delta = delta - ((cum[:, t] - cum[:, s]).exp() * (kb[:, t] * kb[:, s]).sum(-1)).unsqueeze(-1) * ds[s]
+            ds.append(delta * bb[:, t].unsqueeze(-1))
+            out = cum[:, t].exp().unsqueeze(-1) * query_state[:, t]
+            for s in range(t + 1):
+                out = out + ((cum[:, t] - cum[:, s]).exp() * (qb[:, t] * kb[:, s]).sum(-1)).unsqueeze(-1) * ds[s]
+            outs.append(out)
+        _, want_b, want_db = textbook(want_state, accepted, k)
+        assert torch.allclose(torch.stack(outs, 1), want_b, atol=1e-5)
+        assert torch.allclose(torch.stack(ds, 1), want_db, atol=1e-5)
+
+
+def test_verify_attention_equals_full_softmax_over_the_visible_keys(monkeypatch):
+    """Each verify token attends to cached positions before `position` and to its own step's tokens up to itself:
+    brute force in float64 over exactly those keys."""
+    monkeypatch.setattr(om, "ROUND_E5M2", False)
+    cfg, layers = _float32_tiny(("full_attention",))
+    w = layers[0]
+    k, batch, s = 4, 3, 48
+    positions = [10, 0, 30]
+    st = {key: v.float() for key, v in synth.kv_states(cfg, batch, s, [10, 0, 30], 9, "y").items()}
+    cache_k, cache_v = st["k_cache"].clone(), st["v_cache"].clone()
+    x = torch.randn(batch, k, cfg.hidden_size, generator=torch.Generator().manual_seed(2))
+    inputs = verify_inputs(cfg, positions, k, s, torch.float32, [True] * batch, [0] * batch)
+    query, key, value, gate = om._attention_project(cfg, w, x, inputs["cos"], inputs["sin"])
+    got_o = om.attention_verify(cfg, w, st, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"])
+    groups = cfg.num_key_value_groups
+    out = torch.zeros(batch, k, cfg.num_attention_heads, cfg.head_dim, dtype=torch.float64)
+    for b in range(batch):
+        for h in range(cfg.num_attention_heads):
+            kv = h // groups
+            for t in range(k):
+                keys = torch.cat((cache_k[b, kv, : positions[b]], key[b, kv, : t + 1])).double()
+                vals = torch.cat((cache_v[b, kv, : positions[b]], value[b, kv, : t + 1])).double()
+                p = torch.softmax(keys @ query[b, h, t].double() / math.sqrt(cfg.head_dim), 0)
+                out[b, t, h] = p @ vals
+    want = om.linear_fp8((out.reshape(batch, k, -1).float() * torch.sigmoid(gate)), w["self_attn.o_proj"])
+    assert torch.allclose(got_o, want, atol=1e-4, rtol=1e-4)
+    # Writes land at position..position+K-1 and nowhere else.
+    for b in range(batch):
+        assert torch.equal(st["k_cache"][b, :, positions[b] : positions[b] + k], key[b])
+        assert torch.equal(st["k_cache"][b, :, : positions[b]], cache_k[b, :, : positions[b]])
+
+
+def test_chip_head_picks_what_the_host_head_picks():
+    """Reference tests/test_model_parity.py:280-309: group maxima plus the exact recheck pick the full argmax."""
+    cfg = tiny_config(1)
+    specs = [sp for sp in synth.head_specs(cfg) if sp.name != "embed_tokens"]
+    values = dict((sp.name, v) for sp, v in synth.make_all(specs, 11))
+    _, _, head = oracle_weights(values, cfg)
+    hidden = torch.randn(24, 1, cfg.hidden_size, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    maxima = om.head_group_maxima(cfg, head["norm_weight"], head["lm_head"], hidden)
+    got = om.chip_next_tokens(cfg, head["norm_weight"], head["lm_head"], hidden, maxima)
+    want = om.host_next_tokens(cfg, head["norm_weight"], head["lm_head"], hidden)
+    gaps = om.top2_gap(cfg, head["norm_weight"], head["lm_head"], hidden)
+    assert all(g == w or gap < 1e-3 for g, w, gap in zip(got, want, gaps.tolist()))
+    # Group maxima are the largest logits of their groups: their argmax group holds the argmax token (ties aside).
+    assert sum(int(maxima[r].argmax()) == want[r] // 32 for r in range(24)) >= 22
+
+
+def test_acceptance_is_the_longest_matching_draft_prefix():
+    assert om.accept([5, 6, 7, 8], [5, 6, 9], 4) == (2, [5, 6, 7])
+    assert om.accept([5, 6, 7, 8], [5, 6, 7], 4) == (3, [5, 6, 7, 8])
+    assert om.accept([5, 6, 7, 8], [1, 6, 7], 4) == (0, [5])
+    assert om.accept([5], [], 1) == (0, [5])
+
+
+# ------------------------------------------------------------------------------------------- formats
+
+
+def test_e4m3_bit_field_decode_equals_torchs_cast_for_every_byte():
+    codes = torch.arange(256, dtype=torch.uint8)
+    want = codes.view(torch.float8_e4m3fn).float()
+    got = om.e4m3_to_float(codes)
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    assert torch.equal(got[~torch.isnan(got)], want[~torch.isnan(want)])
+
+
+def test_quantizer_keeps_groups_in_range_and_dequantizes_exactly_in_bf16():
+    w = torch.randn(64, 512, generator=torch.Generator().manual_seed(0)) * 0.02
+    w[3, :32] = 0.0
+    w[5, 64:96] *= 1e3
+    coded, scales = quantize_e4m3(w)
+    d = dequantize_e4m3(coded, scales)
+    assert torch.equal(d, om.FP8Weight(coded, scales).dense())
+    assert torch.equal(d.to(torch.bfloat16).float(), d)
+    groups = (d.reshape(64, 16, 32).abs().amax(-1) / torch.pow(2.0, scales.float() - 127))
+    nonzero = groups > 0
+    assert (groups[nonzero] >= 256).all() and (groups[nonzero] <= 448).all()
+    # Rounding error per element is at most half an e4m3 step (2**-4 relative for normals) or saturation.
+    rel = ((d - w).abs() / w.abs().clamp_min(1e-30))[w.abs() > 1e-3]
+    assert rel.max() <= 0.0625 + 1e-6 or ((d - w).abs().max() <= 64 * torch.pow(2.0, scales.float().max() - 127))
+
+
+def test_e5m2_rounding_of_every_bf16_value_is_round_to_nearest_even():
+    """The activation rounding the kernels must reproduce: e5m2 is bf16's sign and exponent range with 2 mantissa
+    bits, so rounding a bf16 to it is round-half-even on the low 5 mantissa bits, with overflow to infinity only past
+    the largest finite e5m2 (57344) after rounding, and subnormals below 2**-14."""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    got = bits.to(torch.float8_e5m2).float()
+    x = bits.double()
+    finite = torch.isfinite(x)
+    mag = x.abs()
+    exponent = torch.floor(torch.log2(mag.clamp_min(2.0**-40))).clamp(min=-14)
+    step = torch.pow(2.0, exponent - 2)
+    q = mag / step
+    r = torch.floor(q)
+    frac = q - r
+    up = (frac > 0.5) | ((frac == 0.5) & (torch.remainder(r, 2) == 1))
+    want = torch.where(up, r + 1, r) * step * torch.sign(x)
+    want = torch.where(want.abs() > 57344, torch.sign(x) * math.inf, want)
+    sel = finite & (mag < 2.0**17)
+    assert torch.equal(got[sel].double(), want[sel])
