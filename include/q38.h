@@ -1,0 +1,125 @@
+/* C ABI of the MI355X verify-step library (libq38.so), built from qwen38-27b-aws_amd/qwen38_amd/csrc.
+ *
+ * It replaces, for the MTP speculative-decoding verify step of the Qwen3.8 hybrid model, the reference's compiled
+ * Neuron graphs and the CPU path that stands in for them:
+ *   q38_verify       <- `verify(**verify_inputs(...))`, the K-token graph: Qwen38Step.forward with `accepted`
+ *                       (reference qwen38_inf2/model.py:933-995; call site scheduler.py:288; inputs generate.py:72-87)
+ *   q38_mtp_step     <- `mtp(hidden=..., inputs_embeds=..., **mtp_step_inputs(...))`, MTPStep.forward
+ *                       (model.py:843-860; call sites scheduler.py:179,192)
+ *   q38_head_groupmax<- the head graph `run_graph(hidden=...)`, HeadStep.forward (model.py:890-900;
+ *                       generate.py:195)
+ *   q38_head_pick    <- ChipHead.next_tokens' top-group recheck (generate.py:196-208), on the GPU
+ *   q38_accept       <- the greedy acceptance loop (scheduler.py:291-300), for the on-device step
+ *   q38_embed        <- ChipHead.embed_batch (generate.py:183-184)
+ *
+ * Conventions. Every function returns 0 on success or a nonzero code; q38_last_error() then describes the failure
+ * (thread-local). All tensor arguments are device pointers; `stream` is a hipStream_t (0 for the null stream). The
+ * library allocates no device memory: the caller binds every weight, state and workspace buffer with q38_bind, after
+ * asking q38_buffer_size for its size. A handle is not re-entrant: one call at a time per handle; different handles
+ * are independent. bf16 is passed as uint16_t bits.
+ */
+#ifndef Q38_H
+#define Q38_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct q38_handle q38_handle;
+
+#define Q38_MAX_LAYERS 128
+#define Q38_LINEAR 0
+#define Q38_FULL 1
+
+/* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
+ * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
+ * max_seq_len, mtp_tokens; neuron.py:128-140,182-185). */
+typedef struct q38_config {
+    int hidden_size, intermediate_size, vocab_size;
+    int num_layers;
+    int layer_types[Q38_MAX_LAYERS]; /* Q38_LINEAR (gated delta) or Q38_FULL (attention) */
+    int num_attention_heads, num_key_value_heads, head_dim, rotary_dim;
+    int linear_num_key_heads, linear_num_value_heads, linear_key_head_dim, linear_value_head_dim;
+    int linear_conv_kernel_dim;
+    float rms_norm_eps;
+    int batch_size, verify_tokens, max_seq_len, mtp;
+} q38_config;
+
+const char* q38_last_error(void);
+
+/* Validates the shapes the kernels support and creates a handle with nothing bound. */
+int q38_create(const q38_config* cfg, q38_handle** out);
+void q38_destroy(q38_handle* h);
+
+/* Buffers, by name and layer (layer -1 for model-wide buffers; layer num_layers is the MTP layer). Sizes in bytes.
+ * Weights (FP8 projections bound as packed tiles + scale words from q38_pack_weight):
+ *   per layer: input_layernorm, post_attention_layernorm (bf16 [H]), mlp.gate_up.{tiles,scales} (gate and up rows
+ *     interleaved by 32), mlp.down.{tiles,scales}
+ *   gated-delta layers: linear_attn.in_proj_qkvz.{tiles,scales} (in_proj_qkv rows then in_proj_z rows),
+ *     linear_attn.out_proj.{tiles,scales}, linear_attn.in_proj_a, linear_attn.in_proj_b (bf16 [Hv][H]),
+ *     linear_attn.conv_weight (bf16 [C][4]), linear_attn.A_log, linear_attn.dt_bias (bf16 [Hv]),
+ *     linear_attn.norm_weight (bf16 [128])
+ *   attention layers and the MTP layer: self_attn.qkv.{tiles,scales} (q_proj, k_proj, v_proj rows),
+ *     self_attn.o_proj.{tiles,scales}, self_attn.q_norm, self_attn.k_norm (bf16 [head_dim])
+ *   MTP layer only: mtp.fc.{tiles,scales}, mtp.embedding_norm, mtp.hidden_norm, mtp.norm (bf16 [H])
+ *   model-wide: head.norm (bf16 [H], also the MTP's final norm), head.lm_head.{tiles,scales}, embed_tokens (bf16 [V][H])
+ * State (per layer):
+ *   linear_attn.recurrent_state bf16 [B][Hv][128][128]
+ *   linear_attn.conv_state bf16 [2][B][C][3], linear_attn.pending_key f32 [2][B][K][Hk][128],
+ *   linear_attn.pending_delta f32 [2][B][K][Hv][128], linear_attn.pending_decay f32 [2][B][K][Hv],
+ *   linear_attn.pending_input bf16 [2][B][K][C]: two halves, the current one given by q38_parity
+ *   self_attn.k_cache bf16 [B][Hkv][S][hd]; self_attn.v_cache bf16 [B][Hkv][S/32][hd][32] (transposed per 32 positions)
+ * Scratch: workspace (model-wide). */
+int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
+int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
+
+/* Which half of the double-buffered gated-delta state is current (read by the next q38_verify), and setting it. */
+int q38_parity(q38_handle* h, int* parity);
+int q38_set_parity(q38_handle* h, int parity);
+
+/* Pack an FP8 projection: e4m3 bytes [N][K] and E8M0 scale bytes [N][K/32] (row-major, a torch Linear weight's
+ * layout) into tiles [N/32][K/64][64][32] and scale words [N/32][K/256][64]. N % 32 == 0, K % 256 == 0. */
+int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint32_t* scale_words,
+                    void* stream);
+
+/* A standalone FP8 projection, `FP8Linear.forward` (reference model.py:211-229): x bf16 [rows][k] rounded to e5m2,
+ * times the packed weight ([n][k] e4m3 + E8M0), float32 sums, bf16 out [rows][n]. act_scratch holds
+ * q38_fp8_linear_scratch(rows, k) bytes. n % 256 == 0, k % 256 == 0. */
+int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
+                   uint8_t* act_scratch, uint16_t* out, void* stream);
+size_t q38_fp8_linear_scratch(int rows, int k);
+/* The same with float32 output [rows][n] (no bf16 rounding); rows in {32, 64, 128} or a multiple of 256. */
+int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
+                       uint8_t* act_scratch, float* out, void* stream);
+
+/* One verify step over all B rows: embeds bf16 [B][K][H]; cos, sin bf16 [B][K][rotary_dim]; position int32 [B];
+ * active f32 [B]; accepted int32 [B]. Writes the last layer's hidden state bf16 [B][K][H] (before the final norm),
+ * commits each row's `accepted` tokens of the previous step, and flips the parity. */
+int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
+               const float* active, const int32_t* accepted, uint16_t* out_hidden, void* stream);
+
+/* One MTP step: hidden, embeds bf16 [B][K][H]; cos, sin [B][K][rotary_dim]; position, active [B]. Writes bf16
+ * [B][K][H]. */
+int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin,
+                 const int32_t* position, const float* active, uint16_t* out, void* stream);
+
+/* Head: rows bf16 [R][H] (R <= B*K). q38_head_groupmax writes the group maxima f32 [R][V/32]; q38_head_pick computes
+ * them itself and writes ids int32 [R] (-1: no finite logit) after rechecking the best `groups` (1..4) groups. */
+int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* maxima, void* stream);
+int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, int32_t* ids, void* stream);
+
+/* Embedding rows for ids int32 [n] into bf16 [n][H]. */
+int q38_embed(q38_handle* h, const int32_t* ids, int n, uint16_t* out, void* stream);
+
+/* Greedy acceptance: picks int32 [B][K], drafts int32 [B][K-1], active f32 [B] -> match, accepted int32 [B]. */
+int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const float* active, int32_t* match,
+               int32_t* accepted, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

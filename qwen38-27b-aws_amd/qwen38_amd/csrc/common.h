@@ -1,0 +1,91 @@
+// Device helpers shared by every kernel of the verify path (gfx950 / CDNA4).
+//
+// Number formats and rounding follow the reference's CPU path (qwen38_inf2/model.py), which runs torch CPU ops in
+// bf16: every bf16 result is fp32 rounded to nearest even, and activations are rounded to FP8 e5m2 at each
+// projection input (model.py:85-87, 222-225).
+//
+// Activation tiles. Every FP8 (and the head's bf16) GEMM reads its activations in the layout the MFMA operand wants,
+// written that way by the kernel that produced them. One K-step of 64 inputs for 32 tokens is a 2 KiB tile; lane l
+// holds 32 bytes of token l % 32 from lane half h = l / 32, in the order v_mfma_scale_f32_32x32x64_f8f6f4 reads them:
+//     byte i of lane half h  <->  input k = 32 * (i / 16) + 16 * h + i % 16  (within the K-step)
+// (bytes 0-15 of both halves form the step's first 32-input MX block, whose E8M0 scale lane half 0 supplies; bytes
+// 16-31 the second, scaled by lane half 1; measured on gfx950). Weights use the same layout with output features in
+// place of tokens (pack.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+#define Q38_HOST_DEVICE __host__ __device__ __forceinline__
+
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// fp32 -> bf16, round to nearest even (c10::BFloat16's rounding); NaN stays NaN.
+__device__ __forceinline__ bf16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+// Round to bf16 and back: the value a torch bf16 op stores.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// FP8 e5m2 code of x, round to nearest even, overflow past 57344 to infinity (torch's non-saturating cast).
+__device__ __forceinline__ uint32_t f2e5m2(float x) {
+    uint32_t u = __float_as_uint(x);
+    uint32_t s = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return s | 0x7fu;
+    if (a >= 0x38800000u) {  // |x| >= 2^-14: normal e5m2, keep 2 mantissa bits
+        uint32_t r = (a + 0xfffffu + ((a >> 21) & 1u)) & ~0x1fffffu;
+        if (r > 0x47600000u) return s | 0x7cu;
+        return s | ((((r >> 23) - 112u) << 2) | ((r >> 21) & 3u));
+    }
+    // Subnormal e5m2: multiples of 2^-16. 4 units is the smallest normal, whose code is also 4.
+    return s | (uint32_t)__builtin_rintf(__uint_as_float(a) * 65536.0f);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// torch.nn.functional.softplus with beta 1, threshold 20.
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+// Position of input k (0..63) within a K-step: lane half and byte (element for bf16 tiles).
+Q38_HOST_DEVICE int kstep_half(int k) { return (k & 31) >> 4; }
+Q38_HOST_DEVICE int kstep_byte(int k) { return ((k & 63) >> 5) * 16 + (k & 15); }
+
+// Element offset of (t, k) in a tile buffer with K inputs (K a multiple of 64): bytes for e5m2 tiles, bf16 elements
+// for the head's bf16 tiles. Four consecutive k from a multiple of 4 are contiguous.
+Q38_HOST_DEVICE size_t act_offset(int t, int k, int K) {
+    return ((size_t)(t >> 5) * (K >> 6) + (k >> 6)) * 2048 + (size_t)(((t & 31) + kstep_half(k) * 32) * 32) + kstep_byte(k);
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Sum over a 256-thread block; `red` is 4 floats of shared memory. Every thread gets the total.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = warp_sum(v);
+    int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}

@@ -1,0 +1,648 @@
+// Host side of libq38: the C ABI declared in include/q38.h. It validates shapes, keeps the bound buffers of one loaded
+// model and sequences the kernels of a verify step, an MTP step and the head on the caller's stream. It allocates no
+// device memory.
+//
+// Per layer of a verify step (reference DecoderLayer.forward, qwen38_inf2/model.py:918-930):
+//   gated delta:  qkvz GEMM -> gates -> gdn_verify -> out_proj GEMM (split-K) -> residual + post-norm
+//   attention:    qkv GEMM -> attn_verify -> o_proj GEMM (split-K) -> residual + post-norm
+//   MLP:          gate/up GEMM with SwiGLU epilogue -> down GEMM (split-K) -> residual + next layer's input norm
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../../include/q38.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const std::string& msg) {
+    g_error = msg;
+    return 1;
+}
+
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr int SPLIT_MAX = 16;
+
+struct Buf {
+    void* p = nullptr;
+    size_t n = 0;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Token counts padded the way the GEMMs tile them: 32, 64, 128, then multiples of 256.
+int pad_tokens(int t) {
+    if (t <= 32) return 32;
+    if (t <= 64) return 64;
+    if (t <= 128) return 128;
+    return (t + 255) / 256 * 256;
+}
+
+}  // namespace
+
+struct q38_handle {
+    q38_config cfg;
+    int H, I, V, B, K, S, T, Tpad;
+    int Hq, Hkv, hd, Hk, Hv, dk, C;
+    std::vector<std::map<std::string, Buf>> layer;  // num_layers + 1 (the MTP layer)
+    std::map<std::string, Buf> global;
+    int parity = 0;
+    // workspace carve-up
+    size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_beta, off_g, off_part,
+        off_scores, off_weights, off_htiles, off_x32, off_maxima, workspace_bytes;
+    int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
+
+    uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
+};
+
+namespace {
+
+bool is_linear(const q38_handle* h, int layer) { return layer < h->cfg.num_layers && h->cfg.layer_types[layer] == Q38_LINEAR; }
+
+// Expected size of a named buffer, or 0 if the name does not exist for that layer.
+size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
+    const size_t H = h->H, I = h->I, V = h->V, B = h->B, K = h->K, S = h->S;
+    const size_t Hq = h->Hq, Hkv = h->Hkv, hd = h->hd, Hk = h->Hk, Hv = h->Hv, dk = h->dk, C = h->C;
+    auto fp8 = [&](const std::string& base, size_t n, size_t k) -> size_t {
+        if (name == base + ".tiles") return n * k;
+        if (name == base + ".scales") return n * k / 32;
+        return 0;
+    };
+    size_t r;
+    if (layer == -1) {
+        if (name == "head.norm") return H * 2;
+        if ((r = fp8("head.lm_head", V, H))) return r;
+        if (name == "embed_tokens") return V * H * 2;
+        if (name == "workspace") return h->workspace_bytes;
+        return 0;
+    }
+    if (layer < 0 || layer > h->cfg.num_layers) return 0;
+    if (layer == h->cfg.num_layers && !h->cfg.mtp) return 0;
+    if (name == "input_layernorm" || name == "post_attention_layernorm") return H * 2;
+    if ((r = fp8("mlp.gate_up", 2 * I, H))) return r;
+    if ((r = fp8("mlp.down", H, I))) return r;
+    if (is_linear(h, layer)) {
+        if ((r = fp8("linear_attn.in_proj_qkvz", C + Hv * dk, H))) return r;
+        if ((r = fp8("linear_attn.out_proj", H, Hv * dk))) return r;
+        if (name == "linear_attn.in_proj_a" || name == "linear_attn.in_proj_b") return Hv * H * 2;
+        if (name == "linear_attn.conv_weight") return C * 4 * 2;
+        if (name == "linear_attn.A_log" || name == "linear_attn.dt_bias") return Hv * 2;
+        if (name == "linear_attn.norm_weight") return dk * 2;
+        if (name == "linear_attn.recurrent_state") return B * Hv * dk * dk * 2;
+        if (name == "linear_attn.conv_state") return 2 * B * C * 3 * 2;
+        if (name == "linear_attn.pending_key") return 2 * B * K * Hk * dk * 4;
+        if (name == "linear_attn.pending_delta") return 2 * B * K * Hv * dk * 4;
+        if (name == "linear_attn.pending_decay") return 2 * B * K * Hv * 4;
+        if (name == "linear_attn.pending_input") return 2 * B * K * C * 2;
+        return 0;
+    }
+    if ((r = fp8("self_attn.qkv", Hq * hd * 2 + 2 * Hkv * hd, H))) return r;
+    if ((r = fp8("self_attn.o_proj", H, Hq * hd))) return r;
+    if (name == "self_attn.q_norm" || name == "self_attn.k_norm") return hd * 2;
+    if (name == "self_attn.k_cache" || name == "self_attn.v_cache") return B * Hkv * S * hd * 2;
+    if (layer == h->cfg.num_layers) {
+        if ((r = fp8("mtp.fc", H, 2 * H))) return r;
+        if (name == "mtp.embedding_norm" || name == "mtp.hidden_norm" || name == "mtp.norm") return H * 2;
+    }
+    return 0;
+}
+
+// Pointer of a bound buffer; sets the error and returns null when it was never bound.
+template <typename T>
+T* get(q38_handle* h, const std::string& name, int layer, bool* ok) {
+    const auto& m = layer < 0 ? h->global : h->layer[layer];
+    auto it = m.find(name);
+    if (it == m.end() || !it->second.p) {
+        if (*ok) g_error = "buffer '" + name + "' of layer " + std::to_string(layer) + " is not bound";
+        *ok = false;
+        return nullptr;
+    }
+    return (T*)it->second.p;
+}
+
+// Split-K count for an N-column GEMM with partial sums: enough workgroups to fill 256 CUs, K-steps per split even.
+int choose_splits(const q38_handle* h, int N, int K) {
+    const int wg_feat = h->Tpad >= 256 ? 128 : 256;
+    const int tiles = (N / wg_feat) * (h->Tpad >= 256 ? h->Tpad / 256 : 1);
+    const int ks = K / 64;
+    int best = 1;
+    for (int s = 1; s <= SPLIT_MAX; ++s) {
+        if (ks % s || (ks / s) % 2) continue;
+        best = s;
+        if (tiles * s >= 256) break;
+    }
+    return best;
+}
+
+int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint8_t* act, int K, int N, int epi,
+         void* out0, int ld0, int n0, void* out1, int ld1, hipStream_t stream, int* splits_out = nullptr) {
+    if (N % 256 || K % 256) return fail("GEMM shape N=" + std::to_string(N) + " K=" + std::to_string(K) + " not tileable");
+    GemmArgs a{};
+    a.w = tiles;
+    a.ws = scales;
+    a.act = act;
+    a.K = K;
+    a.N = N;
+    a.T = h->T;
+    a.Tpad = h->Tpad;
+    a.unit_scale = 127;
+    a.out0 = out0;
+    a.ld0 = ld0;
+    a.n0 = n0;
+    a.out1 = out1;
+    a.ld1 = ld1;
+    int splits = 1;
+    if (epi == EPI_PARTIAL) {
+        splits = choose_splits(h, N, K);
+        a.part = (float*)h->ws(h->off_part);
+    }
+    a.ksteps = K / 64 / splits;
+    if (a.ksteps % 2) return fail("GEMM K-steps per split must be even");
+    HIP_TRY(q38_gemm_fp8(a, epi, splits, stream));
+    if (splits_out) *splits_out = splits;
+    return 0;
+}
+
+int norm_rows(q38_handle* h, const float* part, int splits, const uint16_t* xin, const uint16_t* resid, uint16_t* xout,
+              const uint16_t* w, uint8_t* act, int kact, int col0, uint16_t* hout, const uint16_t* div_w, hipStream_t stream) {
+    NormArgs a{};
+    a.part = part;
+    a.splits = splits;
+    a.Tpad = h->Tpad;
+    a.xin = xin;
+    a.resid = resid;
+    a.xout = xout;
+    a.w = w;
+    a.eps = h->cfg.rms_norm_eps;
+    a.act = act;
+    a.Kact = kact;
+    a.act_col0 = col0;
+    a.hout = hout;
+    a.div_w = div_w;
+    a.H = h->H;
+    a.T = h->T;
+    HIP_TRY(q38_residual_norm(a, stream));
+    return 0;
+}
+
+struct StepIO {
+    const uint16_t* cos;
+    const uint16_t* sin;
+    const int32_t* position;
+    const float* active;
+    const int32_t* accepted;
+};
+
+// Mixer of layer `li` on act_h; leaves x += mixer and act_h = e5m2(post_attention_layernorm(x)).
+int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream_t stream) {
+    bool ok = true;
+    const int H = h->H;
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint8_t* act_mid = h->ws(h->off_act_mid);
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    int splits, kmid;
+    const uint8_t* otiles;
+    const uint32_t* oscales;
+    if (is_linear(h, li)) {
+        auto qkvz_t = get<uint8_t>(h, "linear_attn.in_proj_qkvz.tiles", li, &ok);
+        auto qkvz_s = get<uint32_t>(h, "linear_attn.in_proj_qkvz.scales", li, &ok);
+        auto pin = get<uint16_t>(h, "linear_attn.pending_input", li, &ok);
+        auto wa = get<uint16_t>(h, "linear_attn.in_proj_a", li, &ok);
+        auto wb = get<uint16_t>(h, "linear_attn.in_proj_b", li, &ok);
+        auto alog = get<uint16_t>(h, "linear_attn.A_log", li, &ok);
+        auto dtb = get<uint16_t>(h, "linear_attn.dt_bias", li, &ok);
+        auto convw = get<uint16_t>(h, "linear_attn.conv_weight", li, &ok);
+        auto normw = get<uint16_t>(h, "linear_attn.norm_weight", li, &ok);
+        auto state = get<uint16_t>(h, "linear_attn.recurrent_state", li, &ok);
+        auto conv = get<uint16_t>(h, "linear_attn.conv_state", li, &ok);
+        auto pkey = get<float>(h, "linear_attn.pending_key", li, &ok);
+        auto pdelta = get<float>(h, "linear_attn.pending_delta", li, &ok);
+        auto pdecay = get<float>(h, "linear_attn.pending_decay", li, &ok);
+        otiles = get<uint8_t>(h, "linear_attn.out_proj.tiles", li, &ok);
+        oscales = get<uint32_t>(h, "linear_attn.out_proj.scales", li, &ok);
+        if (!ok) return 1;
+        const size_t BKC = (size_t)h->B * h->K * h->C;
+        uint16_t* z = (uint16_t*)h->ws(h->off_z);
+        if (gemm(h, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, pin + wr * BKC, h->C, h->C, z, h->Hv * h->dk,
+                 stream))
+            return 1;
+        GatesArgs ga{};
+        ga.x = (const bf16_t*)h->ws(h->off_hbf);
+        ga.wb = wb;
+        ga.wa = wa;
+        ga.a_log = alog;
+        ga.dt_bias = dtb;
+        ga.active = io.active;
+        ga.T = h->T;
+        ga.H = H;
+        ga.Hv = h->Hv;
+        ga.K = h->K;
+        ga.beta = (float*)h->ws(h->off_beta);
+        ga.g = (float*)h->ws(h->off_g);
+        HIP_TRY(q38_gdn_gates(ga, stream));
+        GdnArgs g{};
+        g.B = h->B;
+        g.K = h->K;
+        g.Hk = h->Hk;
+        g.Hv = h->Hv;
+        g.C = h->C;
+        g.qkv_new = pin + wr * BKC;
+        g.qkv_old = pin + rd * BKC;
+        g.z = z;
+        g.beta = ga.beta;
+        g.g = ga.g;
+        g.conv_w = convw;
+        g.norm_w = normw;
+        g.position = io.position;
+        g.active = io.active;
+        g.accepted = io.accepted;
+        g.state = state;
+        const size_t convn = (size_t)h->B * h->C * 3, keyn = (size_t)h->B * h->K * h->Hk * h->dk,
+                     deltan = (size_t)h->B * h->K * h->Hv * h->dk, decayn = (size_t)h->B * h->K * h->Hv;
+        g.conv_old = conv + rd * convn;
+        g.conv_new = conv + wr * convn;
+        g.key_old = pkey + rd * keyn;
+        g.key_new = pkey + wr * keyn;
+        g.delta_old = pdelta + rd * deltan;
+        g.delta_new = pdelta + wr * deltan;
+        g.decay_old = pdecay + rd * decayn;
+        g.decay_new = pdecay + wr * decayn;
+        g.act = act_mid;
+        g.eps = h->cfg.rms_norm_eps;
+        HIP_TRY(q38_gdn_verify(g, stream));
+        kmid = h->Hv * h->dk;
+    } else {
+        auto qkv_t = get<uint8_t>(h, "self_attn.qkv.tiles", li, &ok);
+        auto qkv_s = get<uint32_t>(h, "self_attn.qkv.scales", li, &ok);
+        auto qn = get<uint16_t>(h, "self_attn.q_norm", li, &ok);
+        auto kn = get<uint16_t>(h, "self_attn.k_norm", li, &ok);
+        auto kc = get<uint16_t>(h, "self_attn.k_cache", li, &ok);
+        auto vc = get<uint16_t>(h, "self_attn.v_cache", li, &ok);
+        otiles = get<uint8_t>(h, "self_attn.o_proj.tiles", li, &ok);
+        oscales = get<uint32_t>(h, "self_attn.o_proj.scales", li, &ok);
+        if (!ok) return 1;
+        const int nqkv = h->Hq * h->hd * 2 + 2 * h->Hkv * h->hd;
+        uint16_t* qkv = (uint16_t*)h->ws(h->off_qkv);
+        if (gemm(h, qkv_t, qkv_s, act_h, H, nqkv, EPI_BF16, qkv, nqkv, nqkv, nullptr, 0, stream)) return 1;
+        AttnArgs a{};
+        a.B = h->B;
+        a.K = h->K;
+        a.Hq = h->Hq;
+        a.Hkv = h->Hkv;
+        a.S = h->S;
+        a.qkv = qkv;
+        a.ld = nqkv;
+        a.q_norm = qn;
+        a.k_norm = kn;
+        a.cos = io.cos;
+        a.sin = io.sin;
+        a.position = io.position;
+        a.active = io.active;
+        a.k_cache = kc;
+        a.v_cache = vc;
+        a.scores = (float*)h->ws(h->off_scores);
+        a.weights = (bf16_t*)h->ws(h->off_weights);
+        a.act = act_mid;
+        a.eps = h->cfg.rms_norm_eps;
+        HIP_TRY(q38_attn_verify(a, stream));
+        kmid = h->Hq * h->hd;
+    }
+    if (gemm(h, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    auto post = get<uint16_t>(h, "post_attention_layernorm", li, &ok);
+    if (!ok) return 1;
+    return norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, x, x, post, act_h, H, 0, nullptr, nullptr, stream);
+}
+
+// MLP of layer `li` on act_h, then the residual; `next` is the following layer (its input norm is fused), or -1 for
+// the last layer, whose x goes to `final_out` (or, with `tail_norm`, the MTP output tail).
+int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail, hipStream_t stream) {
+    bool ok = true;
+    const int H = h->H, I = h->I;
+    auto gu_t = get<uint8_t>(h, "mlp.gate_up.tiles", li, &ok);
+    auto gu_s = get<uint32_t>(h, "mlp.gate_up.scales", li, &ok);
+    auto dn_t = get<uint8_t>(h, "mlp.down.tiles", li, &ok);
+    auto dn_s = get<uint32_t>(h, "mlp.down.scales", li, &ok);
+    if (!ok) return 1;
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint8_t* act_ffn = h->ws(h->off_act_ffn);
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    if (gemm(h, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
+    int splits = 0;
+    if (gemm(h, dn_t, dn_s, act_ffn, I, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    const float* part = (const float*)h->ws(h->off_part);
+    if (mtp_tail) {
+        auto nw = get<uint16_t>(h, "mtp.norm", li, &ok);
+        auto fw = get<uint16_t>(h, "head.norm", -1, &ok);
+        if (!ok) return 1;
+        return norm_rows(h, part, splits, nullptr, x, nullptr, nw, nullptr, 0, 0, final_out, fw, stream);
+    }
+    if (next < 0) return norm_rows(h, part, splits, nullptr, x, final_out, nullptr, nullptr, 0, 0, nullptr, nullptr, stream);
+    auto nw = get<uint16_t>(h, "input_layernorm", next, &ok);
+    if (!ok) return 1;
+    uint16_t* hbf = is_linear(h, next) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
+    return norm_rows(h, part, splits, nullptr, x, x, nw, act_h, H, 0, hbf, nullptr, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* q38_last_error(void) { return g_error.c_str(); }
+
+int q38_create(const q38_config* cfg, q38_handle** out) {
+    if (!cfg || !out) return fail("null argument");
+    const q38_config& c = *cfg;
+    std::string bad;
+    if (c.num_layers < 1 || c.num_layers > Q38_MAX_LAYERS) bad += "num_layers out of range; ";
+    if (c.linear_key_head_dim != 128 || c.linear_value_head_dim != 128) bad += "gated-delta head dims must be 128; ";
+    if (c.head_dim != 256) bad += "head_dim must be 256; ";
+    if (c.rotary_dim != 64) bad += "rotary_dim must be 64; ";
+    if (c.linear_conv_kernel_dim != 4) bad += "conv width must be 4; ";
+    if (c.num_key_value_heads <= 0 || c.num_attention_heads % c.num_key_value_heads) bad += "query heads per KV head; ";
+    if (c.linear_num_key_heads <= 0 || c.linear_num_value_heads % c.linear_num_key_heads) bad += "value heads per key head; ";
+    if (c.linear_num_value_heads % 8) bad += "value heads must be a multiple of 8; ";
+    if (c.hidden_size % 256 || c.hidden_size > 8192) bad += "hidden_size must be a multiple of 256, at most 8192; ";
+    if (c.intermediate_size % 256) bad += "intermediate_size must be a multiple of 256; ";
+    if (c.vocab_size % 256) bad += "vocab_size must be a multiple of 256; ";
+    if (c.verify_tokens < 1 || c.verify_tokens > 8) bad += "verify_tokens must be 1..8; ";
+    if (c.num_attention_heads / c.num_key_value_heads * c.verify_tokens > 64) bad += "query rows per KV head above 64; ";
+    if (c.batch_size < 1) bad += "batch_size must be positive; ";
+    if (c.max_seq_len % 32 || c.max_seq_len < 64) bad += "max_seq_len must be a multiple of 32; ";
+    for (int i = 0; i < c.num_layers && i < Q38_MAX_LAYERS; ++i)
+        if (c.layer_types[i] != Q38_LINEAR && c.layer_types[i] != Q38_FULL) bad += "unknown layer type; ";
+    if (!bad.empty()) return fail(bad);
+
+    auto* h = new q38_handle();
+    h->cfg = c;
+    h->H = c.hidden_size;
+    h->I = c.intermediate_size;
+    h->V = c.vocab_size;
+    h->B = c.batch_size;
+    h->K = c.verify_tokens;
+    h->S = c.max_seq_len;
+    h->T = h->B * h->K;
+    h->Tpad = pad_tokens(h->T);
+    h->Hq = c.num_attention_heads;
+    h->Hkv = c.num_key_value_heads;
+    h->hd = c.head_dim;
+    h->Hk = c.linear_num_key_heads;
+    h->Hv = c.linear_num_value_heads;
+    h->dk = c.linear_key_head_dim;
+    h->C = 2 * h->Hk * h->dk + h->Hv * h->dk;
+    h->layer.resize(c.num_layers + 1);
+    h->act_h_k = c.mtp ? 2 * h->H : h->H;
+
+    const size_t Tp = h->Tpad, H = h->H;
+    const size_t mid = std::max((size_t)h->Hv * h->dk, (size_t)h->Hq * h->hd);
+    const size_t nqkv = (size_t)h->Hq * h->hd * 2 + 2 * (size_t)h->Hkv * h->hd;
+    size_t o = 0;
+    auto take = [&](size_t n) {
+        size_t at = o;
+        o += align256(n);
+        return at;
+    };
+    h->off_x = take(Tp * H * 2);
+    h->off_hbf = take(Tp * H * 2);
+    h->off_tmp = take(Tp * H * 2);
+    h->off_act_h = take(Tp * h->act_h_k);
+    h->off_act_mid = take(Tp * mid);
+    h->off_act_ffn = take(Tp * h->I);
+    h->off_z = take(Tp * h->Hv * h->dk * 2);
+    h->off_qkv = take(Tp * nqkv * 2);
+    h->off_beta = take(Tp * h->Hv * 4);
+    h->off_g = take(Tp * h->Hv * 4);
+    h->off_part = take((size_t)SPLIT_MAX * Tp * H * 4);
+    h->off_scores = take((size_t)h->B * h->Hkv * 64 * h->S * 4);
+    h->off_weights = take((size_t)h->B * h->Hkv * 64 * h->S * 2);
+    h->off_htiles = take(Tp * H * 2);
+    h->off_x32 = take(Tp * H * 4);
+    h->off_maxima = take(Tp * (h->V / 32) * 4);
+    h->workspace_bytes = o;
+    *out = h;
+    return 0;
+}
+
+void q38_destroy(q38_handle* h) { delete h; }
+
+int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes) {
+    if (!h || !name || !nbytes) return fail("null argument");
+    size_t n = expected_size(h, name, layer);
+    if (!n) return fail(std::string("no buffer '") + name + "' for layer " + std::to_string(layer));
+    *nbytes = n;
+    return 0;
+}
+
+int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes) {
+    if (!h || !name || !dev_ptr) return fail("null argument");
+    size_t n = expected_size(h, name, layer);
+    if (!n) return fail(std::string("no buffer '") + name + "' for layer " + std::to_string(layer));
+    if (nbytes != n)
+        return fail(std::string("buffer '") + name + "' needs " + std::to_string(n) + " bytes, got " + std::to_string(nbytes));
+    if ((uintptr_t)dev_ptr % 16) return fail(std::string("buffer '") + name + "' is not 16-byte aligned");
+    Buf b;
+    b.p = dev_ptr;
+    b.n = nbytes;
+    (layer < 0 ? h->global : h->layer[layer])[name] = b;
+    return 0;
+}
+
+int q38_parity(q38_handle* h, int* parity) {
+    if (!h || !parity) return fail("null argument");
+    *parity = h->parity;
+    return 0;
+}
+
+int q38_set_parity(q38_handle* h, int parity) {
+    if (!h || (parity != 0 && parity != 1)) return fail("parity must be 0 or 1");
+    h->parity = parity;
+    return 0;
+}
+
+int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint32_t* scale_words,
+                    void* stream) {
+    if (!coded || !scales || !tiles || !scale_words) return fail("null argument");
+    if (n <= 0 || k <= 0 || n % 32 || k % 256) return fail("pack needs N % 32 == 0 and K % 256 == 0");
+    HIP_TRY(q38_pack(coded, scales, n, k, tiles, scale_words, (hipStream_t)stream));
+    return 0;
+}
+
+int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
+                   uint8_t* act_scratch, uint16_t* out, void* stream_) {
+    if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
+    if (rows < 1 || n % 256 || k % 256) return fail("fp8_linear needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+    hipStream_t stream = (hipStream_t)stream_;
+    const int tpad = pad_tokens(rows);
+    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
+    GemmArgs a{};
+    a.w = tiles;
+    a.ws = scale_words;
+    a.act = act_scratch;
+    a.K = k;
+    a.N = n;
+    a.T = rows;
+    a.Tpad = tpad;
+    a.ksteps = k / 64;
+    a.unit_scale = 127;
+    a.out0 = out;
+    a.ld0 = n;
+    a.n0 = n;
+    HIP_TRY(q38_gemm_fp8(a, EPI_BF16, 1, stream));
+    return 0;
+}
+
+size_t q38_fp8_linear_scratch(int rows, int k) { return (size_t)pad_tokens(rows) * k; }
+
+int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
+                       uint8_t* act_scratch, float* out, void* stream_) {
+    if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
+    if (rows < 1 || rows % 32 || n % 256 || k % 256)
+        return fail("fp8_linear_f32 needs rows % 32 == 0, N % 256 == 0 and K % 256 == 0");
+    hipStream_t stream = (hipStream_t)stream_;
+    const int tpad = pad_tokens(rows);
+    if (tpad != rows) return fail("fp8_linear_f32 needs rows in {32, 64, 128} or a multiple of 256");
+    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
+    GemmArgs a{};
+    a.w = tiles;
+    a.ws = scale_words;
+    a.act = act_scratch;
+    a.K = k;
+    a.N = n;
+    a.T = rows;
+    a.Tpad = tpad;
+    a.ksteps = k / 64;
+    a.unit_scale = 127;
+    a.part = out;
+    HIP_TRY(q38_gemm_fp8(a, EPI_PARTIAL, 1, stream));
+    return 0;
+}
+
+int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
+               const float* active, const int32_t* accepted, uint16_t* out_hidden, void* stream_) {
+    if (!h || !embeds || !cos || !sin || !position || !active || !accepted || !out_hidden) return fail("null argument");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto in0 = get<uint16_t>(h, "input_layernorm", 0, &ok);
+    if (!ok) return 1;
+    const int L = h->cfg.num_layers, rd = h->parity, wr = 1 - h->parity;
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    uint16_t* hbf = is_linear(h, 0) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
+    StepIO io{cos, sin, position, active, accepted};
+    for (int li = 0; li < L; ++li) {
+        if (run_mixer(h, li, io, rd, wr, stream)) return 1;
+        if (run_mlp(h, li, li + 1 < L ? li + 1 : -1, out_hidden, false, stream)) return 1;
+    }
+    h->parity = wr;
+    return 0;
+}
+
+int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin,
+                 const int32_t* position, const float* active, uint16_t* out, void* stream_) {
+    if (!h || !hidden || !embeds || !cos || !sin || !position || !active || !out) return fail("null argument");
+    if (!h->cfg.mtp) return fail("the handle was created without the MTP layer");
+    hipStream_t stream = (hipStream_t)stream_;
+    const int M = h->cfg.num_layers, H = h->H;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto en = get<uint16_t>(h, "mtp.embedding_norm", M, &ok);
+    auto hn = get<uint16_t>(h, "mtp.hidden_norm", M, &ok);
+    auto fin = get<uint16_t>(h, "head.norm", -1, &ok);
+    auto fc_t = get<uint8_t>(h, "mtp.fc.tiles", M, &ok);
+    auto fc_s = get<uint32_t>(h, "mtp.fc.scales", M, &ok);
+    auto in0 = get<uint16_t>(h, "input_layernorm", M, &ok);
+    if (!ok) return 1;
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint16_t* tmp = (uint16_t*)h->ws(h->off_tmp);
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    // [rms(embeds) | rms(rms(hidden, final norm), hidden norm)] as the fc's 2H-wide e5m2 input (model.py:845-851).
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, nullptr, en, act_h, 2 * H, 0, nullptr, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, hidden, nullptr, nullptr, fin, nullptr, 0, 0, tmp, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, tmp, nullptr, nullptr, hn, act_h, 2 * H, H, nullptr, nullptr, stream)) return 1;
+    int splits = 0;
+    if (gemm(h, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, nullptr, x, in0, act_h, H, 0, nullptr, nullptr, stream))
+        return 1;
+    StepIO io{cos, sin, position, active, nullptr};
+    if (run_mixer(h, M, io, 0, 0, stream)) return 1;
+    return run_mlp(h, M, -1, out, true, stream);
+}
+
+int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* maxima, void* stream_) {
+    if (!h || !hidden || !maxima) return fail("null argument");
+    if (rows < 1 || rows > h->T) return fail("head rows must be 1..B*K");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto nw = get<uint16_t>(h, "head.norm", -1, &ok);
+    auto wt = get<uint8_t>(h, "head.lm_head.tiles", -1, &ok);
+    auto wsc = get<uint32_t>(h, "head.lm_head.scales", -1, &ok);
+    if (!ok) return 1;
+    HIP_TRY(q38_head_norm(hidden, nw, h->cfg.rms_norm_eps, h->H, rows, (bf16_t*)h->ws(h->off_htiles),
+                          (float*)h->ws(h->off_x32), stream));
+    HeadArgs a{};
+    a.w = wt;
+    a.ws = wsc;
+    a.act = (const bf16_t*)h->ws(h->off_htiles);
+    a.K = h->H;
+    a.V = h->V;
+    a.R = rows;
+    a.Rpad = pad_tokens(rows);
+    a.maxima = maxima;
+    HIP_TRY(q38_head_groupmax(a, stream));
+    return 0;
+}
+
+int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, int32_t* ids, void* stream_) {
+    if (!h || !hidden || !ids) return fail("null argument");
+    if (groups < 1 || groups > 4) return fail("recheck groups must be 1..4");
+    float* maxima = (float*)h->ws(h->off_maxima);
+    if (q38_head_groupmax(h, hidden, rows, maxima, stream_)) return 1;
+    bool ok = true;
+    auto wt = get<uint8_t>(h, "head.lm_head.tiles", -1, &ok);
+    auto wsc = get<uint32_t>(h, "head.lm_head.scales", -1, &ok);
+    if (!ok) return 1;
+    PickArgs a{};
+    a.maxima = maxima;
+    a.ngroups = h->V / 32;
+    a.x32 = (const float*)h->ws(h->off_x32);
+    a.w = wt;
+    a.ws = wsc;
+    a.H = h->H;
+    a.R = rows;
+    a.groups = groups;
+    a.ids = ids;
+    HIP_TRY(q38_head_pick(a, (hipStream_t)stream_));
+    return 0;
+}
+
+int q38_embed(q38_handle* h, const int32_t* ids, int n, uint16_t* out, void* stream) {
+    if (!h || !ids || !out) return fail("null argument");
+    bool ok = true;
+    auto table = get<uint16_t>(h, "embed_tokens", -1, &ok);
+    if (!ok) return 1;
+    if (n <= 0) return 0;
+    HIP_TRY(q38_embed(ids, n, table, h->V, h->H, out, (hipStream_t)stream));
+    return 0;
+}
+
+int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const float* active, int32_t* match,
+               int32_t* accepted, void* stream) {
+    if (!h || !picks || !drafts || !active || !match || !accepted) return fail("null argument");
+    if (h->K < 2) return fail("acceptance needs at least 2 verify tokens");
+    HIP_TRY(q38_accept(picks, drafts, active, h->B, h->K, match, accepted, (hipStream_t)stream));
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,124 @@
+// Kernel argument blocks and launchers of the verify path; the host engine (engine.cpp) fills these.
+#pragma once
+
+#include "common.h"
+
+enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2 };
+
+struct GemmArgs {
+    const uint8_t* w;    // weight tiles [N/32][K/64][64][32]
+    const uint32_t* ws;  // scale words [N/32][K/256][64]: byte j of a lane's word is K-step 4q+j
+    const uint8_t* act;  // activation tiles [Tpad/32][K/64][64][32]
+    int K, N, T, Tpad;
+    int ksteps;          // K-steps of 64 per split (even)
+    int unit_scale;      // 127: E8M0 of 1.0 for the activations, passed at run time
+    void* out0;
+    int ld0, n0;
+    void* out1;
+    int ld1;
+    float* part;
+};
+
+struct HeadArgs {
+    const uint8_t* w;
+    const uint32_t* ws;
+    const bf16_t* act;
+    int K, V, R, Rpad;
+    float* maxima;       // [R][V/32]
+};
+
+struct NormArgs {
+    const float* part;     // split-K partials [splits][Tpad][H], or null
+    int splits, Tpad;
+    const bf16_t* xin;     // without partials: the rows to normalize
+    const bf16_t* resid;   // with partials: x_new = bf16(resid + bf16(sum)); null: x_new = bf16(sum)
+    bf16_t* xout;          // x_new (may alias resid), or null
+    const bf16_t* w;       // norm weight, used as (1 + w)
+    float eps;
+    uint8_t* act;          // e5m2 tiles of width Kact at column act_col0, or null
+    int Kact, act_col0;
+    bf16_t* hout;          // bf16 normed rows [T][H], or null
+    const bf16_t* div_w;   // MTP tail: hout = bf16(normed / (1 + div_w))
+    int H, T;
+};
+
+struct GatesArgs {
+    const bf16_t* x;       // [T][H] bf16 (the input norm's output)
+    const bf16_t* wb;      // in_proj_b [Hv][H]
+    const bf16_t* wa;      // in_proj_a [Hv][H]
+    const bf16_t* a_log;   // [Hv]
+    const bf16_t* dt_bias; // [Hv]
+    const float* active;   // [B]
+    int T, H, Hv, K;
+    float* beta;           // [T][Hv]
+    float* g;              // [T][Hv]
+};
+
+struct GdnArgs {
+    int B, K, Hk, Hv, C;
+    const bf16_t* qkv_new;   // [B*K][C]: this step's in_proj_qkv output, also the new pending input snapshot
+    const bf16_t* qkv_old;   // [B*K][C]: the last step's (pending_input_state)
+    const bf16_t* z;         // [B*K][Hv*128]
+    const float* beta;       // [B*K][Hv]
+    const float* g;          // [B*K][Hv]
+    const bf16_t* conv_w;    // [C][4]
+    const bf16_t* norm_w;    // [128]
+    const int* position;
+    const float* active;
+    const int* accepted;
+    bf16_t* state;           // [B][Hv][128][128]
+    const bf16_t* conv_old;  // [B][C][3]
+    bf16_t* conv_new;
+    const float* key_old;    // [B][K][Hk][128]
+    float* key_new;
+    const float* delta_old;  // [B][K][Hv][128]
+    float* delta_new;
+    const float* decay_old;  // [B][K][Hv]
+    float* decay_new;
+    uint8_t* act;            // e5m2 tiles of width Hv*128 for out_proj
+    float eps;
+};
+
+struct AttnArgs {
+    int B, K, Hq, Hkv, S;
+    const bf16_t* qkv;      // [B*K][ld]: per query head [q 256 | gate 256], then k [Hkv][256], then v [Hkv][256]
+    int ld;
+    const bf16_t* q_norm;   // [256]
+    const bf16_t* k_norm;   // [256]
+    const bf16_t* cos;      // [B*K][64]
+    const bf16_t* sin;
+    const int* position;
+    const float* active;
+    bf16_t* k_cache;
+    bf16_t* v_cache;
+    float* scores;          // [B*Hkv][64][S]
+    bf16_t* weights;        // [B*Hkv][64][S]
+    uint8_t* act;           // e5m2 tiles of width Hq*256 for o_proj
+    float eps;
+};
+
+struct PickArgs {
+    const float* maxima;   // [R][ngroups]
+    int ngroups;
+    const float* x32;      // [R][H]
+    const uint8_t* w;      // lm_head tiles [V/32][H/64][64][32]
+    const uint32_t* ws;    // lm_head scale words
+    int H, R, groups;
+    int* ids;              // [R]
+};
+
+hipError_t q38_gemm_fp8(const GemmArgs& a, int epi, int splits, hipStream_t stream);
+hipError_t q38_head_groupmax(const HeadArgs& a, hipStream_t stream);
+hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream);
+hipError_t q38_head_norm(const bf16_t* hidden, const bf16_t* w, float eps, int H, int rows, bf16_t* tiles, float* x32,
+                         hipStream_t stream);
+hipError_t q38_embed(const int* ids, int n, const bf16_t* table, int V, int H, bf16_t* out, hipStream_t stream);
+hipError_t q38_gdn_gates(const GatesArgs& a, hipStream_t stream);
+hipError_t q38_gdn_verify(const GdnArgs& a, hipStream_t stream);
+hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream);
+hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream);
+hipError_t q38_accept(const int* picks, const int* drafts, const float* active, int B, int K, int* match, int* accepted,
+                      hipStream_t stream);
+hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint32_t* words,
+                    hipStream_t stream);
+hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);

@@ -1,0 +1,163 @@
+// Token choice from the head's group maxima: `ChipHead.next_tokens` after its graph (reference
+// qwen38_inf2/generate.py:186-208), on the GPU so only ids go back to the host.
+//   1. the `groups` best groups of 32 vocabulary rows by group maximum (torch.topk order: largest first);
+//   2. exact float32 logits of their rows against the float32-normed hidden state (lm_head rows dequantized exactly);
+//   3. the best row of each group, and across groups the first strictly larger in top-k order.
+// A row with no finite logit gets id -1, which the host turns into the reference's FloatingPointError.
+// Greedy acceptance (scheduler.py:291-300) is here too, for the on-device speculative step.
+#include "kernels.h"
+
+#define PICK_GMAX 4
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// torch.topk order: NaN first, then larger values; equal values by lower index.
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+    bool na = a != a, nb = b != b;
+    if (na != nb) return na;
+    if (na) return ia < ib;
+    return a > b || (a == b && ia < ib);
+}
+
+__global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
+    __shared__ float lv[256][PICK_GMAX];
+    __shared__ int li[256][PICK_GMAX];
+    __shared__ float xrow[8192];
+    __shared__ float glogit[PICK_GMAX];
+    __shared__ int gtoken[PICK_GMAX];
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.groups;
+
+    float bv[PICK_GMAX];
+    int bi[PICK_GMAX];
+#pragma unroll
+    for (int k = 0; k < PICK_GMAX; ++k) {
+        bv[k] = -INFINITY;
+        bi[k] = 0x7fffffff;
+    }
+    const float* mrow = a.maxima + (size_t)r * a.ngroups;
+    for (int i = tid; i < a.ngroups; i += 256) {
+        float v = mrow[i];
+        if (!ranks_before(v, i, bv[G - 1], bi[G - 1])) continue;
+        int k = G - 1;
+        while (k > 0 && ranks_before(v, i, bv[k - 1], bi[k - 1])) {
+            bv[k] = bv[k - 1];
+            bi[k] = bi[k - 1];
+            --k;
+        }
+        bv[k] = v;
+        bi[k] = i;
+    }
+#pragma unroll
+    for (int k = 0; k < PICK_GMAX; ++k) {
+        lv[tid][k] = bv[k];
+        li[tid][k] = bi[k];
+    }
+    for (int c = tid; c < a.H; c += 256) xrow[c] = a.x32[(size_t)r * a.H + c];
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (tid < stride) {
+            float mv[PICK_GMAX];
+            int mi[PICK_GMAX];
+            int x = 0, y = 0;
+            for (int k = 0; k < G; ++k) {
+                bool takex = ranks_before(lv[tid][x], li[tid][x], lv[tid + stride][y], li[tid + stride][y]);
+                mv[k] = takex ? lv[tid][x] : lv[tid + stride][y];
+                mi[k] = takex ? li[tid][x] : li[tid + stride][y];
+                if (takex) ++x; else ++y;
+            }
+            for (int k = 0; k < G; ++k) {
+                lv[tid][k] = mv[k];
+                li[tid][k] = mi[k];
+            }
+        }
+        __syncthreads();
+    }
+
+    // Exact logits: wave w rechecks the w-th best group, which is one 32-row weight tile.
+    const int KS = a.H >> 6;
+    if (wave < G) {
+        const int grp = li[0][wave];
+        float acc = 0.0f;
+        if (grp >= 0 && grp < a.ngroups) {
+            // Lane half h holds inputs [16h, 16h + 16) of the K-step in bytes 0-15 (first MX block, scale byte of
+            // lane half 0) and [32 + 16h, 48 + 16h) in bytes 16-31 (second block, scale byte of lane half 1).
+            const uint8_t* tile = a.w + (size_t)grp * KS * 2048 + lane * 32;
+            const uint32_t* sw = a.ws + (size_t)grp * (KS >> 2) * 64 + (lane & 31);
+            const float* xp = xrow + (lane >> 5) * 16;
+            for (int ks = 0; ks < KS; ++ks) {
+                const int shift = (ks & 3) * 8;
+                const float s0 = __uint_as_float(((sw[(size_t)(ks >> 2) * 64] >> shift) & 0xff) << 23);
+                const float s1 = __uint_as_float(((sw[(size_t)(ks >> 2) * 64 + 32] >> shift) & 0xff) << 23);
+                const v4i* p = (const v4i*)(tile + (size_t)ks * 2048);
+                v4i lo = p[0], hi = p[1];
+                uint32_t words[8] = {(uint32_t)lo[0], (uint32_t)lo[1], (uint32_t)lo[2], (uint32_t)lo[3],
+                                     (uint32_t)hi[0], (uint32_t)hi[1], (uint32_t)hi[2], (uint32_t)hi[3]};
+#pragma unroll
+                for (int wi = 0; wi < 8; ++wi) {
+                    const float scale = wi < 4 ? s0 : s1;
+                    v2f f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[wi], scale, false);
+                    v2f f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(words[wi], scale, true);
+                    const float* xv = xp + ks * 64 + (wi >> 2) * 32 + (wi & 3) * 4;
+                    acc += f0[0] * xv[0];
+                    acc += f0[1] * xv[1];
+                    acc += f1[0] * xv[2];
+                    acc += f1[1] * xv[3];
+                }
+            }
+        }
+        acc += __shfl_xor(acc, 32);
+        // Largest logit of the group, first index on ties; NaN propagates as torch.max does.
+        float v = acc;
+        int idx = lane & 31;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            float ov = __shfl_xor(v, o);
+            int oi = __shfl_xor(idx, o);
+            bool take = (ov != ov && v == v) || (!(v != v) && (ov > v || (ov == v && oi < idx)));
+            if (take) {
+                v = ov;
+                idx = oi;
+            }
+        }
+        if (lane == 0) {
+            glogit[wave] = v;
+            gtoken[wave] = grp * 32 + idx;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int best = -1;
+        float bestv = -INFINITY;
+        for (int k = 0; k < G; ++k) {
+            if (glogit[k] > bestv) {
+                bestv = glogit[k];
+                best = gtoken[k];
+            }
+        }
+        a.ids[r] = best;
+    }
+}
+
+hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(head_pick_kernel, dim3(a.R), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+// Greedy acceptance per row: match = leading drafts equal to the picks (at most K - 1), accepted = match + 1 for
+// active rows, else 0. picks [B][K], drafts [B][K-1].
+__global__ void accept_kernel(const int* picks, const int* drafts, const float* active, int B, int K, int* match,
+                              int* accepted) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    int m = 0;
+    while (m < K - 1 && drafts[b * (K - 1) + m] == picks[b * K + m]) ++m;
+    match[b] = m;
+    accepted[b] = active[b] > 0.5f ? m + 1 : 0;
+}
+
+hipError_t q38_accept(const int* picks, const int* drafts, const float* active, int B, int K, int* match, int* accepted,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(accept_kernel, dim3((B + 63) / 64), dim3(64), 0, stream, picks, drafts, active, B, K, match, accepted);
+    return hipGetLastError();
+}

@@ -1,0 +1,191 @@
+"""ctypes binding of libq38.so (include/q38.h). Device tensors are passed as raw pointers on torch's current HIP stream.
+
+There is no fallback: if the library is missing or was built for another architecture, `library()` raises, and every
+step object fails with it. Build it with `python -m qwen38_amd.build` (or `__graft_entry__.build()`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+from .config import FULL, LINEAR, TextConfig
+
+LIB_PATH = Path(__file__).resolve().parent / "libq38.so"
+MAX_LAYERS = 128
+
+EXPORTS = (
+    "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
+    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_verify", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept",
+)
+
+
+class Q38Config(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", ctypes.c_int), ("intermediate_size", ctypes.c_int), ("vocab_size", ctypes.c_int),
+        ("num_layers", ctypes.c_int), ("layer_types", ctypes.c_int * MAX_LAYERS),
+        ("num_attention_heads", ctypes.c_int), ("num_key_value_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+        ("rotary_dim", ctypes.c_int),
+        ("linear_num_key_heads", ctypes.c_int), ("linear_num_value_heads", ctypes.c_int),
+        ("linear_key_head_dim", ctypes.c_int), ("linear_value_head_dim", ctypes.c_int),
+        ("linear_conv_kernel_dim", ctypes.c_int), ("rms_norm_eps", ctypes.c_float),
+        ("batch_size", ctypes.c_int), ("verify_tokens", ctypes.c_int), ("max_seq_len", ctypes.c_int), ("mtp", ctypes.c_int),
+    ]
+
+
+_lib = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded libq38.so with argument types set. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m qwen38_amd.build` (the verify path has no fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    p, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.q38_last_error.restype = ctypes.c_char_p
+    lib.q38_last_error.argtypes = []
+    lib.q38_create.argtypes = [ctypes.POINTER(Q38Config), ctypes.POINTER(p)]
+    lib.q38_destroy.argtypes = [p]
+    lib.q38_destroy.restype = None
+    lib.q38_buffer_size.argtypes = [p, ctypes.c_char_p, i, ctypes.POINTER(sz)]
+    lib.q38_bind.argtypes = [p, ctypes.c_char_p, i, p, sz]
+    lib.q38_parity.argtypes = [p, ctypes.POINTER(i)]
+    lib.q38_set_parity.argtypes = [p, i]
+    lib.q38_pack_weight.argtypes = [p, p, i, i, p, p, p]
+    lib.q38_fp8_linear.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_fp8_linear_scratch.argtypes = [i, i]
+    lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_verify.argtypes = [p] * 8 + [p]
+    lib.q38_mtp_step.argtypes = [p] * 8 + [p]
+    lib.q38_head_groupmax.argtypes = [p, p, i, p, p]
+    lib.q38_head_pick.argtypes = [p, p, i, i, p, p]
+    lib.q38_embed.argtypes = [p, p, i, p, p]
+    lib.q38_accept.argtypes = [p, p, p, p, p, p, p]
+    for name in EXPORTS:
+        if name not in ("q38_last_error", "q38_destroy"):
+            getattr(lib, name).restype = ctypes.c_size_t if name == "q38_fp8_linear_scratch" else ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc:
+        raise RuntimeError("libq38: " + library().q38_last_error().decode())
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("libq38 takes device tensors")
+    if not t.is_contiguous():
+        raise ValueError("libq38 takes contiguous tensors")
+    return t.data_ptr()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool) -> Q38Config:
+    c = Q38Config()
+    c.hidden_size, c.intermediate_size, c.vocab_size = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    if cfg.num_hidden_layers > MAX_LAYERS:
+        raise ValueError(f"at most {MAX_LAYERS} layers")
+    c.num_layers = cfg.num_hidden_layers
+    for i, kind in enumerate(cfg.layer_types):
+        c.layer_types[i] = {LINEAR: 0, FULL: 1}[kind]
+    c.num_attention_heads, c.num_key_value_heads, c.head_dim = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    c.rotary_dim = cfg.rotary_dim
+    c.linear_num_key_heads, c.linear_num_value_heads = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+    c.linear_key_head_dim, c.linear_value_head_dim = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    c.linear_conv_kernel_dim = cfg.linear_conv_kernel_dim
+    c.rms_norm_eps = cfg.rms_norm_eps
+    c.batch_size, c.verify_tokens, c.max_seq_len, c.mtp = batch, tokens, max_seq_len, int(mtp)
+    return c
+
+
+class Handle:
+    """One q38_handle: shapes fixed at creation, every buffer bound by the owner."""
+
+    def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool):
+        self.lib = library()
+        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp)
+        h = ctypes.c_void_p()
+        check(self.lib.q38_create(ctypes.byref(self.c), ctypes.byref(h)))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None) and self.h.value:
+            self.lib.q38_destroy(self.h)
+            self.h = None
+
+    def buffer_size(self, name: str, layer: int) -> int:
+        n = ctypes.c_size_t()
+        check(self.lib.q38_buffer_size(self.h, name.encode(), layer, ctypes.byref(n)))
+        return n.value
+
+    def bind(self, name: str, layer: int, t: torch.Tensor) -> None:
+        check(self.lib.q38_bind(self.h, name.encode(), layer, ptr(t), t.numel() * t.element_size()))
+
+    @property
+    def parity(self) -> int:
+        p = ctypes.c_int()
+        check(self.lib.q38_parity(self.h, ctypes.byref(p)))
+        return p.value
+
+    @parity.setter
+    def parity(self, value: int) -> None:
+        check(self.lib.q38_set_parity(self.h, value))
+
+    def verify(self, embeds, cos, sin, position, active, accepted, out) -> None:
+        check(self.lib.q38_verify(self.h, *map(ptr, (embeds, cos, sin, position, active, accepted, out)), stream()))
+
+    def mtp_step(self, hidden, embeds, cos, sin, position, active, out) -> None:
+        check(self.lib.q38_mtp_step(self.h, *map(ptr, (hidden, embeds, cos, sin, position, active, out)), stream()))
+
+    def head_groupmax(self, hidden, rows: int, maxima) -> None:
+        check(self.lib.q38_head_groupmax(self.h, ptr(hidden), rows, ptr(maxima), stream()))
+
+    def head_pick(self, hidden, rows: int, groups: int, ids) -> None:
+        check(self.lib.q38_head_pick(self.h, ptr(hidden), rows, groups, ptr(ids), stream()))
+
+    def embed(self, ids, n: int, out) -> None:
+        check(self.lib.q38_embed(self.h, ptr(ids), n, ptr(out), stream()))
+
+    def accept(self, picks, drafts, active, match, accepted) -> None:
+        check(self.lib.q38_accept(self.h, *map(ptr, (picks, drafts, active, match, accepted)), stream()))
+
+
+def pack_weight(coded: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(e4m3 bytes [N, K], E8M0 bytes [N, K/32]) on the GPU -> (tiles, scale words) in the GEMM layout."""
+    n, k = coded.shape
+    tiles = torch.empty(n * k, dtype=torch.uint8, device=coded.device)
+    words = torch.empty(n // 32 * (k // 256) * 64, dtype=torch.int32, device=coded.device)
+    check(library().q38_pack_weight(ptr(coded.contiguous()), ptr(scales.contiguous()), n, k, ptr(tiles), ptr(words), stream()))
+    return tiles, words
+
+
+def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, n: int) -> torch.Tensor:
+    """`FP8Linear.forward` on the GPU: bf16 x [rows, k] -> bf16 [rows, n] through a packed FP8 weight."""
+    rows, k = x.shape
+    lib = library()
+    scratch = torch.empty(lib.q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(words), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def fp8_linear_f32(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, n: int) -> torch.Tensor:
+    """The FP8 projection with float32 output (no bf16 rounding): rows in {32, 64, 128} or a multiple of 256."""
+    rows, k = x.shape
+    lib = library()
+    scratch = torch.empty(lib.q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
+    out = torch.empty(rows, n, dtype=torch.float32, device=x.device)
+    check(lib.q38_fp8_linear_f32(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(words), n, ptr(scratch), ptr(out), stream()))
+    return out

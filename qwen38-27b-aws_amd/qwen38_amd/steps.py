@@ -1,0 +1,298 @@
+"""Step objects with the reference's call contracts, running on libq38 (the HIP library) on one GPU.
+
+* `VerifyStep.__call__(inputs_embeds, cos, sin, position, active, accepted)` -> hidden ``[B, K, H]``: the reference's
+  verify graph, `Qwen38Step.forward` with `accepted` (qwen38_inf2/model.py:933-995, called at scheduler.py:288).
+* `MTPStep.__call__(hidden, inputs_embeds, cos, sin, position, active)` -> ``[B, K, H]``: `MTPStep.forward`
+  (model.py:843-860, called at scheduler.py:179,192).
+* `HeadGraph.__call__(hidden=[R, 1, H])` -> group maxima ``[R, V/32]`` float32: the head graph `run_graph`
+  (`HeadStep.forward`, model.py:890-900, called at generate.py:195); `pick` runs `ChipHead.next_tokens`'s recheck on the
+  GPU too, and `embed` gathers embedding rows.
+
+`Engine` owns every device buffer the library uses (weights packed once, recurrent/conv/snapshot states, KV caches, the
+workspace) and binds them to one handle. Inputs may be host or device tensors; outputs are device tensors.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterable, Sequence
+
+import torch
+
+from . import ext
+from .config import FULL, LINEAR, TextConfig
+
+DTYPE = torch.bfloat16
+
+
+def _interleave32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Rows of a and b alternating in blocks of 32: the gate/up tile pairs the SwiGLU epilogue reads."""
+    n = a.shape[0]
+    return torch.stack((a.reshape(n // 32, 32, -1), b.reshape(n // 32, 32, -1)), dim=1).reshape(2 * n, -1)
+
+
+def _cat_fp8(parts: Sequence[tuple[torch.Tensor, torch.Tensor]]):
+    return torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
+
+
+class Engine:
+    """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
+
+    def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda"):
+        if not torch.cuda.is_available():
+            raise RuntimeError("the verify path runs on the GPU only")
+        self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
+        self.device = torch.device(device)
+        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp)
+        self.buffers: dict[tuple[str, int], torch.Tensor] = {}
+        self.mtp_layer = cfg.num_hidden_layers
+        self._bind_zeros("workspace", -1, torch.uint8)
+        for i, kind in enumerate(cfg.layer_types):
+            if kind == LINEAR:
+                self._bind_zeros("linear_attn.recurrent_state", i, DTYPE)
+                self._bind_zeros("linear_attn.conv_state", i, DTYPE)
+                self._bind_zeros("linear_attn.pending_key", i, torch.float32)
+                self._bind_zeros("linear_attn.pending_delta", i, torch.float32)
+                self._bind_zeros("linear_attn.pending_decay", i, torch.float32)
+                self._bind_zeros("linear_attn.pending_input", i, DTYPE)
+            else:
+                self._bind_zeros("self_attn.k_cache", i, DTYPE)
+                self._bind_zeros("self_attn.v_cache", i, DTYPE)
+        if mtp:
+            self._bind_zeros("self_attn.k_cache", self.mtp_layer, DTYPE)
+            self._bind_zeros("self_attn.v_cache", self.mtp_layer, DTYPE)
+
+    # ------------------------------------------------------------------------------------------------ buffers
+
+    def _bind_zeros(self, name: str, layer: int, dtype: torch.dtype) -> torch.Tensor:
+        nbytes = self.handle.buffer_size(name, layer)
+        size = torch.empty((), dtype=dtype).element_size()
+        t = torch.zeros(nbytes // size, dtype=dtype, device=self.device)
+        return self.bind(name, layer, t)
+
+    def bind(self, name: str, layer: int, t: torch.Tensor) -> torch.Tensor:
+        t = t.to(self.device).contiguous()
+        self.handle.bind(name, layer, t)
+        self.buffers[(name, layer)] = t
+        return t
+
+    def buffer(self, name: str, layer: int) -> torch.Tensor:
+        return self.buffers[(name, layer)]
+
+    # ------------------------------------------------------------------------------------------------ weights
+
+    def _fp8(self, name: str, layer: int, coded: torch.Tensor, scales: torch.Tensor) -> None:
+        tiles, words = ext.pack_weight(coded.to(self.device), scales.to(self.device))
+        self.bind(name + ".tiles", layer, tiles)
+        self.bind(name + ".scales", layer, words)
+
+    def load_layer(self, layer: int, w: dict, kind: str) -> None:
+        """One decoder layer's weights by the reference's short names (synth.layer_specs without the prefix)."""
+        self.bind("input_layernorm", layer, w["input_layernorm_weight"])
+        self.bind("post_attention_layernorm", layer, w["post_attention_layernorm_weight"])
+        g, u = w["mlp.gate_proj"], w["mlp.up_proj"]
+        self._fp8("mlp.gate_up", layer, _interleave32(g[0], u[0]), _interleave32(g[1], u[1]))
+        self._fp8("mlp.down", layer, *w["mlp.down_proj"])
+        if kind == LINEAR:
+            la = "linear_attn."
+            self._fp8(la + "in_proj_qkvz", layer, *_cat_fp8([w[la + "in_proj_qkv"], w[la + "in_proj_z"]]))
+            self._fp8(la + "out_proj", layer, *w[la + "out_proj"])
+            for key in ("in_proj_a", "in_proj_b", "conv_weight", "A_log", "dt_bias", "norm_weight"):
+                self.bind(la + key, layer, w[la + key].to(DTYPE))
+        else:
+            sa = "self_attn."
+            self._fp8(sa + "qkv", layer, *_cat_fp8([w[sa + "q_proj"], w[sa + "k_proj"], w[sa + "v_proj"]]))
+            self._fp8(sa + "o_proj", layer, *w[sa + "o_proj"])
+            self.bind(sa + "q_norm", layer, w[sa + "q_norm_weight"])
+            self.bind(sa + "k_norm", layer, w[sa + "k_norm_weight"])
+
+    def load(self, weights: Iterable[tuple[str, object]]) -> None:
+        """Weights by their full names (`synth.model_specs`): ``layers.{i}.*``, ``mtp.*``, ``head.*``, ``embed_tokens``.
+        Consumed layer by layer, so a generator keeps host and device peaks to one layer."""
+        pending: dict[int, dict] = {}
+        need = {}
+        for name, value in weights:
+            if name.startswith("layers."):
+                i = int(name.split(".")[1])
+                short = name[len(f"layers.{i}.") :]
+                pending.setdefault(i, {})[short] = value
+                kind = self.cfg.layer_types[i]
+                if i not in need:
+                    need[i] = self._layer_names(kind)
+                if need[i] <= set(pending[i]):
+                    self.load_layer(i, pending.pop(i), kind)
+            elif name.startswith("mtp.layer."):
+                pending.setdefault(self.mtp_layer, {})[name[len("mtp.layer.") :]] = value
+                if self._layer_names(FULL) <= set(pending[self.mtp_layer]):
+                    self.load_layer(self.mtp_layer, pending.pop(self.mtp_layer), FULL)
+            elif name == "mtp.fc":
+                self._fp8("mtp.fc", self.mtp_layer, *value)
+            elif name in ("mtp.embedding_norm_weight", "mtp.hidden_norm_weight", "mtp.norm_weight"):
+                self.bind(name[: -len("_weight")], self.mtp_layer, value)
+            elif name == "head.norm_weight":
+                self.bind("head.norm", -1, value)
+            elif name == "head.lm_head":
+                self._fp8("head.lm_head", -1, *value)
+            elif name == "embed_tokens":
+                self.bind("embed_tokens", -1, value)
+            else:
+                raise KeyError(f"unknown weight {name}")
+        if pending:
+            raise ValueError(f"incomplete layers {sorted(pending)}")
+
+    @staticmethod
+    def _layer_names(kind: str) -> set:
+        from .config import tiny_config, with_layers
+        from .synth import layer_specs
+
+        return {s.name[len("layers.0.") :] for s in layer_specs(with_layers(tiny_config(1), (kind,)), 0)}
+
+    # ------------------------------------------------------------------------------------------------ state views
+
+    @property
+    def parity(self) -> int:
+        return self.handle.parity
+
+    def gdn_state(self, layer: int, current: bool = True) -> dict:
+        """Views of a gated-delta layer's state in the reference's buffer shapes where they agree: recurrent_state
+        [B,Hv,d,d], conv_state [B,C,3], pending_key [B,K,Hk,d] (one per key head; the reference repeats it per value
+        head), pending_delta [B,K,Hv,d], pending_decay [B,K,Hv], pending_input [B,K,C]. ``current`` picks the half the
+        next verify step reads."""
+        cfg, b, k = self.cfg, self.batch_size, self.verify_tokens
+        half = self.parity if current else 1 - self.parity
+        hv, hk, d, c = cfg.linear_num_value_heads, cfg.linear_num_key_heads, cfg.linear_key_head_dim, cfg.linear_conv_dim
+        get = lambda n: self.buffer("linear_attn." + n, layer)
+        return {
+            "recurrent_state": get("recurrent_state").view(b, hv, d, d),
+            "conv_state": get("conv_state").view(2, b, c, 3)[half],
+            "pending_key_state": get("pending_key").view(2, b, k, hk, d)[half],
+            "pending_delta_state": get("pending_delta").view(2, b, k, hv, d)[half],
+            "pending_decay_state": get("pending_decay").view(2, b, k, hv)[half],
+            "pending_input_state": get("pending_input").view(2, b, k, c)[half],
+        }
+
+    def kv_cache(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """(k_cache [B,Hkv,S,hd], v_cache stored transposed [B,Hkv,S/32,hd,32])."""
+        cfg, b, s = self.cfg, self.batch_size, self.max_seq_len
+        kc = self.buffer("self_attn.k_cache", layer).view(b, cfg.num_key_value_heads, s, cfg.head_dim)
+        vc = self.buffer("self_attn.v_cache", layer).view(b, cfg.num_key_value_heads, s // 32, cfg.head_dim, 32)
+        return kc, vc
+
+    def set_kv(self, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+        """Write reference-layout caches [B,Hkv,S,hd]."""
+        kc, vc = self.kv_cache(layer)
+        kc.copy_(k_cache)
+        b, h, s, d = v_cache.shape
+        vc.copy_(v_cache.reshape(b, h, s // 32, 32, d).transpose(-1, -2))
+
+    def get_kv(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Caches in the reference layout [B,Hkv,S,hd]."""
+        kc, vc = self.kv_cache(layer)
+        b, h, n, d, _ = vc.shape
+        return kc.clone(), vc.transpose(-1, -2).reshape(b, h, n * 32, d)
+
+    def set_gdn(self, layer: int, st: dict) -> None:
+        """Load reference-shaped gated-delta state (pending_key_state per value head) into the current half."""
+        mine = self.gdn_state(layer)
+        rep = self.cfg.linear_key_repeat
+        for key, value in st.items():
+            value = value.to(self.device)
+            if key == "pending_key_state":
+                value = value[:, :, ::rep]
+            mine[key].copy_(value)
+
+
+def _dev(t: torch.Tensor, dtype: torch.dtype, device) -> torch.Tensor:
+    return t.to(device=device, dtype=dtype, non_blocking=True).contiguous()
+
+
+class VerifyStep:
+    """The verify graph over the engine's B rows and K tokens per row."""
+
+    def __init__(self, engine: Engine):
+        self.engine = engine
+
+    def __call__(self, inputs_embeds: torch.Tensor, **inputs: torch.Tensor) -> torch.Tensor:
+        e = self.engine
+        if "accepted" not in inputs:
+            raise NotImplementedError("only the verify form (inputs with `accepted`) runs on this build")
+        b, k, h = e.batch_size, e.verify_tokens, e.cfg.hidden_size
+        if tuple(inputs_embeds.shape) != (b, k, h):
+            raise ValueError(f"inputs_embeds must be [{b}, {k}, {h}], got {list(inputs_embeds.shape)}")
+        dev = e.device
+        out = torch.empty(b, k, h, dtype=DTYPE, device=dev)
+        e.handle.verify(
+            _dev(inputs_embeds, DTYPE, dev), _dev(inputs["cos"], DTYPE, dev), _dev(inputs["sin"], DTYPE, dev),
+            _dev(inputs["position"], torch.int32, dev), _dev(inputs["active"], torch.float32, dev),
+            _dev(inputs["accepted"], torch.int32, dev), out,
+        )
+        return out
+
+
+class MTPStep:
+    """The MTP drafter's step form over [B, K] rows and tokens."""
+
+    def __init__(self, engine: Engine):
+        if not engine.mtp:
+            raise ValueError("the engine was built without the MTP layer")
+        self.engine = engine
+
+    def __call__(self, hidden: torch.Tensor, inputs_embeds: torch.Tensor, **inputs: torch.Tensor) -> torch.Tensor:
+        e = self.engine
+        if "slot" in inputs:
+            raise NotImplementedError("the MTP prefill form is not part of the verify path")
+        b, k, h = e.batch_size, e.verify_tokens, e.cfg.hidden_size
+        for name, t in (("hidden", hidden), ("inputs_embeds", inputs_embeds)):
+            if tuple(t.shape) != (b, k, h):
+                raise ValueError(f"{name} must be [{b}, {k}, {h}], got {list(t.shape)}")
+        dev = e.device
+        out = torch.empty(b, k, h, dtype=DTYPE, device=dev)
+        e.handle.mtp_step(
+            _dev(hidden, DTYPE, dev), _dev(inputs_embeds, DTYPE, dev), _dev(inputs["cos"], DTYPE, dev),
+            _dev(inputs["sin"], DTYPE, dev), _dev(inputs["position"], torch.int32, dev),
+            _dev(inputs["active"], torch.float32, dev), out,
+        )
+        return out
+
+
+class HeadGraph:
+    """The head: group maxima, the exact top-group recheck and embedding rows, all on the GPU."""
+
+    def __init__(self, engine: Engine, group_rows: int = 32):
+        if group_rows != 32:
+            raise ValueError("the head's groups are 32 rows (one weight tile)")
+        self.engine = engine
+        self.batch_size = engine.batch_size * engine.verify_tokens
+
+    def _rows(self, hidden: torch.Tensor) -> torch.Tensor:
+        e = self.engine
+        rows = hidden.reshape(-1, e.cfg.hidden_size)
+        if rows.shape[0] > self.batch_size:
+            raise ValueError(f"the head takes at most {self.batch_size} rows, got {rows.shape[0]}")
+        return _dev(rows, DTYPE, e.device)
+
+    def __call__(self, hidden: torch.Tensor) -> torch.Tensor:
+        rows = self._rows(hidden)
+        maxima = torch.empty(rows.shape[0], self.engine.cfg.vocab_size // 32, dtype=torch.float32, device=rows.device)
+        self.engine.handle.head_groupmax(rows, rows.shape[0], maxima)
+        return maxima
+
+    def pick(self, hidden: torch.Tensor, groups: int) -> torch.Tensor:
+        """Greedy token per row (`ChipHead.next_tokens`); raises FloatingPointError for a row with no finite logit."""
+        rows = self._rows(hidden)
+        ids = torch.empty(rows.shape[0], dtype=torch.int32, device=rows.device)
+        self.engine.handle.head_pick(rows, rows.shape[0], groups, ids)
+        ids = ids.cpu()
+        bad = (ids < 0).nonzero()
+        if len(bad):
+            raise FloatingPointError(f"row {int(bad[0])}'s logits are not finite, so the graph produced NaN or infinity")
+        return ids
+
+    def embed(self, token_ids) -> torch.Tensor:
+        e = self.engine
+        ids = torch.as_tensor(list(token_ids), dtype=torch.int32)
+        if len(ids) and (int(ids.min()) < 0 or int(ids.max()) >= e.cfg.vocab_size):
+            raise ValueError(f"token ids must be in [0, {e.cfg.vocab_size})")
+        out = torch.empty(len(ids), e.cfg.hidden_size, dtype=DTYPE, device=e.device)
+        if len(ids):
+            e.handle.embed(ids.to(e.device), len(ids), out)
+        return out

@@ -1,0 +1,71 @@
+"""FP8 projection kernel (scaled MFMA, packed e4m3 + E8M0 weights, e5m2 activation tiles) against the CPU oracle's
+`linear_fp8` (reference FP8Linear.forward, qwen38_inf2/model.py:221-225)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import model as om
+from qwen38_amd import ext
+from qwen38_amd.quant import dequantize_e4m3, quantize_e4m3, round_e5m2
+
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    mag = x.float().abs().clamp_min(2.0**-126)
+    return torch.pow(2.0, torch.floor(torch.log2(mag)) - 7)
+
+
+@pytest.mark.gpu
+def test_activation_rounding_to_e5m2_matches_torch_for_every_bf16_value(gpu):
+    """Identity weights (e4m3 1.0, scale 2^0) make the GEMM return its e5m2-rounded input: every finite bf16 value
+    whose e5m2 rounding is finite, against torch's cast (the reference's fp8_round)."""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits.clone()
+    bad = ~torch.isfinite(x.float()) | (x.float().abs() >= 61440)
+    x[bad] = 0
+    x = x.reshape(256, 256)
+    coded = torch.zeros(256, 256, dtype=torch.uint8)
+    coded[torch.arange(256), torch.arange(256)] = 0x38
+    scales = torch.full((256, 8), 127, dtype=torch.uint8)
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    got = ext.fp8_linear(x.cuda(), tiles, words, 256).cpu()
+    want = x.to(torch.float8_e5m2).to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)) or torch.equal(got.float(), want.float())
+
+
+@pytest.mark.gpu
+def test_each_mx_block_is_scaled_by_its_own_e8m0_scale(gpu):
+    """All-ones weights whose block b (of 32 inputs) has scale 2^b, against one-hot activations: the output for
+    input k must be 2^(k // 32), so every input sits in the MX block whose scale the hardware applies to it."""
+    n, k = 256, 256
+    coded = torch.full((n, k), 0x38, dtype=torch.uint8)
+    scales = (127 + torch.arange(k // 32)).to(torch.uint8).repeat(n, 1)
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    x = torch.eye(k, dtype=torch.bfloat16)
+    got = ext.fp8_linear(x.cuda(), tiles, words, n).cpu().float()
+    want = torch.pow(2.0, (torch.arange(k) // 32).float()).unsqueeze(1).expand(k, n)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,k,n", [(16, 1024, 512), (64, 5120, 256), (128, 2048, 768), (256, 1024, 1024), (300, 512, 256)])
+def test_fp8_linear_matches_the_oracle_within_rounding_and_accumulation_error(gpu, rows, k, n):
+    print(f"fp8_linear rows={rows} k={k} n={n}", flush=True)
+    g = torch.Generator().manual_seed(rows * 7 + k + n)
+    w = torch.randn(n, k, generator=g) * 0.02
+    w[:, :32] *= 50.0  # groups with different scales
+    coded, scales = quantize_e4m3(w)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    want = om.linear_fp8(x, om.FP8Weight(coded, scales))
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    got = ext.fp8_linear(x.cuda(), tiles, words, n).cpu()
+    # Error bound: bf16 rounding of the result plus the scaled MFMA's accumulation error. On gfx950 that error reaches
+    # about 2^-16 of the sum of |x * w| (measured: it moves a few fp32 sums across a bf16 rounding midpoint); the bound
+    # allows 2^-14. The CPU oracle rounds the exact sum correctly at these sizes.
+    xq, wd = round_e5m2(x).double(), dequantize_e4m3(coded, scales).double()
+    exact = xq @ wd.T
+    abs_sum = xq.abs() @ wd.abs().T
+    err = (got.double() - exact).abs()
+    assert (err <= 0.5 * bf16_ulp(exact) + 2.0**-14 * abs_sum).all(), float((err / abs_sum).max())
+    assert (got.float() == want.float()).float().mean() > 0.98
