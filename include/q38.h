@@ -87,13 +87,13 @@ int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, u
 
 /* A standalone FP8 projection, `FP8Linear.forward` (reference model.py:211-229): x bf16 [rows][k] rounded to e5m2,
  * times the packed weight ([n][k] e4m3 + E8M0), float32 sums, bf16 out [rows][n]. act_scratch holds
- * q38_fp8_linear_scratch(rows, k) bytes. n % 256 == 0, k % 256 == 0. */
+ * q38_fp8_linear_scratch(rows, k) bytes (the e5m2-rounded input as bf16 tiles). n % 256 == 0, k % 256 == 0. */
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                   uint8_t* act_scratch, uint16_t* out, void* stream);
+                   uint16_t* act_scratch, uint16_t* out, void* stream);
 size_t q38_fp8_linear_scratch(int rows, int k);
 /* The same with float32 output [rows][n] (no bf16 rounding); rows in {32, 64, 128} or a multiple of 256. */
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                       uint8_t* act_scratch, float* out, void* stream);
+                       uint16_t* act_scratch, float* out, void* stream);
 
 /* One verify step over all B rows: embeds bf16 [B][K][H]; cos, sin bf16 [B][K][rotary_dim]; position int32 [B];
  * active f32 [B]; accepted int32 [B]. Writes the last layer's hidden state bf16 [B][K][H] (before the final norm),

@@ -4,13 +4,13 @@
 // bf16: every bf16 result is fp32 rounded to nearest even, and activations are rounded to FP8 e5m2 at each
 // projection input (model.py:85-87, 222-225).
 //
-// Activation tiles. Every FP8 (and the head's bf16) GEMM reads its activations in the layout the MFMA operand wants,
-// written that way by the kernel that produced them. One K-step of 64 inputs for 32 tokens is a 2 KiB tile; lane l
-// holds 32 bytes of token l % 32 from lane half h = l / 32, in the order v_mfma_scale_f32_32x32x64_f8f6f4 reads them:
-//     byte i of lane half h  <->  input k = 32 * (i / 16) + 16 * h + i % 16  (within the K-step)
-// (bytes 0-15 of both halves form the step's first 32-input MX block, whose E8M0 scale lane half 0 supplies; bytes
-// 16-31 the second, scaled by lane half 1; measured on gfx950). Weights use the same layout with output features in
-// place of tokens (pack.hip).
+// Tiles. Every GEMM reads its operands in the layout the MFMA wants, written that way by the kernel that produced
+// them. One K-step of 64 inputs for 32 tokens (or 32 weight rows) is one tile; lane l holds 32 elements of token
+// (row) l % 32 from lane half h = l / 32, in the order of v_mfma_scale_f32_32x32x64_f8f6f4's operands:
+//     element i of lane half h  <->  input k = 32 * (i / 16) + 16 * h + i % 16  (within the K-step)
+// (for FP8 weights, bytes 0-15 of both halves form the step's first 32-input MX block, whose E8M0 scale lane half 0
+// holds, and bytes 16-31 the second, scaled by lane half 1; measured on gfx950). Weight tiles are FP8 bytes (2 KiB,
+// pack.hip); activation tiles are bf16 (4 KiB) holding e5m2-rounded values, or plain bf16 for the head.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,19 +38,18 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
 // Round to bf16 and back: the value a torch bf16 op stores.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
-// FP8 e5m2 code of x, round to nearest even, overflow past 57344 to infinity (torch's non-saturating cast).
-__device__ __forceinline__ uint32_t f2e5m2(float x) {
+// x rounded to FP8 e5m2 and back (torch's cast: round to nearest even, past 57344 to infinity), as a float.
+__device__ __forceinline__ float e5m2_round(float x) {
     uint32_t u = __float_as_uint(x);
-    uint32_t s = (u >> 24) & 0x80u;
+    uint32_t s = u & 0x80000000u;
     uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return s | 0x7fu;
+    if (a > 0x7f800000u) return x;
     if (a >= 0x38800000u) {  // |x| >= 2^-14: normal e5m2, keep 2 mantissa bits
         uint32_t r = (a + 0xfffffu + ((a >> 21) & 1u)) & ~0x1fffffu;
-        if (r > 0x47600000u) return s | 0x7cu;
-        return s | ((((r >> 23) - 112u) << 2) | ((r >> 21) & 3u));
+        return __uint_as_float(s | (r > 0x47600000u ? 0x7f800000u : r));
     }
-    // Subnormal e5m2: multiples of 2^-16. 4 units is the smallest normal, whose code is also 4.
-    return s | (uint32_t)__builtin_rintf(__uint_as_float(a) * 65536.0f);
+    // Subnormal e5m2: multiples of 2^-16.
+    return __uint_as_float(s | __float_as_uint(__builtin_rintf(__uint_as_float(a) * 65536.0f) * (1.0f / 65536.0f)));
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -62,8 +61,8 @@ __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : lo
 Q38_HOST_DEVICE int kstep_half(int k) { return (k & 31) >> 4; }
 Q38_HOST_DEVICE int kstep_byte(int k) { return ((k & 63) >> 5) * 16 + (k & 15); }
 
-// Element offset of (t, k) in a tile buffer with K inputs (K a multiple of 64): bytes for e5m2 tiles, bf16 elements
-// for the head's bf16 tiles. Four consecutive k from a multiple of 4 are contiguous.
+// Element offset of (t, k) in a tile buffer with K inputs (K a multiple of 64). Four consecutive k from a multiple of 4
+// are contiguous.
 Q38_HOST_DEVICE size_t act_offset(int t, int k, int K) {
     return ((size_t)(t >> 5) * (K >> 6) + (k >> 6)) * 2048 + (size_t)(((t & 31) + kstep_half(k) * 32) * 32) + kstep_byte(k);
 }

@@ -145,7 +145,7 @@ int choose_splits(const q38_handle* h, int N, int K) {
     return best;
 }
 
-int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint8_t* act, int K, int N, int epi,
+int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint16_t* act, int K, int N, int epi,
          void* out0, int ld0, int n0, void* out1, int ld1, hipStream_t stream, int* splits_out = nullptr) {
     if (N % 256 || K % 256) return fail("GEMM shape N=" + std::to_string(N) + " K=" + std::to_string(K) + " not tileable");
     GemmArgs a{};
@@ -156,7 +156,6 @@ int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint
     a.N = N;
     a.T = h->T;
     a.Tpad = h->Tpad;
-    a.unit_scale = 127;
     a.out0 = out0;
     a.ld0 = ld0;
     a.n0 = n0;
@@ -169,13 +168,13 @@ int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint
     }
     a.ksteps = K / 64 / splits;
     if (a.ksteps % 2) return fail("GEMM K-steps per split must be even");
-    HIP_TRY(q38_gemm_fp8(a, epi, splits, stream));
+    HIP_TRY(q38_gemm(a, epi, splits, stream));
     if (splits_out) *splits_out = splits;
     return 0;
 }
 
 int norm_rows(q38_handle* h, const float* part, int splits, const uint16_t* xin, const uint16_t* resid, uint16_t* xout,
-              const uint16_t* w, uint8_t* act, int kact, int col0, uint16_t* hout, const uint16_t* div_w, hipStream_t stream) {
+              const uint16_t* w, uint16_t* act, int kact, int col0, uint16_t* hout, const uint16_t* div_w, hipStream_t stream) {
     NormArgs a{};
     a.part = part;
     a.splits = splits;
@@ -208,8 +207,8 @@ struct StepIO {
 int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream_t stream) {
     bool ok = true;
     const int H = h->H;
-    uint8_t* act_h = h->ws(h->off_act_h);
-    uint8_t* act_mid = h->ws(h->off_act_mid);
+    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
+    uint16_t* act_mid = (uint16_t*)h->ws(h->off_act_mid);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     int splits, kmid;
     const uint8_t* otiles;
@@ -334,8 +333,8 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     auto dn_t = get<uint8_t>(h, "mlp.down.tiles", li, &ok);
     auto dn_s = get<uint32_t>(h, "mlp.down.scales", li, &ok);
     if (!ok) return 1;
-    uint8_t* act_h = h->ws(h->off_act_h);
-    uint8_t* act_ffn = h->ws(h->off_act_ffn);
+    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
+    uint16_t* act_ffn = (uint16_t*)h->ws(h->off_act_ffn);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     if (gemm(h, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
     int splits = 0;
@@ -415,9 +414,9 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_x = take(Tp * H * 2);
     h->off_hbf = take(Tp * H * 2);
     h->off_tmp = take(Tp * H * 2);
-    h->off_act_h = take(Tp * h->act_h_k);
-    h->off_act_mid = take(Tp * mid);
-    h->off_act_ffn = take(Tp * h->I);
+    h->off_act_h = take(Tp * h->act_h_k * 2);
+    h->off_act_mid = take(Tp * mid * 2);
+    h->off_act_ffn = take(Tp * h->I * 2);
     h->off_z = take(Tp * h->Hv * h->dk * 2);
     h->off_qkv = take(Tp * nqkv * 2);
     h->off_beta = take(Tp * h->Hv * 4);
@@ -478,11 +477,10 @@ int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, u
 }
 
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                   uint8_t* act_scratch, uint16_t* out, void* stream_) {
+                   uint16_t* act_scratch, uint16_t* out, void* stream_) {
     if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
     if (rows < 1 || n % 256 || k % 256) return fail("fp8_linear needs rows >= 1, N % 256 == 0 and K % 256 == 0");
     hipStream_t stream = (hipStream_t)stream_;
-    const int tpad = pad_tokens(rows);
     HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
     GemmArgs a{};
     a.w = tiles;
@@ -491,26 +489,23 @@ int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, con
     a.K = k;
     a.N = n;
     a.T = rows;
-    a.Tpad = tpad;
+    a.Tpad = pad_tokens(rows);
     a.ksteps = k / 64;
-    a.unit_scale = 127;
     a.out0 = out;
     a.ld0 = n;
     a.n0 = n;
-    HIP_TRY(q38_gemm_fp8(a, EPI_BF16, 1, stream));
+    HIP_TRY(q38_gemm(a, EPI_BF16, 1, stream));
     return 0;
 }
 
-size_t q38_fp8_linear_scratch(int rows, int k) { return (size_t)pad_tokens(rows) * k; }
+size_t q38_fp8_linear_scratch(int rows, int k) { return (size_t)pad_tokens(rows) * k * 2; }
 
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                       uint8_t* act_scratch, float* out, void* stream_) {
+                       uint16_t* act_scratch, float* out, void* stream_) {
     if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
-    if (rows < 1 || rows % 32 || n % 256 || k % 256)
-        return fail("fp8_linear_f32 needs rows % 32 == 0, N % 256 == 0 and K % 256 == 0");
+    if (rows < 1 || n % 256 || k % 256) return fail("fp8_linear_f32 needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+    if (pad_tokens(rows) != rows) return fail("fp8_linear_f32 needs rows in {32, 64, 128} or a multiple of 256");
     hipStream_t stream = (hipStream_t)stream_;
-    const int tpad = pad_tokens(rows);
-    if (tpad != rows) return fail("fp8_linear_f32 needs rows in {32, 64, 128} or a multiple of 256");
     HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
     GemmArgs a{};
     a.w = tiles;
@@ -519,11 +514,10 @@ int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles,
     a.K = k;
     a.N = n;
     a.T = rows;
-    a.Tpad = tpad;
+    a.Tpad = rows;
     a.ksteps = k / 64;
-    a.unit_scale = 127;
     a.part = out;
-    HIP_TRY(q38_gemm_fp8(a, EPI_PARTIAL, 1, stream));
+    HIP_TRY(q38_gemm(a, EPI_PARTIAL, 1, stream));
     return 0;
 }
 
@@ -538,7 +532,7 @@ int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const
     const int L = h->cfg.num_layers, rd = h->parity, wr = 1 - h->parity;
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     uint16_t* hbf = is_linear(h, 0) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
-    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, (uint16_t*)h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
     StepIO io{cos, sin, position, active, accepted};
     for (int li = 0; li < L; ++li) {
         if (run_mixer(h, li, io, rd, wr, stream)) return 1;
@@ -563,7 +557,7 @@ int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, 
     auto fc_s = get<uint32_t>(h, "mtp.fc.scales", M, &ok);
     auto in0 = get<uint16_t>(h, "input_layernorm", M, &ok);
     if (!ok) return 1;
-    uint8_t* act_h = h->ws(h->off_act_h);
+    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
     uint16_t* tmp = (uint16_t*)h->ws(h->off_tmp);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     // [rms(embeds) | rms(rms(hidden, final norm), hidden norm)] as the fc's 2H-wide e5m2 input (model.py:845-851).
@@ -591,16 +585,17 @@ int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* ma
     if (!ok) return 1;
     HIP_TRY(q38_head_norm(hidden, nw, h->cfg.rms_norm_eps, h->H, rows, (bf16_t*)h->ws(h->off_htiles),
                           (float*)h->ws(h->off_x32), stream));
-    HeadArgs a{};
+    GemmArgs a{};
     a.w = wt;
     a.ws = wsc;
     a.act = (const bf16_t*)h->ws(h->off_htiles);
     a.K = h->H;
-    a.V = h->V;
-    a.R = rows;
-    a.Rpad = pad_tokens(rows);
-    a.maxima = maxima;
-    HIP_TRY(q38_head_groupmax(a, stream));
+    a.N = h->V;
+    a.T = rows;
+    a.Tpad = pad_tokens(rows);
+    a.ksteps = h->H / 64;
+    a.part = maxima;
+    HIP_TRY(q38_gemm(a, EPI_GROUPMAX, 1, stream));
     return 0;
 }
 

@@ -3,28 +3,19 @@
 
 #include "common.h"
 
-enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2 };
+enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2, EPI_GROUPMAX = 3 };
 
 struct GemmArgs {
-    const uint8_t* w;    // weight tiles [N/32][K/64][64][32]
-    const uint32_t* ws;  // scale words [N/32][K/256][64]: byte j of a lane's word is K-step 4q+j
-    const uint8_t* act;  // activation tiles [Tpad/32][K/64][64][32]
+    const uint8_t* w;    // weight tiles [N/32][K/64][64][32] (e4m3)
+    const uint32_t* ws;  // scale words [N/32][K/256][64]: byte j of lane half h's word scales MX block h of K-step 4q+j
+    const bf16_t* act;   // activation tiles [Tpad/32][K/64][64][32] (bf16)
     int K, N, T, Tpad;
-    int ksteps;          // K-steps of 64 per split (even)
-    int unit_scale;      // 127: E8M0 of 1.0 for the activations, passed at run time
+    int ksteps;          // K-steps of 64 per split
     void* out0;
     int ld0, n0;
     void* out1;
     int ld1;
-    float* part;
-};
-
-struct HeadArgs {
-    const uint8_t* w;
-    const uint32_t* ws;
-    const bf16_t* act;
-    int K, V, R, Rpad;
-    float* maxima;       // [R][V/32]
+    float* part;         // EPI_PARTIAL: [split][Tpad][N]; EPI_GROUPMAX: maxima [T][N/32]
 };
 
 struct NormArgs {
@@ -35,7 +26,7 @@ struct NormArgs {
     bf16_t* xout;          // x_new (may alias resid), or null
     const bf16_t* w;       // norm weight, used as (1 + w)
     float eps;
-    uint8_t* act;          // e5m2 tiles of width Kact at column act_col0, or null
+    bf16_t* act;           // activation tiles (e5m2 values) of width Kact at column act_col0, or null
     int Kact, act_col0;
     bf16_t* hout;          // bf16 normed rows [T][H], or null
     const bf16_t* div_w;   // MTP tail: hout = bf16(normed / (1 + div_w))
@@ -75,7 +66,7 @@ struct GdnArgs {
     float* delta_new;
     const float* decay_old;  // [B][K][Hv]
     float* decay_new;
-    uint8_t* act;            // e5m2 tiles of width Hv*128 for out_proj
+    bf16_t* act;             // activation tiles (e5m2 values) of width Hv*128 for out_proj
     float eps;
 };
 
@@ -93,7 +84,7 @@ struct AttnArgs {
     bf16_t* v_cache;
     float* scores;          // [B*Hkv][64][S]
     bf16_t* weights;        // [B*Hkv][64][S]
-    uint8_t* act;           // e5m2 tiles of width Hq*256 for o_proj
+    bf16_t* act;            // activation tiles (e5m2 values) of width Hq*256 for o_proj
     float eps;
 };
 
@@ -107,8 +98,7 @@ struct PickArgs {
     int* ids;              // [R]
 };
 
-hipError_t q38_gemm_fp8(const GemmArgs& a, int epi, int splits, hipStream_t stream);
-hipError_t q38_head_groupmax(const HeadArgs& a, hipStream_t stream);
+hipError_t q38_gemm(const GemmArgs& a, int epi, int splits, hipStream_t stream);
 hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream);
 hipError_t q38_head_norm(const bf16_t* hidden, const bf16_t* w, float eps, int H, int rows, bf16_t* tiles, float* x32,
                          hipStream_t stream);
@@ -121,4 +111,4 @@ hipError_t q38_accept(const int* picks, const int* drafts, const float* active, 
                       hipStream_t stream);
 hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint32_t* words,
                     hipStream_t stream);
-hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);
+hipError_t q38_act_tiles(const bf16_t* x, int T, int K, bf16_t* act, hipStream_t stream);

@@ -1,5 +1,5 @@
-"""FP8 projection kernel (scaled MFMA, packed e4m3 + E8M0 weights, e5m2 activation tiles) against the CPU oracle's
-`linear_fp8` (reference FP8Linear.forward, qwen38_inf2/model.py:221-225)."""
+"""FP8 projection kernel (packed e4m3 + E8M0 weights widened to bf16 in registers, bf16 MFMA, e5m2-rounded activation
+tiles) against the CPU oracle's `linear_fp8` (reference FP8Linear.forward, qwen38_inf2/model.py:221-225)."""
 
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
 
 @pytest.mark.gpu
 def test_activation_rounding_to_e5m2_matches_torch_for_every_bf16_value(gpu):
-    """Identity weights (e4m3 1.0, scale 2^0) make the GEMM return its e5m2-rounded input: every finite bf16 value
+    """Identity weights (e4m3 1.0, scale 2^0) make the projection return its e5m2-rounded input: every finite bf16 value
     whose e5m2 rounding is finite, against torch's cast (the reference's fp8_round)."""
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     x = bits.clone()
@@ -60,12 +60,12 @@ def test_fp8_linear_matches_the_oracle_within_rounding_and_accumulation_error(gp
     want = om.linear_fp8(x, om.FP8Weight(coded, scales))
     tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
     got = ext.fp8_linear(x.cuda(), tiles, words, n).cpu()
-    # Error bound: bf16 rounding of the result plus the scaled MFMA's accumulation error. On gfx950 that error reaches
-    # about 2^-16 of the sum of |x * w| (measured: it moves a few fp32 sums across a bf16 rounding midpoint); the bound
-    # allows 2^-14. The CPU oracle rounds the exact sum correctly at these sizes.
+    # Error bound: bf16 rounding of the result plus float32 accumulation error (the bf16 MFMA's sums are float32-grade:
+    # about 1e-8 of the sum of |x * w|, measured); the bound allows 2^-20. Outputs then differ from the CPU oracle only
+    # where one of the two float32 sums lands across a bf16 rounding midpoint.
     xq, wd = round_e5m2(x).double(), dequantize_e4m3(coded, scales).double()
     exact = xq @ wd.T
     abs_sum = xq.abs() @ wd.abs().T
     err = (got.double() - exact).abs()
-    assert (err <= 0.5 * bf16_ulp(exact) + 2.0**-14 * abs_sum).all(), float((err / abs_sum).max())
-    assert (got.float() == want.float()).float().mean() > 0.98
+    assert (err <= 0.5 * bf16_ulp(exact) + 2.0**-20 * abs_sum).all(), float((err / abs_sum).max())
+    assert (got.float() == want.float()).float().mean() > 0.999
