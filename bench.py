@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""Benchmark of the MTP speculative-decoding verify step on one MI355X.
+
+One step = the reference's Scheduler._verify_step with MTP drafts (qwen38_inf2/scheduler.py:160-193, 269-301) for
+all 64 rows: 3 MTP calls and 3 one-group head passes to draft 3 tokens per row, the 64-layer verify of 4 tokens per
+row (512-token contexts), the head's group maxima and exact top-4-group recheck over 256 rows, greedy acceptance and
+the state advance. It runs as one library call, `q38_spec_step`, on torch's current HIP stream; inputs and state are
+resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
+checkpoint.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+
+prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
+its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
+the SwiGLU epilogue, 2 x 17408 x 5120 FP8 weights against 256 tokens), timed with HIP events on the stream it runs on.
+`step_roofline` is the whole step's algorithmic HBM bytes over its time. `cpu_baseline` is the CPU oracle (this
+repository's restatement of the reference's CPU path) on a bounded sample: one 27B block (3 gated-delta + 1 attention
+layer) of the verify at the same B, K and context, scaled x16 to 64 layers, without the MTP and head passes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "qwen38-27b-aws_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def fp8_bytes(n: int, k: int) -> int:
+    return n * k + n * k // 32
+
+
+def algorithmic_bytes(cfg, batch: int, tokens: int, context: int) -> dict:
+    """Compulsory HBM bytes of one step, each counted once: FP8 weights + E8M0 scales of every projection streamed,
+    bf16 small weights, gated-delta state and conv state read + written, KV read over each row's context plus the
+    step's own K/V written, the head read once per pass plus the recheck rows, the MTP layer per call, inputs/outputs."""
+    h, inter, v = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    hv, hk, d, c = cfg.linear_num_value_heads, cfg.linear_num_key_heads, cfg.linear_key_head_dim, cfg.linear_conv_dim
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    t = batch * tokens
+    mlp = fp8_bytes(2 * inter, h) + fp8_bytes(h, inter)
+    gdn_w = fp8_bytes(c + hv * d, h) + fp8_bytes(h, hv * d) + mlp + 2 * hv * h * 2 + c * 4 * 2
+    attn_w = fp8_bytes(hq * hd * 2 + 2 * hkv * hd, h) + fp8_bytes(h, hq * hd) + mlp
+    n_gdn = sum(1 for k in cfg.layer_types if k == "linear_attention")
+    n_attn = cfg.num_hidden_layers - n_gdn
+    weights = n_gdn * gdn_w + n_attn * attn_w
+    state = n_gdn * batch * (hv * d * d * 2 * 2 + c * 3 * 2 * 2)
+    kv_read = batch * hkv * context * hd * 2 * 2
+    kv = n_attn * (kv_read + t * hkv * hd * 2 * 2)
+    io = t * h * 2 * 2
+    head_pass = fp8_bytes(v, h)
+    head = 4 * head_pass + (t * 4 + 3 * batch) * 32 * (h + h // 32)
+    mtp_w = fp8_bytes(h, 2 * h) + attn_w
+    mtp = 3 * (mtp_w + kv_read + t * hkv * hd * 2 * 2 + 3 * t * h * 2)
+    total = weights + state + kv + io + head + mtp
+    return {"total": total, "weights": weights, "state": state, "kv": kv, "head": head, "mtp": mtp, "io": io}
+
+
+def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int):
+    import torch
+
+    from qwen38_amd import synth
+    from qwen38_amd.generate import rope_table
+    from qwen38_amd.steps import Engine
+
+    dev = "cuda"
+    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev)
+    started = time.time()
+    specs = synth.model_specs(cfg, mtp=True, head=True)
+
+    def weights():
+        for n, spec in enumerate(specs):
+            if n % 100 == 0:
+                log(f"weights {n}/{len(specs)} ({time.time() - started:.0f}s)")
+            yield spec.name, synth.make(spec, seed, dev)
+
+    engine.load(weights())
+    ctx = [context] * batch
+    for i, kind in enumerate(cfg.layer_types):
+        if kind == "linear_attention":
+            engine.set_gdn(i, synth.gdn_states(cfg, batch, tokens, seed, f"state.{i}", dev))
+        else:
+            kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, f"kv.{i}", dev)
+            engine.set_kv(i, kv["k_cache"], kv["v_cache"])
+    kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, "kv.mtp", dev)
+    engine.set_kv(engine.mtp_layer, kv["k_cache"], kv["v_cache"])
+    engine.bind("rope_table", -1, rope_table(cfg, max_seq_len))
+    torch.cuda.synchronize()
+    log(f"model and state ready in {time.time() - started:.0f}s")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    state = {
+        "position": torch.full((batch,), context, dtype=torch.int32, device=dev),
+        "index": torch.full((batch,), context - 1, dtype=torch.int32, device=dev),
+        "match": torch.zeros(batch, dtype=torch.int32, device=dev),
+        "accepted": torch.ones(batch, dtype=torch.int32, device=dev),
+        "active": torch.ones(batch, dtype=torch.float32, device=dev),
+        "hidden": synth.hidden_states((batch, tokens, cfg.hidden_size), seed, "bench.hidden", dev),
+        "picks": torch.randint(0, cfg.vocab_size, (batch, tokens), generator=g, device=dev, dtype=torch.int32),
+        "drafts": torch.zeros(batch, tokens - 1, dtype=torch.int32, device=dev),
+    }
+    return engine, state
+
+
+def time_dominant_kernel(engine, cfg, rows: int, reps: int = 20) -> float:
+    """Average duration (ms) of the MLP gate/up projection on layer 0's weights, HIP events on the current stream."""
+    import torch
+
+    from qwen38_amd import ext
+
+    x = torch.randn(rows, cfg.hidden_size, device="cuda").to(torch.bfloat16)
+    tiles, words = engine.buffer("mlp.gate_up.tiles", 0), engine.buffer("mlp.gate_up.scales", 0)
+    lib = ext.library()
+    scratch = torch.empty(lib.q38_tiles_size(rows, cfg.hidden_size), dtype=torch.uint8, device="cuda")
+    out = torch.empty(lib.q38_tiles_size(rows, cfg.intermediate_size), dtype=torch.uint8, device="cuda")
+    for _ in range(3):
+        ext.mlp_up(x, tiles, words, cfg.intermediate_size, scratch, out)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        ext.mlp_up(x, tiles, words, cfg.intermediate_size, scratch, out)
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(cfg_block, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, accepted_per_step: float,
+                 n_blocks: int) -> dict:
+    """The CPU oracle on one block of the same verify (bf16, all host threads), timed once after one warm-up."""
+    import torch
+
+    from oracle import model as om
+    from qwen38_amd import synth
+    from qwen38_amd.generate import verify_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    values = {}
+    for spec in synth.model_specs(cfg_block, mtp=False, head=False):
+        v = synth.make(spec, seed, "cuda")
+        values[spec.name] = tuple(x.cpu() for x in v) if isinstance(v, tuple) else v.cpu()
+    layers = []
+    for i in range(cfg_block.num_hidden_layers):
+        prefix = f"layers.{i}."
+        layers.append({n[len(prefix):]: (om.FP8Weight(*v) if isinstance(v, tuple) else v) for n, v in values.items() if n.startswith(prefix)})
+    states = []
+    for i, kind in enumerate(cfg_block.layer_types):
+        if kind == "linear_attention":
+            states.append({k: v.cpu() for k, v in synth.gdn_states(cfg_block, batch, tokens, seed, f"cpu.{i}", "cuda").items()})
+        else:
+            states.append({k: v.cpu() for k, v in synth.kv_states(cfg_block, batch, max_seq_len, [context] * batch, seed, f"cpu.{i}", "cuda").items()})
+    x = synth.hidden_states((batch, tokens, cfg_block.hidden_size), seed, "cpu.x")
+    inp = verify_inputs(cfg_block, [context] * batch, tokens, max_seq_len, torch.bfloat16, [True] * batch, [1] * batch)
+    times = []
+    for _ in range(2):
+        started = time.perf_counter()
+        om.step_verify(cfg_block, layers, states, x, inp["cos"], inp["sin"], inp["position"], inp["active"], inp["accepted"])
+        times.append(time.perf_counter() - started)
+        log(f"cpu block {times[-1]:.2f}s")
+    step = times[-1] * n_blocks
+    cpu_name = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": accepted_per_step / step,
+        "unit": "accepted tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one block (3 gated-delta + 1 attention layer) of the B={batch}, K={tokens}, context-{context} verify "
+        f"on the CPU oracle in bf16 ({times[-1]:.2f} s after one warm-up), x{n_blocks} for 64 layers; MTP and head "
+        f"passes not included; host {cpu_name}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (rows shard across GPUs with no exchange); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from qwen38_amd.config import qwen38_27b_config
+
+    batch, tokens, context, max_seq_len, seed = 64, 4, 512, 1024, args.seed
+    cfg = qwen38_27b_config(16)
+    log(f"device {torch.cuda.get_device_name(0)}")
+    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed)
+
+    def step():
+        engine.handle.spec_step(st["position"], st["index"], st["match"], st["accepted"], st["active"], st["hidden"],
+                                st["picks"], st["drafts"])
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+    start_pos = st["position"].clone()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    accepted = int((st["position"] - start_pos).sum())
+    value = accepted / (ms * args.steps / 1000.0)
+    log(f"{ms:.3f} ms/step, {accepted} accepted tokens over {args.steps} steps")
+
+    kernel_ms = time_dominant_kernel(engine, cfg, batch * tokens)
+    flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
+    achieved = flops / (kernel_ms / 1000.0) / 1e12
+    alg = algorithmic_bytes(cfg, batch, tokens, context)
+    step_gbs = alg["total"] / (ms / 1000.0) / 1e9
+    result = {
+        "metric": "accepted tokens/s/GPU, 64-layer verify step, batch 64, 4 tokens; HBM GB/s %peak",
+        "value": round(value, 2),
+        "unit": "accepted tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
+        "config": {
+            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)",
+            "global_batch": batch,
+            "tokens_per_row": tokens,
+            "context": context,
+            "parallelism": "none (one GPU)",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_kernel<2,2,2,4,SWIGLU> (MLP gate/up, 256 x 34816 x 5120)",
+            "achieved": round(achieved, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_ms": round(kernel_ms, 4),
+        },
+        "step_roofline": {
+            "bound": "hbm",
+            "achieved": round(step_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_step": alg["total"],
+        },
+        "accepted_per_step": accepted / args.steps,
+    }
+    if not args.no_cpu_baseline:
+        from qwen38_amd.config import qwen38_27b_config as big
+
+        del engine
+        torch.cuda.empty_cache()
+        result["cpu_baseline"] = cpu_baseline(big(1), batch, tokens, max_seq_len, context, seed, accepted / args.steps, 16)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -65,7 +65,8 @@ void q38_destroy(q38_handle* h);
  *   attention layers and the MTP layer: self_attn.qkv.{tiles,scales} (q_proj, k_proj, v_proj rows),
  *     self_attn.o_proj.{tiles,scales}, self_attn.q_norm, self_attn.k_norm (bf16 [head_dim])
  *   MTP layer only: mtp.fc.{tiles,scales}, mtp.embedding_norm, mtp.hidden_norm, mtp.norm (bf16 [H])
- *   model-wide: head.norm (bf16 [H], also the MTP's final norm), head.lm_head.{tiles,scales}, embed_tokens (bf16 [V][H])
+ *   model-wide: head.norm (bf16 [H], also the MTP's final norm), head.lm_head.{tiles,scales}, embed_tokens (bf16 [V][H]),
+ *     rope_table (bf16 [max_seq_len][2][rotary_dim], for q38_spec_step)
  * State (per layer):
  *   linear_attn.recurrent_state bf16 [B][Hv][128][128]
  *   linear_attn.conv_state bf16 [2][B][C][3], linear_attn.pending_key f32 [2][B][K][Hk][128],
@@ -95,6 +96,15 @@ size_t q38_fp8_linear_scratch(int rows, int k);
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
                        uint16_t* act_scratch, float* out, void* stream);
 
+/* The MLP's fused gate/up projection, the chip's `mlp_up` (reference kernels.py:74-118, model.py:250-259):
+ * x bf16 [rows][k] rounded to e5m2, times the gate/up weight packed with gate and up rows interleaved by 32
+ * ([2*inter][k]), then bf16(silu(gate)) * up rounded to e5m2, written as the down projection's input tiles
+ * (bf16 [pad(rows)/32][inter/64][64][32], q38_tiles_size(rows, inter) bytes). act_scratch holds
+ * q38_tiles_size(rows, k) bytes. */
+int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int inter,
+               uint16_t* act_scratch, uint16_t* out_tiles, void* stream);
+size_t q38_tiles_size(int rows, int k);
+
 /* One verify step over all B rows: embeds bf16 [B][K][H]; cos, sin bf16 [B][K][rotary_dim]; position int32 [B];
  * active f32 [B]; accepted int32 [B]. Writes the last layer's hidden state bf16 [B][K][H] (before the final norm),
  * commits each row's `accepted` tokens of the previous step, and flips the parity. */
@@ -117,6 +127,18 @@ int q38_embed(q38_handle* h, const int32_t* ids, int n, uint16_t* out, void* str
 /* Greedy acceptance: picks int32 [B][K], drafts int32 [B][K-1], active f32 [B] -> match, accepted int32 [B]. */
 int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const float* active, int32_t* match,
                int32_t* accepted, void* stream);
+
+/* One whole speculative step on the device (the reference's Scheduler._verify_step with MTP drafts,
+ * scheduler.py:160-193,269-301), for all B rows, with no host round trip. Device state, read and updated:
+ *   position int32 [B]  the verify step's first position (row.written); advanced by the accepted count
+ *   index    int32 [B]  the last step's position (the MTP drafter's index); set to the old position
+ *   match    int32 [B]  the last step's matched drafts (the MTP's `take`); replaced by this step's
+ *   accepted int32 [B]  tokens the verify commits from the last step (match + 1); replaced by this step's
+ *   hidden   bf16 [B][K][H], picks int32 [B][K]: the last step's verify output and picks; replaced by this step's
+ * active f32 [B] is read; drafts int32 [B][K-1] receives this step's drafts. Needs the MTP layer, the head, the
+ * embeddings and a bound "rope_table" (bf16 [max_seq_len][2][rotary_dim]: cos then sin of each position). */
+int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
+                  uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
 
 #ifdef __cplusplus
 }

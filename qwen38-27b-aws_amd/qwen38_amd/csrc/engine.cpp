@@ -60,7 +60,8 @@ struct q38_handle {
     int parity = 0;
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_beta, off_g, off_part,
-        off_scores, off_weights, off_htiles, off_x32, off_maxima, workspace_bytes;
+        off_scores, off_weights, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
+        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, workspace_bytes;
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
@@ -84,6 +85,7 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
         if (name == "head.norm") return H * 2;
         if ((r = fp8("head.lm_head", V, H))) return r;
         if (name == "embed_tokens") return V * H * 2;
+        if (name == "rope_table") return S * 2 * 64 * 2;
         if (name == "workspace") return h->workspace_bytes;
         return 0;
     }
@@ -427,6 +429,15 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_htiles = take(Tp * H * 2);
     h->off_x32 = take(Tp * H * 4);
     h->off_maxima = take(Tp * (h->V / 32) * 4);
+    h->off_sp_embeds = take(Tp * H * 2);
+    h->off_sp_cos = take(Tp * 64 * 2);
+    h->off_sp_sin = take(Tp * 64 * 2);
+    h->off_sp_states = take(Tp * H * 2);
+    h->off_sp_out = take(Tp * H * 2);
+    h->off_sp_current = take(Tp * H * 2);
+    h->off_sp_ids = take(Tp * 4);
+    h->off_sp_at = take(Tp * 4);
+    h->off_sp_draft = take(Tp * 4);
     h->workspace_bytes = o;
     *out = h;
     return 0;
@@ -520,6 +531,28 @@ int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles,
     HIP_TRY(q38_gemm(a, EPI_PARTIAL, 1, stream));
     return 0;
 }
+
+int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int inter,
+               uint16_t* act_scratch, uint16_t* out_tiles, void* stream_) {
+    if (!x || !tiles || !scale_words || !act_scratch || !out_tiles) return fail("null argument");
+    if (rows < 1 || (2 * inter) % 256 || inter % 64 || k % 256) return fail("mlp_up needs 2*inter % 256 == 0 and K % 256 == 0");
+    hipStream_t stream = (hipStream_t)stream_;
+    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
+    GemmArgs a{};
+    a.w = tiles;
+    a.ws = scale_words;
+    a.act = act_scratch;
+    a.K = k;
+    a.N = 2 * inter;
+    a.T = rows;
+    a.Tpad = pad_tokens(rows);
+    a.ksteps = k / 64;
+    a.out0 = out_tiles;
+    HIP_TRY(q38_gemm(a, EPI_SWIGLU, 1, stream));
+    return 0;
+}
+
+size_t q38_tiles_size(int rows, int k) { return (size_t)pad_tokens(rows) * k * 2; }
 
 int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
                const float* active, const int32_t* accepted, uint16_t* out_hidden, void* stream_) {
@@ -619,6 +652,57 @@ int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, i
     a.groups = groups;
     a.ids = ids;
     HIP_TRY(q38_head_pick(a, (hipStream_t)stream_));
+    return 0;
+}
+
+int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
+                  uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream_) {
+    if (!h || !position || !index || !match || !accepted || !active || !hidden || !picks || !drafts)
+        return fail("null argument");
+    if (!h->cfg.mtp) return fail("the speculative step needs the MTP layer");
+    if (h->K < 2) return fail("the speculative step needs at least 2 verify tokens");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto rope = get<uint16_t>(h, "rope_table", -1, &ok);
+    if (!ok) return 1;
+    const int B = h->B, K = h->K, H = h->H, S = h->S;
+    uint16_t* embeds = (uint16_t*)h->ws(h->off_sp_embeds);
+    uint16_t* cos = (uint16_t*)h->ws(h->off_sp_cos);
+    uint16_t* sin = (uint16_t*)h->ws(h->off_sp_sin);
+    uint16_t* states = (uint16_t*)h->ws(h->off_sp_states);
+    uint16_t* out = (uint16_t*)h->ws(h->off_sp_out);
+    uint16_t* current = (uint16_t*)h->ws(h->off_sp_current);
+    int32_t* ids = (int32_t*)h->ws(h->off_sp_ids);
+    int32_t* at = (int32_t*)h->ws(h->off_sp_at);
+    int32_t* draft = (int32_t*)h->ws(h->off_sp_draft);
+
+    // Drafts (scheduler.py:160-193): the first MTP call takes the last step's K hidden states and picks at its
+    // positions; the draft comes from its output at each row's match; each further draft from an MTP call on the
+    // previous draft alone.
+    if (q38_embed(h, picks, B * K, embeds, stream_)) return 1;
+    HIP_TRY(q38_rope_gather(index, 1, B, K, S, rope, cos, sin, stream));
+    if (q38_mtp_step(h, hidden, embeds, cos, sin, index, active, out, stream_)) return 1;
+    HIP_TRY(q38_select_rows(out, match, B, K, H, current, stream));
+    for (int j = 0; j < K - 1; ++j) {
+        if (q38_head_pick(h, current, B, 1, draft, stream_)) return 1;
+        HIP_TRY(q38_draft_column(draft, K, B, j, drafts, stream));
+        if (j == K - 2) break;
+        HIP_TRY(q38_mtp_followup(current, draft, B, K, H, states, ids, stream));
+        if (q38_embed(h, ids, B * K, embeds, stream_)) return 1;
+        HIP_TRY(q38_offset_positions(index, match, j, B, at, stream));
+        HIP_TRY(q38_rope_gather(at, 1, B, K, S, rope, cos, sin, stream));
+        if (q38_mtp_step(h, states, embeds, cos, sin, at, active, out, stream_)) return 1;
+        HIP_TRY(q38_select_rows(out, nullptr, B, K, H, current, stream));
+    }
+    // Verify (scheduler.py:276-301): [last emitted token, drafts] per row, the head over all B*K rows, acceptance.
+    HIP_TRY(q38_verify_tokens(picks, match, drafts, B, K, ids, stream));
+    if (q38_embed(h, ids, B * K, embeds, stream_)) return 1;
+    HIP_TRY(q38_rope_gather(position, 0, B, K, S, rope, cos, sin, stream));
+    if (q38_verify(h, embeds, cos, sin, position, active, accepted, hidden, stream_)) return 1;
+    if (q38_head_pick(h, hidden, B * K, 4, picks, stream_)) return 1;
+    HIP_TRY(q38_accept(picks, drafts, active, B, K, match, accepted, stream));
+    HIP_TRY(q38_advance(position, index, accepted, B, stream));
     return 0;
 }
 

@@ -112,3 +112,12 @@ hipError_t q38_accept(const int* picks, const int* drafts, const float* active, 
 hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint32_t* words,
                     hipStream_t stream);
 hipError_t q38_act_tiles(const bf16_t* x, int T, int K, bf16_t* act, hipStream_t stream);
+hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
+                           hipStream_t s);
+hipError_t q38_select_rows(const bf16_t* rows, const int* idx, int B, int K, int H, bf16_t* out, hipStream_t s);
+hipError_t q38_mtp_followup(const bf16_t* current, const int* draft, int B, int K, int H, bf16_t* states, int* ids,
+                            hipStream_t s);
+hipError_t q38_verify_tokens(const int* picks, const int* match, const int* drafts, int B, int K, int* ids, hipStream_t s);
+hipError_t q38_offset_positions(const int* index, const int* match, int add, int B, int* at, hipStream_t s);
+hipError_t q38_advance(int* position, int* index, const int* accepted, int B, hipStream_t s);
+hipError_t q38_draft_column(const int* ids, int K, int B, int j, int* drafts, hipStream_t s);

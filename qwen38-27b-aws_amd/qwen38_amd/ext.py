@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_verify", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept",
+    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
 )
 
 
@@ -60,15 +60,18 @@ def library() -> ctypes.CDLL:
     lib.q38_fp8_linear.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_fp8_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_mlp_up.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_tiles_size.argtypes = [i, i]
     lib.q38_verify.argtypes = [p] * 8 + [p]
     lib.q38_mtp_step.argtypes = [p] * 8 + [p]
     lib.q38_head_groupmax.argtypes = [p, p, i, p, p]
     lib.q38_head_pick.argtypes = [p, p, i, i, p, p]
     lib.q38_embed.argtypes = [p, p, i, p, p]
     lib.q38_accept.argtypes = [p, p, p, p, p, p, p]
+    lib.q38_spec_step.argtypes = [p] * 10
     for name in EXPORTS:
         if name not in ("q38_last_error", "q38_destroy"):
-            getattr(lib, name).restype = ctypes.c_size_t if name == "q38_fp8_linear_scratch" else ctypes.c_int
+            getattr(lib, name).restype = ctypes.c_size_t if name in ("q38_fp8_linear_scratch", "q38_tiles_size") else ctypes.c_int
     _lib = lib
     return lib
 
@@ -161,6 +164,9 @@ class Handle:
     def accept(self, picks, drafts, active, match, accepted) -> None:
         check(self.lib.q38_accept(self.h, *map(ptr, (picks, drafts, active, match, accepted)), stream()))
 
+    def spec_step(self, position, index, match, accepted, active, hidden, picks, drafts) -> None:
+        check(self.lib.q38_spec_step(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
+
 
 def pack_weight(coded: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """(e4m3 bytes [N, K], E8M0 bytes [N, K/32]) on the GPU -> (tiles, scale words) in the GEMM layout."""
@@ -188,4 +194,16 @@ def fp8_linear_f32(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, n:
     scratch = torch.empty(lib.q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
     out = torch.empty(rows, n, dtype=torch.float32, device=x.device)
     check(lib.q38_fp8_linear_f32(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(words), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def mlp_up(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, inter: int, scratch=None, out=None) -> torch.Tensor:
+    """The fused gate/up projection with SwiGLU (`mlp_up`): bf16 x [rows, k] -> the down projection's input tiles."""
+    rows, k = x.shape
+    lib = library()
+    if scratch is None:
+        scratch = torch.empty(lib.q38_tiles_size(rows, k), dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty(lib.q38_tiles_size(rows, inter), dtype=torch.uint8, device=x.device)
+    check(lib.q38_mlp_up(ptr(x), rows, k, ptr(tiles), ptr(words), inter, ptr(scratch), ptr(out), stream()))
     return out
