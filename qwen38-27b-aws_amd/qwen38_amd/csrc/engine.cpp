@@ -135,8 +135,8 @@ T* get(q38_handle* h, const std::string& name, int layer, bool* ok) {
 
 // Split-K count for an N-column GEMM with partial sums: enough workgroups to fill 256 CUs, K-steps per split even.
 int choose_splits(const q38_handle* h, int N, int K) {
-    const int wg_feat = h->Tpad >= 256 ? 128 : 256;
-    const int tiles = (N / wg_feat) * (h->Tpad >= 256 ? h->Tpad / 256 : 1);
+    const int wg_feat = h->Tpad >= 128 ? 128 : 256;
+    const int tiles = (N / wg_feat) * (h->Tpad >= 128 ? h->Tpad / 128 : 1);
     const int ks = K / 64;
     int best = 1;
     for (int s = 1; s <= SPLIT_MAX; ++s) {

@@ -13,8 +13,6 @@
 // The pending input snapshot is the in_proj_qkv output itself (the GEMM writes it into the half being written).
 #include "kernels.h"
 
-#define GDN_KMAX 8
-
 // `_gates` (model.py:333-337) and the active masks (model.py:411-413): beta = bf16 sigmoid of a bf16 linear, and
 // g = -exp(A_log) * softplus(float(bf16 linear) + dt_bias), both times active. Block: 8 tokens x 16 outputs
 // (output o < Hv is in_proj_b's row o, else in_proj_a's row o - Hv); each wave owns 4 outputs.
@@ -79,19 +77,20 @@ __global__ __launch_bounds__(256) void gdn_gates_kernel(const GatesArgs a) {
     }
 }
 
+// K (tokens per row) is a template parameter so that every per-token array lives in registers.
+template <int K>
 __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     constexpr int D = 128;
-    __shared__ float mixed[GDN_KMAX][3 * D];   // SiLU(conv) of this head's q, k, v channels
-    __shared__ float qn[GDN_KMAX][D], kn[GDN_KMAX][D];
-    __shared__ float wk[GDN_KMAX][D];          // committed snapshot keys times their decay weights
-    __shared__ float part[4][2 * GDN_KMAX][D]; // reads, one partial per row quarter
-    __shared__ float kk[GDN_KMAX][GDN_KMAX], qk[GDN_KMAX][GDN_KMAX];
-    __shared__ float ob[GDN_KMAX][D];
-    __shared__ float rms[GDN_KMAX];
-    __shared__ float coef[GDN_KMAX];
+    __shared__ float mixed[K][3 * D];   // SiLU(conv) of this head's q, k, v channels
+    __shared__ float qn[K][D], kn[K][D];
+    __shared__ float wk[K][D];          // committed snapshot keys times their decay weights
+    __shared__ float part[4][2 * K][D]; // reads, one partial per row quarter
+    __shared__ float kk[K][K], qk[K][K];
+    __shared__ float ob[K][D];
+    __shared__ float rms[K];
 
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = a.K, Hv = a.Hv, Hk = a.Hk, C = a.C;
+    const int Hv = a.Hv, Hk = a.Hk, C = a.C;
     const int rep = Hv / Hk, kh = h / rep;
     const bool owner = (h % rep) == 0;  // writes the shared key-head channels
     const bool on = a.active[b] > 0.5f;
@@ -100,42 +99,41 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
 
     // Commit coefficients (model.py:386-398): decays of the taken snapshots, the state's scale and each snapshot's
     // weight exp(sum of later decays), all float32 in the reference's order.
-    float decays[GDN_KMAX];
+    float decays[K], coef[K];
     float total = 0.0f;
 #pragma unroll
-    for (int s = 0; s < GDN_KMAX; ++s) {
-        decays[s] = 0.0f;
-        if (s < K) {
-            float taken = acc_n > s ? 1.0f : 0.0f;
-            decays[s] = a.decay_old[((size_t)b * K + s) * Hv + h] * taken;
-            total = total + decays[s];
-        }
+    for (int s = 0; s < K; ++s) {
+        decays[s] = a.decay_old[((size_t)b * K + s) * Hv + h] * (acc_n > s ? 1.0f : 0.0f);
+        total = total + decays[s];
     }
     const float scale = on ? expf(total) * keep : 1.0f;
-    if (tid < K) {
+    {
         float rem = total;
-        for (int s = 0; s <= tid; ++s) rem = rem - decays[s];
-        coef[tid] = expf(rem) * (acc_n > tid ? 1.0f : 0.0f) * keep * (on ? 1.0f : 0.0f);
+#pragma unroll
+        for (int s = 0; s < K; ++s) {
+            rem = rem - decays[s];
+            coef[s] = expf(rem) * (acc_n > s ? 1.0f : 0.0f) * keep * (on ? 1.0f : 0.0f);
+        }
     }
 
     // Conv history and conv (model.py:399-409). Channel groups: q of key head kh, k of key head kh, v of head h.
     for (int ci = tid; ci < 3 * D; ci += 256) {
         const int grp = ci / D, j = ci % D;
         const int c = grp == 0 ? kh * D + j : grp == 1 ? Hk * D + kh * D + j : 2 * Hk * D + h * D + j;
-        float win[3 + GDN_KMAX];
         const bf16_t* old = a.conv_old + ((size_t)b * C + c) * 3;
+        float w_old[3 + K];
+        w_old[0] = bf2f(old[0]);
+        w_old[1] = bf2f(old[1]);
+        w_old[2] = bf2f(old[2]);
+#pragma unroll
+        for (int s = 0; s < K; ++s) w_old[3 + s] = bf2f(a.qkv_old[((size_t)b * K + s) * C + c]);
         float hist[3];
-        if (on) {
-            float w_old[3 + GDN_KMAX];
-            w_old[0] = bf2f(old[0]);
-            w_old[1] = bf2f(old[1]);
-            w_old[2] = bf2f(old[2]);
-            for (int s = 0; s < K; ++s) w_old[3 + s] = bf2f(a.qkv_old[((size_t)b * K + s) * C + c]);
-            for (int jj = 0; jj < 3; ++jj) hist[jj] = w_old[acc_n + jj] * keep;
-        } else {
-            hist[0] = bf2f(old[0]);
-            hist[1] = bf2f(old[1]);
-            hist[2] = bf2f(old[2]);
+#pragma unroll
+        for (int jj = 0; jj < 3; ++jj) {
+            float v = w_old[jj];
+#pragma unroll
+            for (int s = 1; s <= K; ++s) v = acc_n == s ? w_old[s + jj] : v;
+            hist[jj] = on ? v * keep : w_old[jj];
         }
         if (grp == 2 || owner) {
             bf16_t* dst = a.conv_new + ((size_t)b * C + c) * 3;
@@ -143,12 +141,15 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
             dst[1] = f2bf(hist[1]);
             dst[2] = f2bf(hist[2]);
         }
+        float win[3 + K];
         win[0] = hist[0];
         win[1] = hist[1];
         win[2] = hist[2];
+#pragma unroll
         for (int t = 0; t < K; ++t) win[3 + t] = bf2f(a.qkv_new[((size_t)b * K + t) * C + c]);
         const bf16_t* cw = a.conv_w + (size_t)c * 4;
         const float w0 = bf2f(cw[0]), w1 = bf2f(cw[1]), w2 = bf2f(cw[2]), w3 = bf2f(cw[3]);
+#pragma unroll
         for (int t = 0; t < K; ++t) {
             float m = rbf(((rbf(win[t] * w0) + rbf(win[t + 1] * w1)) + rbf(win[t + 2] * w2)) + rbf(win[t + 3] * w3));
             mixed[t][ci] = rbf(m * rbf(sigmoidf_(m)));
@@ -172,8 +173,11 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     }
     // Snapshot keys times their commit weights (model.py:397-398).
     for (int i = tid; i < K * D; i += 256) {
-        int s = i / D, j = i % D;
-        wk[s][j] = a.key_old[(((size_t)b * K + s) * Hk + kh) * D + j] * coef[s];
+        const int s = i / D, j = i % D;
+        float c = 0.0f;
+#pragma unroll
+        for (int r = 0; r < K; ++r) c = s == r ? coef[r] : c;
+        wk[s][j] = a.key_old[(((size_t)b * K + s) * Hk + kh) * D + j] * c;
     }
     __syncthreads();
 
@@ -189,75 +193,75 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     // [32*wave, 32*wave+32).
     {
         const int j0 = lane * 2, i0 = wave * 32;
-        float d0[GDN_KMAX], d1[GDN_KMAX];
+        float d0[K], d1[K];
 #pragma unroll
-        for (int s = 0; s < GDN_KMAX; ++s) {
-            d0[s] = d1[s] = 0.0f;
-            if (s < K) {
-                const float* dp = a.delta_old + (((size_t)b * K + s) * Hv + h) * D + j0;
-                d0[s] = dp[0];
-                d1[s] = dp[1];
-            }
+        for (int s = 0; s < K; ++s) {
+            const float2 dp = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + j0);
+            d0[s] = dp.x;
+            d1[s] = dp.y;
         }
-        float p0[2 * GDN_KMAX], p1[2 * GDN_KMAX];
+        float p0[2 * K], p1[2 * K];
 #pragma unroll
-        for (int r = 0; r < 2 * GDN_KMAX; ++r) p0[r] = p1[r] = 0.0f;
+        for (int r = 0; r < 2 * K; ++r) p0[r] = p1[r] = 0.0f;
         bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
+        uint32_t sv[32];
+#pragma unroll
+        for (int ii = 0; ii < 32; ++ii) sv[ii] = *(const uint32_t*)(st + (size_t)(i0 + ii) * D + j0);
+#pragma unroll 4
         for (int ii = 0; ii < 32; ++ii) {
             const int i = i0 + ii;
-            uint32_t sv = *(const uint32_t*)(st + (size_t)i * D + j0);
             float u0 = 0.0f, u1 = 0.0f;
 #pragma unroll
-            for (int s = 0; s < GDN_KMAX; ++s) {
-                if (s < K) {
-                    u0 += wk[s][i] * d0[s];
-                    u1 += wk[s][i] * d1[s];
-                }
+            for (int s = 0; s < K; ++s) {
+                u0 += wk[s][i] * d0[s];
+                u1 += wk[s][i] * d1[s];
             }
-            float c0 = rbf(bf2f(sv & 0xffff) * scale + u0);
-            float c1 = rbf(bf2f(sv >> 16) * scale + u1);
+            const float c0 = rbf(bf2f(sv[ii] & 0xffff) * scale + u0);
+            const float c1 = rbf(bf2f(sv[ii] >> 16) * scale + u1);
             *(uint32_t*)(st + (size_t)i * D + j0) = (uint32_t)f2bf(c0) | ((uint32_t)f2bf(c1) << 16);
 #pragma unroll
-            for (int r = 0; r < 2 * GDN_KMAX; ++r) {
-                if (r < 2 * K) {
-                    float rv = r < K ? kn[r][i] : qn[r - K][i];
-                    p0[r] += rv * c0;
-                    p1[r] += rv * c1;
-                }
+            for (int r = 0; r < 2 * K; ++r) {
+                const float rv = r < K ? kn[r][i] : qn[r - K][i];
+                p0[r] += rv * c0;
+                p1[r] += rv * c1;
             }
         }
 #pragma unroll
-        for (int r = 0; r < 2 * GDN_KMAX; ++r) {
-            if (r < 2 * K) {
-                part[wave][r][j0] = p0[r];
-                part[wave][r][j0 + 1] = p1[r];
-            }
-        }
+        for (int r = 0; r < 2 * K; ++r) *(float2*)&part[wave][r][j0] = make_float2(p0[r], p1[r]);
     }
     __syncthreads();
 
     // In-step solve (model.py:431-448), one column per thread.
     if (tid < D) {
         const int j = tid;
-        float cum[GDN_KMAX], beta[GDN_KMAX], gl[GDN_KMAX], dl[GDN_KMAX];
+        float cum[K], beta[K], gl[K], dl[K];
+#pragma unroll
         for (int t = 0; t < K; ++t) {
             gl[t] = a.g[((size_t)b * K + t) * Hv + h];
             beta[t] = a.beta[((size_t)b * K + t) * Hv + h];
             cum[t] = t == 0 ? gl[0] : cum[t - 1] + gl[t];
         }
+#pragma unroll
         for (int t = 0; t < K; ++t) {
-            float ks = ((part[0][t][j] + part[1][t][j]) + part[2][t][j]) + part[3][t][j];
-            float qs = ((part[0][K + t][j] + part[1][K + t][j]) + part[2][K + t][j]) + part[3][K + t][j];
+            const float ks = ((part[0][t][j] + part[1][t][j]) + part[2][t][j]) + part[3][t][j];
+            const float qs = ((part[0][K + t][j] + part[1][K + t][j]) + part[2][K + t][j]) + part[3][K + t][j];
             float delta = mixed[t][2 * D + j] - expf(cum[t]) * ks;
+#pragma unroll
             for (int s = 0; s < t; ++s) delta = delta - (expf(cum[t] - cum[s]) * kk[t][s]) * dl[s];
             dl[t] = delta * beta[t];
             float out = expf(cum[t]) * qs;
+#pragma unroll
             for (int s = 0; s <= t; ++s) out = out + (expf(cum[t] - cum[s]) * qk[t][s]) * dl[s];
             ob[t][j] = rbf(out);
             a.delta_new[(((size_t)b * K + t) * Hv + h) * D + j] = dl[t];
             if (owner) a.key_new[(((size_t)b * K + t) * Hk + kh) * D + j] = kn[t][j] + 0.0f;
         }
-        if (j < K) a.decay_new[((size_t)b * K + j) * Hv + h] = gl[j] + 0.0f;
+        if (j < K) {
+            float g = 0.0f;
+#pragma unroll
+            for (int t = 0; t < K; ++t) g = j == t ? gl[t] : g;
+            a.decay_new[((size_t)b * K + j) * Hv + h] = g + 0.0f;
+        }
     }
     __syncthreads();
 
@@ -289,7 +293,21 @@ hipError_t q38_gdn_gates(const GatesArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t q38_gdn_verify(const GdnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(gdn_verify_kernel, dim3(a.Hv, a.B), dim3(256), 0, stream, a);
+template <int K>
+static hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(gdn_verify_kernel<K>, dim3(a.Hv, a.B), dim3(256), 0, stream, a);
     return hipGetLastError();
+}
+
+hipError_t q38_gdn_verify(const GdnArgs& a, hipStream_t stream) {
+    switch (a.K) {
+        case 1: return launch_gdn<1>(a, stream);
+        case 2: return launch_gdn<2>(a, stream);
+        case 3: return launch_gdn<3>(a, stream);
+        case 4: return launch_gdn<4>(a, stream);
+        case 5: return launch_gdn<5>(a, stream);
+        case 6: return launch_gdn<6>(a, stream);
+        case 7: return launch_gdn<7>(a, stream);
+        default: return launch_gdn<8>(a, stream);
+    }
 }

@@ -23,15 +23,28 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 template <int WF, int WT, int FR, int TR, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const GemmArgs a) {
     constexpr int TT = WT * TR;       // 32-token tiles per workgroup
     constexpr int STAGE = TT * 4096;  // LDS bytes per K-step of bf16 activations
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wf = wave % WF, wt = wave / WF;
-    const int ft0 = blockIdx.x * (WF * FR) + wf * FR;
-    const int tf0 = blockIdx.y * TT;
+    // Block order: workgroups are dealt to the 8 XCDs round-robin, so when the feature-tile count allows, the token
+    // tiles of one feature tile get ids 8 apart: same XCD, same L2, launched together, and the weight tile is read
+    // from HBM once.
+    const int nf = a.N / (WF * FR * 32), nt = gridDim.x / nf;
+    int fb, tb;
+    if (nf % 8 == 0) {
+        const int lo = blockIdx.x & 7, rest = blockIdx.x >> 3;
+        tb = rest % nt;
+        fb = (rest / nt) * 8 + lo;
+    } else {
+        fb = blockIdx.x % nf;
+        tb = blockIdx.x / nf;
+    }
+    const int ft0 = fb * (WF * FR) + wf * FR;
+    const int tf0 = tb * TT;
     const int KS = a.K >> 6;
     const int ks0 = blockIdx.z * a.ksteps, nks = a.ksteps;
 
@@ -61,7 +74,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
         }
     };
     // Bytes 0-15 of a lane belong to the K-step's first MX block (scale byte in lane half 0), bytes 16-31 to the
-    // second (lane half 1), so each lane reads both scale bytes.
+    // second (lane half 1), so each lane reads both scale words. The bytes are extracted only when used: extracting
+    // them at load time would make every K-step wait for the next one's loads.
     v4i wA[FR][2], wB[FR][2];
     uint32_t sA[FR][2], sB[FR][2];
     auto load_w = [&](int ks, v4i (&wr)[FR][2], uint32_t (&sr)[FR][2]) {
@@ -72,17 +86,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
             wr[f][0] = p[0];
             wr[f][1] = p[1];
             const uint32_t* sw = a.ws + ((size_t)(ft0 + f) * (KS >> 2) + (kabs >> 2)) * 64 + (lane & 31);
-            sr[f][0] = (sw[0] >> ((kabs & 3) * 8)) & 0xff;
-            sr[f][1] = (sw[32] >> ((kabs & 3) * 8)) & 0xff;
+            sr[f][0] = sw[0];
+            sr[f][1] = sw[32];
         }
     };
-    auto compute = [&](int buf, v4i (&wr)[FR][2], uint32_t (&sr)[FR][2]) {
+    auto compute = [&](int ks, int buf, v4i (&wr)[FR][2], uint32_t (&sr)[FR][2]) {
+        const int shift = ((ks0 + ks) & 3) * 8;
         v8bf wb[FR][4];
 #pragma unroll
         for (int f = 0; f < FR; ++f) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const float scale = __uint_as_float(sr[f][m >> 1] << 23);  // 2^(s - 127)
+                const float scale = __uint_as_float(((sr[f][m >> 1] >> shift) & 0xff) << 23);  // 2^(s - 127)
                 uint32_t w0 = (uint32_t)wr[f][m >> 1][(m & 1) * 2], w1 = (uint32_t)wr[f][m >> 1][(m & 1) * 2 + 1];
                 v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false);
                 v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true);
@@ -111,7 +126,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
             load_act(ks + 1);
             load_w(ks + 1, wB, sB);
         }
-        compute(0, wA, sA);
+        compute(ks, 0, wA, sA);
         if (ks + 1 < nks) store_act(1);
         __syncthreads();
         if (ks + 1 >= nks) break;
@@ -119,7 +134,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
             load_act(ks + 2);
             load_w(ks + 2, wA, sA);
         }
-        compute(1, wB, sB);
+        compute(ks + 1, 1, wB, sB);
         if (ks + 2 < nks) store_act(0);
         __syncthreads();
     }
@@ -185,17 +200,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs a) {
 
 template <int WF, int WT, int FR, int TR, int EPI>
 static hipError_t launch_gemm(const GemmArgs& a, int splits, hipStream_t stream) {
-    dim3 grid(a.N / (WF * FR * 32), a.Tpad / (WT * TR * 32), splits);
+    dim3 grid((a.N / (WF * FR * 32)) * (a.Tpad / (WT * TR * 32)), 1, splits);
     hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, EPI>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
-// Shapes are checked by the caller (engine.cpp): N % 256 == 0, K % 256 == 0, Tpad 32, 64, 128 or a multiple of 256,
+// Shapes are checked by the caller (engine.cpp): N % 256 == 0, K % 256 == 0, Tpad 32, 64 or a multiple of 128,
 // (K / 64) % splits == 0.
 template <int EPI>
 static hipError_t gemm_dispatch(const GemmArgs& a, int splits, hipStream_t stream) {
-    if (a.Tpad >= 256) return launch_gemm<2, 2, 2, 4, EPI>(a, splits, stream);
-    if (a.Tpad == 128) return launch_gemm<4, 1, 2, 4, EPI>(a, splits, stream);
+    if (a.Tpad >= 128) return launch_gemm<2, 2, 2, 2, EPI>(a, splits, stream);
     if (a.Tpad == 64) return launch_gemm<4, 1, 2, 2, EPI>(a, splits, stream);
     return launch_gemm<4, 1, 2, 1, EPI>(a, splits, stream);
 }
