@@ -55,7 +55,7 @@ int q38_create(const q38_config* cfg, q38_handle** out);
 void q38_destroy(q38_handle* h);
 
 /* Buffers, by name and layer (layer -1 for model-wide buffers; layer num_layers is the MTP layer). Sizes in bytes.
- * Weights (FP8 projections bound as packed tiles + scale words from q38_pack_weight):
+ * Weights (FP8 projections bound as packed tiles + tile scales from q38_pack_weight):
  *   per layer: input_layernorm, post_attention_layernorm (bf16 [H]), mlp.gate_up.{tiles,scales} (gate and up rows
  *     interleaved by 32), mlp.down.{tiles,scales}
  *   gated-delta layers: linear_attn.in_proj_qkvz.{tiles,scales} (in_proj_qkv rows then in_proj_z rows),
@@ -73,7 +73,7 @@ void q38_destroy(q38_handle* h);
  *   linear_attn.pending_delta f32 [2][B][K][Hv][128], linear_attn.pending_decay f32 [2][B][K][Hv],
  *   linear_attn.pending_input bf16 [2][B][K][C]: two halves, the current one given by q38_parity
  *   self_attn.k_cache bf16 [B][Hkv][S][hd]; self_attn.v_cache bf16 [B][Hkv][S/32][hd][32] (transposed per 32 positions)
- * Scratch: workspace (model-wide). */
+ * Scratch: workspace (model-wide; its GEMM counters are zeroed when it is bound). */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
 int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
 
@@ -82,27 +82,32 @@ int q38_parity(q38_handle* h, int* parity);
 int q38_set_parity(q38_handle* h, int parity);
 
 /* Pack an FP8 projection: e4m3 bytes [N][K] and E8M0 scale bytes [N][K/32] (row-major, a torch Linear weight's
- * layout) into tiles [N/32][K/64][64][32] and scale words [N/32][K/256][64]. N % 32 == 0, K % 256 == 0. */
-int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint32_t* scale_words,
+ * layout) into tiles [N/32][K/64][64][32] and tile scales [N/32][K/64][32][2] (N * K / 32 bytes). N % 32 == 0,
+ * K % 256 == 0. */
+int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint8_t* tile_scales,
                     void* stream);
 
 /* A standalone FP8 projection, `FP8Linear.forward` (reference model.py:211-229): x bf16 [rows][k] rounded to e5m2,
- * times the packed weight ([n][k] e4m3 + E8M0), float32 sums, bf16 out [rows][n]. act_scratch holds
- * q38_fp8_linear_scratch(rows, k) bytes (the e5m2-rounded input as bf16 tiles). n % 256 == 0, k % 256 == 0. */
-int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                   uint16_t* act_scratch, uint16_t* out, void* stream);
+ * times the packed weight ([n][k] e4m3 + E8M0), float32 sums, bf16 out [rows][n]. n % 256 == 0, k % 256 == 0.
+ * scratch holds q38_fp8_linear_scratch(rows, k) bytes: the e5m2 input tiles (q38_tiles_size(rows, k) bytes), then the
+ * GEMM's arrival counters and partial sums. It must be zero-filled before its first use; every call leaves the
+ * counters at zero again. Calls that share a scratch must not overlap. With x null the scratch already holds the input
+ * tiles (of an earlier call with the same rows and k). */
+int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                   uint8_t* scratch, uint16_t* out, void* stream);
 size_t q38_fp8_linear_scratch(int rows, int k);
 /* The same with float32 output [rows][n] (no bf16 rounding); rows in {32, 64, 128} or a multiple of 256. */
-int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                       uint16_t* act_scratch, float* out, void* stream);
+int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                       uint8_t* scratch, float* out, void* stream);
 
 /* The MLP's fused gate/up projection, the chip's `mlp_up` (reference kernels.py:74-118, model.py:250-259):
  * x bf16 [rows][k] rounded to e5m2, times the gate/up weight packed with gate and up rows interleaved by 32
  * ([2*inter][k]), then bf16(silu(gate)) * up rounded to e5m2, written as the down projection's input tiles
- * (bf16 [pad(rows)/32][inter/64][64][32], q38_tiles_size(rows, inter) bytes). act_scratch holds
- * q38_tiles_size(rows, k) bytes. */
-int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int inter,
-               uint16_t* act_scratch, uint16_t* out_tiles, void* stream);
+ * (e5m2 bytes [pad(rows)/32][inter/64][4][64][8], q38_tiles_size(rows, inter) bytes). scratch as for
+ * q38_fp8_linear. */
+int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int inter,
+               uint8_t* scratch, uint8_t* out_tiles, void* stream);
+/* Bytes of e5m2 activation tiles for rows x k (rows padded to 32, 64, 128 or a multiple of 256). */
 size_t q38_tiles_size(int rows, int k);
 
 /* One verify step over all B rows: embeds bf16 [B][K][H]; cos, sin bf16 [B][K][rotary_dim]; position int32 [B];

@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const AttnArgs a) {
                 const int hq = kvh * G + g, tok = b * K + t;
                 float gate = bf2f(a.qkv[(size_t)tok * a.ld + (size_t)hq * 512 + 256 + d]);
                 o = rbf(o * rbf(sigmoidf_(gate)));
-                a.act[act_offset(tok, hq * 256 + d, act_k)] = f2bf(e5m2_round(o));
+                a.act[act_offset(tok, hq * 256 + d, act_k)] = (uint8_t)e5m2_byte(o);
             }
         }
     }

@@ -6,11 +6,13 @@
 //
 // Tiles. Every GEMM reads its operands in the layout the MFMA wants, written that way by the kernel that produced
 // them. One K-step of 64 inputs for 32 tokens (or 32 weight rows) is one tile; lane l holds 32 elements of token
-// (row) l % 32 from lane half h = l / 32, in the order of v_mfma_scale_f32_32x32x64_f8f6f4's operands:
+// (row) l % 32 from lane half h = l / 32:
 //     element i of lane half h  <->  input k = 32 * (i / 16) + 16 * h + i % 16  (within the K-step)
-// (for FP8 weights, bytes 0-15 of both halves form the step's first 32-input MX block, whose E8M0 scale lane half 0
-// holds, and bytes 16-31 the second, scaled by lane half 1; measured on gfx950). Weight tiles are FP8 bytes (2 KiB,
-// pack.hip); activation tiles are bf16 (4 KiB) holding e5m2-rounded values, or plain bf16 for the head.
+// and MFMA m (v_mfma_f32_32x32x16_bf16, 16 inputs) of the K-step takes elements [8m, 8m + 8) of every lane, so
+// elements 0-15 are the K-step's first 32-input MX block and 16-31 its second. Weight tiles are FP8 e4m3 bytes, lane
+// by lane (2 KiB, pack.hip), with their E8M0 scales as [row][block] bytes per tile (64 bytes). Activation tiles are
+// stored MFMA-step-major, [m][lane][8], so that each MFMA's operand is one contiguous run: e5m2 bytes (2 KiB) for the
+// projections, bf16 (4 KiB) for the head.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,10 +63,23 @@ __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : lo
 Q38_HOST_DEVICE int kstep_half(int k) { return (k & 31) >> 4; }
 Q38_HOST_DEVICE int kstep_byte(int k) { return ((k & 63) >> 5) * 16 + (k & 15); }
 
-// Element offset of (t, k) in a tile buffer with K inputs (K a multiple of 64). Four consecutive k from a multiple of 4
-// are contiguous.
+// Element offset of (token t, input k) in activation tiles with K inputs (K a multiple of 64): tile (t / 32, k / 64)
+// of 2048 elements as [m][lane][8] with lane = t % 32 + 32 * kstep_half(k), element e = kstep_byte(k), m = e / 8.
+// Four consecutive k from a multiple of 4 are contiguous.
 Q38_HOST_DEVICE size_t act_offset(int t, int k, int K) {
-    return ((size_t)(t >> 5) * (K >> 6) + (k >> 6)) * 2048 + (size_t)(((t & 31) + kstep_half(k) * 32) * 32) + kstep_byte(k);
+    const int e = kstep_byte(k);
+    return ((size_t)(t >> 5) * (K >> 6) + (k >> 6)) * 2048 +
+           (size_t)((e >> 3) * 512 + ((t & 31) + kstep_half(k) * 32) * 8 + (e & 7));
+}
+
+// The FP8 e5m2 byte of x rounded to e5m2 (e5m2_round): sign, 5 exponent bits (bias 15), 2 mantissa bits.
+__device__ __forceinline__ uint32_t e5m2_byte(float x) {
+    const uint32_t u = __float_as_uint(e5m2_round(x));
+    const uint32_t s = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return s | 0x7eu;  // NaN
+    if (a == 0x7f800000u) return s | 0x7cu;
+    if (a >= 0x38800000u) return s | ((a >> 21) - (112u << 2));  // normal: exponent rebiased from 127 to 15
+    return s | (uint32_t)(__uint_as_float(a) * 65536.0f);        // subnormal: m * 2^-16, m in 0..3
 }
 
 __device__ __forceinline__ float warp_sum(float v) {

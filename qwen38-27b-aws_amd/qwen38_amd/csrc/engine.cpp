@@ -32,8 +32,6 @@ int fail(const std::string& msg) {
         if (e_ != hipSuccess) return fail(std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
-constexpr int SPLIT_MAX = 16;
-
 struct Buf {
     void* p = nullptr;
     size_t n = 0;
@@ -49,19 +47,48 @@ int pad_tokens(int t) {
     return (t + 255) / 256 * 256;
 }
 
+// Compute units of the current device (the GEMMs run one persistent workgroup per CU); 256 (MI355X) when no device
+// answers, as on a build host.
+int device_cus() {
+    static int cus = 0;
+    if (cus) return cus;
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+        cus = n;
+    else {
+        (void)hipGetLastError();
+        cus = 256;
+    }
+    return cus;
+}
+
+// GEMM scratch behind the activation tiles: stream-K arrival counters, then partial slots.
+size_t gemm_scratch_bytes(int cus) { return (size_t)GEMM_COUNTERS * 4 + (size_t)2 * cus * GEMM_SLOT_FLOATS * 4; }
+
+void gemm_scratch(GemmArgs& a, uint8_t* base, int cus) {
+    a.l2_local = q38_gemm_l2_local();
+    a.counters = (int*)base;
+    a.counters_n = GEMM_COUNTERS;
+    a.fix = (float*)(base + (size_t)GEMM_COUNTERS * 4);
+    a.fix_floats = (size_t)2 * cus * GEMM_SLOT_FLOATS;
+    a.cus = cus;
+}
+
 }  // namespace
 
 struct q38_handle {
     q38_config cfg;
     int H, I, V, B, K, S, T, Tpad;
     int Hq, Hkv, hd, Hk, Hv, dk, C;
+    int cus;
     std::vector<std::map<std::string, Buf>> layer;  // num_layers + 1 (the MTP layer)
     std::map<std::string, Buf> global;
     int parity = 0;
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_beta, off_g, off_part,
         off_scores, off_weights, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
-        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, workspace_bytes;
+        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, workspace_bytes;
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
@@ -133,21 +160,7 @@ T* get(q38_handle* h, const std::string& name, int layer, bool* ok) {
     return (T*)it->second.p;
 }
 
-// Split-K count for an N-column GEMM with partial sums: enough workgroups to fill 256 CUs, K-steps per split even.
-int choose_splits(const q38_handle* h, int N, int K) {
-    const int wg_feat = h->Tpad >= 128 ? 128 : 256;
-    const int tiles = (N / wg_feat) * (h->Tpad >= 128 ? h->Tpad / 128 : 1);
-    const int ks = K / 64;
-    int best = 1;
-    for (int s = 1; s <= SPLIT_MAX; ++s) {
-        if (ks % s || (ks / s) % 2) continue;
-        best = s;
-        if (tiles * s >= 256) break;
-    }
-    return best;
-}
-
-int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint16_t* act, int K, int N, int epi,
+int gemm(q38_handle* h, const uint8_t* tiles, const uint8_t* scales, const uint8_t* act, int K, int N, int epi,
          void* out0, int ld0, int n0, void* out1, int ld1, hipStream_t stream, int* splits_out = nullptr) {
     if (N % 256 || K % 256) return fail("GEMM shape N=" + std::to_string(N) + " K=" + std::to_string(K) + " not tileable");
     GemmArgs a{};
@@ -163,20 +176,16 @@ int gemm(q38_handle* h, const uint8_t* tiles, const uint32_t* scales, const uint
     a.n0 = n0;
     a.out1 = out1;
     a.ld1 = ld1;
+    if (epi == EPI_PARTIAL) a.part = (float*)h->ws(h->off_part);
+    gemm_scratch(a, h->ws(h->off_gemm), h->cus);
     int splits = 1;
-    if (epi == EPI_PARTIAL) {
-        splits = choose_splits(h, N, K);
-        a.part = (float*)h->ws(h->off_part);
-    }
-    a.ksteps = K / 64 / splits;
-    if (a.ksteps % 2) return fail("GEMM K-steps per split must be even");
-    HIP_TRY(q38_gemm(a, epi, splits, stream));
+    HIP_TRY(q38_gemm(a, epi, &splits, stream));
     if (splits_out) *splits_out = splits;
     return 0;
 }
 
 int norm_rows(q38_handle* h, const float* part, int splits, const uint16_t* xin, const uint16_t* resid, uint16_t* xout,
-              const uint16_t* w, uint16_t* act, int kact, int col0, uint16_t* hout, const uint16_t* div_w, hipStream_t stream) {
+              const uint16_t* w, uint8_t* act, int kact, int col0, uint16_t* hout, const uint16_t* div_w, hipStream_t stream) {
     NormArgs a{};
     a.part = part;
     a.splits = splits;
@@ -209,15 +218,15 @@ struct StepIO {
 int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream_t stream) {
     bool ok = true;
     const int H = h->H;
-    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
-    uint16_t* act_mid = (uint16_t*)h->ws(h->off_act_mid);
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint8_t* act_mid = h->ws(h->off_act_mid);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     int splits, kmid;
     const uint8_t* otiles;
-    const uint32_t* oscales;
+    const uint8_t* oscales;
     if (is_linear(h, li)) {
         auto qkvz_t = get<uint8_t>(h, "linear_attn.in_proj_qkvz.tiles", li, &ok);
-        auto qkvz_s = get<uint32_t>(h, "linear_attn.in_proj_qkvz.scales", li, &ok);
+        auto qkvz_s = get<uint8_t>(h, "linear_attn.in_proj_qkvz.scales", li, &ok);
         auto pin = get<uint16_t>(h, "linear_attn.pending_input", li, &ok);
         auto wa = get<uint16_t>(h, "linear_attn.in_proj_a", li, &ok);
         auto wb = get<uint16_t>(h, "linear_attn.in_proj_b", li, &ok);
@@ -231,7 +240,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         auto pdelta = get<float>(h, "linear_attn.pending_delta", li, &ok);
         auto pdecay = get<float>(h, "linear_attn.pending_decay", li, &ok);
         otiles = get<uint8_t>(h, "linear_attn.out_proj.tiles", li, &ok);
-        oscales = get<uint32_t>(h, "linear_attn.out_proj.scales", li, &ok);
+        oscales = get<uint8_t>(h, "linear_attn.out_proj.scales", li, &ok);
         if (!ok) return 1;
         const size_t BKC = (size_t)h->B * h->K * h->C;
         uint16_t* z = (uint16_t*)h->ws(h->off_z);
@@ -285,13 +294,13 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         kmid = h->Hv * h->dk;
     } else {
         auto qkv_t = get<uint8_t>(h, "self_attn.qkv.tiles", li, &ok);
-        auto qkv_s = get<uint32_t>(h, "self_attn.qkv.scales", li, &ok);
+        auto qkv_s = get<uint8_t>(h, "self_attn.qkv.scales", li, &ok);
         auto qn = get<uint16_t>(h, "self_attn.q_norm", li, &ok);
         auto kn = get<uint16_t>(h, "self_attn.k_norm", li, &ok);
         auto kc = get<uint16_t>(h, "self_attn.k_cache", li, &ok);
         auto vc = get<uint16_t>(h, "self_attn.v_cache", li, &ok);
         otiles = get<uint8_t>(h, "self_attn.o_proj.tiles", li, &ok);
-        oscales = get<uint32_t>(h, "self_attn.o_proj.scales", li, &ok);
+        oscales = get<uint8_t>(h, "self_attn.o_proj.scales", li, &ok);
         if (!ok) return 1;
         const int nqkv = h->Hq * h->hd * 2 + 2 * h->Hkv * h->hd;
         uint16_t* qkv = (uint16_t*)h->ws(h->off_qkv);
@@ -331,12 +340,12 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     bool ok = true;
     const int H = h->H, I = h->I;
     auto gu_t = get<uint8_t>(h, "mlp.gate_up.tiles", li, &ok);
-    auto gu_s = get<uint32_t>(h, "mlp.gate_up.scales", li, &ok);
+    auto gu_s = get<uint8_t>(h, "mlp.gate_up.scales", li, &ok);
     auto dn_t = get<uint8_t>(h, "mlp.down.tiles", li, &ok);
-    auto dn_s = get<uint32_t>(h, "mlp.down.scales", li, &ok);
+    auto dn_s = get<uint8_t>(h, "mlp.down.scales", li, &ok);
     if (!ok) return 1;
-    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
-    uint16_t* act_ffn = (uint16_t*)h->ws(h->off_act_ffn);
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint8_t* act_ffn = h->ws(h->off_act_ffn);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     if (gemm(h, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
     int splits = 0;
@@ -401,6 +410,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->Hv = c.linear_num_value_heads;
     h->dk = c.linear_key_head_dim;
     h->C = 2 * h->Hk * h->dk + h->Hv * h->dk;
+    h->cus = device_cus();
     h->layer.resize(c.num_layers + 1);
     h->act_h_k = c.mtp ? 2 * h->H : h->H;
 
@@ -416,14 +426,14 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_x = take(Tp * H * 2);
     h->off_hbf = take(Tp * H * 2);
     h->off_tmp = take(Tp * H * 2);
-    h->off_act_h = take(Tp * h->act_h_k * 2);
-    h->off_act_mid = take(Tp * mid * 2);
-    h->off_act_ffn = take(Tp * h->I * 2);
+    h->off_act_h = take(Tp * h->act_h_k);
+    h->off_act_mid = take(Tp * mid);
+    h->off_act_ffn = take(Tp * h->I);
     h->off_z = take(Tp * h->Hv * h->dk * 2);
     h->off_qkv = take(Tp * nqkv * 2);
     h->off_beta = take(Tp * h->Hv * 4);
     h->off_g = take(Tp * h->Hv * 4);
-    h->off_part = take((size_t)SPLIT_MAX * Tp * H * 4);
+    h->off_part = take((size_t)GEMM_SPLIT_MAX * Tp * H * 4);
     h->off_scores = take((size_t)h->B * h->Hkv * 64 * h->S * 4);
     h->off_weights = take((size_t)h->B * h->Hkv * 64 * h->S * 2);
     h->off_htiles = take(Tp * H * 2);
@@ -438,6 +448,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_sp_ids = take(Tp * 4);
     h->off_sp_at = take(Tp * 4);
     h->off_sp_draft = take(Tp * 4);
+    h->off_gemm = take(gemm_scratch_bytes(h->cus));
     h->workspace_bytes = o;
     *out = h;
     return 0;
@@ -460,6 +471,8 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
     if (nbytes != n)
         return fail(std::string("buffer '") + name + "' needs " + std::to_string(n) + " bytes, got " + std::to_string(nbytes));
     if ((uintptr_t)dev_ptr % 16) return fail(std::string("buffer '") + name + "' is not 16-byte aligned");
+    if (layer < 0 && std::string(name) == "workspace")  // the GEMMs' arrival counters start at zero
+        HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 4));
     Buf b;
     b.p = dev_ptr;
     b.n = nbytes;
@@ -479,80 +492,65 @@ int q38_set_parity(q38_handle* h, int parity) {
     return 0;
 }
 
-int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint32_t* scale_words,
+int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint8_t* tile_scales,
                     void* stream) {
-    if (!coded || !scales || !tiles || !scale_words) return fail("null argument");
+    if (!coded || !scales || !tiles || !tile_scales) return fail("null argument");
     if (n <= 0 || k <= 0 || n % 32 || k % 256) return fail("pack needs N % 32 == 0 and K % 256 == 0");
-    HIP_TRY(q38_pack(coded, scales, n, k, tiles, scale_words, (hipStream_t)stream));
+    HIP_TRY(q38_pack(coded, scales, n, k, tiles, tile_scales, (hipStream_t)stream));
     return 0;
 }
 
-int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                   uint16_t* act_scratch, uint16_t* out, void* stream_) {
-    if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
-    if (rows < 1 || n % 256 || k % 256) return fail("fp8_linear needs rows >= 1, N % 256 == 0 and K % 256 == 0");
-    hipStream_t stream = (hipStream_t)stream_;
-    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
+size_t q38_tiles_size(int rows, int k) { return align256((size_t)pad_tokens(rows) * k); }
+
+size_t q38_fp8_linear_scratch(int rows, int k) { return q38_tiles_size(rows, k) + gemm_scratch_bytes(device_cus()); }
+
+namespace {
+
+// One projection outside a handle: e5m2 tiles of x (unless x is null: the scratch already holds them), then the GEMM.
+int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
+               uint8_t* scratch, void* out, int splits_max, hipStream_t stream) {
+    if (!tiles || !tile_scales || !scratch || !out) return fail("null argument");
+    if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+    if (x) HIP_TRY(q38_act_tiles(x, rows, k, scratch, stream));
     GemmArgs a{};
     a.w = tiles;
-    a.ws = scale_words;
-    a.act = act_scratch;
+    a.ws = tile_scales;
+    a.act = scratch;
     a.K = k;
     a.N = n;
     a.T = rows;
     a.Tpad = pad_tokens(rows);
-    a.ksteps = k / 64;
-    a.out0 = out;
-    a.ld0 = n;
-    a.n0 = n;
-    HIP_TRY(q38_gemm(a, EPI_BF16, 1, stream));
+    a.splits_max = splits_max;
+    if (epi == EPI_PARTIAL)
+        a.part = (float*)out;
+    else {
+        a.out0 = out;
+        a.ld0 = n;
+        a.n0 = n;
+    }
+    gemm_scratch(a, scratch + q38_tiles_size(rows, k), device_cus());
+    HIP_TRY(q38_gemm(a, epi, nullptr, stream));
     return 0;
 }
 
-size_t q38_fp8_linear_scratch(int rows, int k) { return (size_t)pad_tokens(rows) * k * 2; }
+}  // namespace
 
-int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int n,
-                       uint16_t* act_scratch, float* out, void* stream_) {
-    if (!x || !tiles || !scale_words || !act_scratch || !out) return fail("null argument");
-    if (rows < 1 || n % 256 || k % 256) return fail("fp8_linear_f32 needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                   uint8_t* scratch, uint16_t* out, void* stream) {
+    return standalone(x, rows, k, tiles, tile_scales, n, EPI_BF16, scratch, out, 0, (hipStream_t)stream);
+}
+
+int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                       uint8_t* scratch, float* out, void* stream) {
     if (pad_tokens(rows) != rows) return fail("fp8_linear_f32 needs rows in {32, 64, 128} or a multiple of 256");
-    hipStream_t stream = (hipStream_t)stream_;
-    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
-    GemmArgs a{};
-    a.w = tiles;
-    a.ws = scale_words;
-    a.act = act_scratch;
-    a.K = k;
-    a.N = n;
-    a.T = rows;
-    a.Tpad = rows;
-    a.ksteps = k / 64;
-    a.part = out;
-    HIP_TRY(q38_gemm(a, EPI_PARTIAL, 1, stream));
-    return 0;
+    return standalone(x, rows, k, tiles, tile_scales, n, EPI_PARTIAL, scratch, out, 1, (hipStream_t)stream);
 }
 
-int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint32_t* scale_words, int inter,
-               uint16_t* act_scratch, uint16_t* out_tiles, void* stream_) {
-    if (!x || !tiles || !scale_words || !act_scratch || !out_tiles) return fail("null argument");
-    if (rows < 1 || (2 * inter) % 256 || inter % 64 || k % 256) return fail("mlp_up needs 2*inter % 256 == 0 and K % 256 == 0");
-    hipStream_t stream = (hipStream_t)stream_;
-    HIP_TRY(q38_act_tiles(x, rows, k, act_scratch, stream));
-    GemmArgs a{};
-    a.w = tiles;
-    a.ws = scale_words;
-    a.act = act_scratch;
-    a.K = k;
-    a.N = 2 * inter;
-    a.T = rows;
-    a.Tpad = pad_tokens(rows);
-    a.ksteps = k / 64;
-    a.out0 = out_tiles;
-    HIP_TRY(q38_gemm(a, EPI_SWIGLU, 1, stream));
-    return 0;
+int q38_mlp_up(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int inter,
+               uint8_t* scratch, uint8_t* out_tiles, void* stream) {
+    if (inter % 64) return fail("mlp_up needs inter % 64 == 0");
+    return standalone(x, rows, k, tiles, tile_scales, 2 * inter, EPI_SWIGLU, scratch, out_tiles, 0, (hipStream_t)stream);
 }
-
-size_t q38_tiles_size(int rows, int k) { return (size_t)pad_tokens(rows) * k * 2; }
 
 int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
                const float* active, const int32_t* accepted, uint16_t* out_hidden, void* stream_) {
@@ -565,7 +563,7 @@ int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const
     const int L = h->cfg.num_layers, rd = h->parity, wr = 1 - h->parity;
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     uint16_t* hbf = is_linear(h, 0) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
-    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, (uint16_t*)h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
     StepIO io{cos, sin, position, active, accepted};
     for (int li = 0; li < L; ++li) {
         if (run_mixer(h, li, io, rd, wr, stream)) return 1;
@@ -587,10 +585,10 @@ int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, 
     auto hn = get<uint16_t>(h, "mtp.hidden_norm", M, &ok);
     auto fin = get<uint16_t>(h, "head.norm", -1, &ok);
     auto fc_t = get<uint8_t>(h, "mtp.fc.tiles", M, &ok);
-    auto fc_s = get<uint32_t>(h, "mtp.fc.scales", M, &ok);
+    auto fc_s = get<uint8_t>(h, "mtp.fc.scales", M, &ok);
     auto in0 = get<uint16_t>(h, "input_layernorm", M, &ok);
     if (!ok) return 1;
-    uint16_t* act_h = (uint16_t*)h->ws(h->off_act_h);
+    uint8_t* act_h = h->ws(h->off_act_h);
     uint16_t* tmp = (uint16_t*)h->ws(h->off_tmp);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     // [rms(embeds) | rms(rms(hidden, final norm), hidden norm)] as the fc's 2H-wide e5m2 input (model.py:845-851).
@@ -614,7 +612,7 @@ int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* ma
     get<uint8_t>(h, "workspace", -1, &ok);
     auto nw = get<uint16_t>(h, "head.norm", -1, &ok);
     auto wt = get<uint8_t>(h, "head.lm_head.tiles", -1, &ok);
-    auto wsc = get<uint32_t>(h, "head.lm_head.scales", -1, &ok);
+    auto wsc = get<uint8_t>(h, "head.lm_head.scales", -1, &ok);
     if (!ok) return 1;
     HIP_TRY(q38_head_norm(hidden, nw, h->cfg.rms_norm_eps, h->H, rows, (bf16_t*)h->ws(h->off_htiles),
                           (float*)h->ws(h->off_x32), stream));
@@ -626,9 +624,9 @@ int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* ma
     a.N = h->V;
     a.T = rows;
     a.Tpad = pad_tokens(rows);
-    a.ksteps = h->H / 64;
     a.part = maxima;
-    HIP_TRY(q38_gemm(a, EPI_GROUPMAX, 1, stream));
+    gemm_scratch(a, h->ws(h->off_gemm), h->cus);
+    HIP_TRY(q38_gemm(a, EPI_GROUPMAX, nullptr, stream));
     return 0;
 }
 
@@ -639,7 +637,7 @@ int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, i
     if (q38_head_groupmax(h, hidden, rows, maxima, stream_)) return 1;
     bool ok = true;
     auto wt = get<uint8_t>(h, "head.lm_head.tiles", -1, &ok);
-    auto wsc = get<uint32_t>(h, "head.lm_head.scales", -1, &ok);
+    auto wsc = get<uint8_t>(h, "head.lm_head.scales", -1, &ok);
     if (!ok) return 1;
     PickArgs a{};
     a.maxima = maxima;

@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
             hv = rbf((half ? nw_hi : nw_lo) * hv);
             float zf = bf2f(a.z[(size_t)tok * Hv * D + h * D + j]);
             float sz = zf * sigmoidf_(zf);
-            a.act[act_offset(tok, h * D + j, Hv * D)] = f2bf(e5m2_round(rbf(hv * sz)));
+            a.act[act_offset(tok, h * D + j, Hv * D)] = (uint8_t)e5m2_byte(rbf(hv * sz));
         }
     }
 }

@@ -2,223 +2,449 @@
 // 32 inputs (the reference's `FP8Linear`, qwen38_inf2/model.py:211-229; its MLP, model.py:250-259; its head,
 // model.py:890-900).
 //
-// Weights stream from HBM as FP8 (1 byte per weight plus 1/32 byte of scale) and are widened in registers to bf16 by
-// v_cvt_scalef32_pk_bf16_fp8, exactly (4 significant bits times a power of two). The products run on the bf16 MFMA,
-// v_mfma_f32_32x32x16_bf16, whose float32 accumulation is as precise as a float32 dot product (measured: about 1e-8 of
-// sum |x w|). The FP8 MFMA, v_mfma_scale_f32_32x32x64_f8f6f4, accumulates internally to only about 2^-14 of that sum,
-// and the reference's activation rounding to e5m2 at every projection input turns such last-bit differences into
-// percent-level divergence within a layer; activations are therefore e5m2-rounded values held as bf16 (exact).
+// Numerics. Weights stream from HBM as FP8 and are widened in registers to bf16 by v_cvt_scalef32_pk_bf16_fp8, exactly
+// (4 significant bits times a power of two); projection activations are e5m2 bytes (the reference rounds every
+// projection input to e5m2) widened exactly by v_cvt_scalef32_pk_bf16_bf8; the head's activations are bf16. Products
+// run on the bf16 MFMA, v_mfma_f32_32x32x16_bf16, whose float32 accumulation is as precise as a float32 dot product
+// (measured: about 1e-8 of sum |x w|). The FP8 MFMA accumulates internally to only about 2^-14 of that sum, and the
+// reference's e5m2 rounding at every projection input turns such last-bit differences into percent-level divergence
+// within a layer, so it is not used.
 //
-// Operands come pre-tiled (common.h), one K-step of 64 inputs at a time; each of the four MFMAs of a K-step takes
-// elements [8m, 8m + 8) of every lane's 32. A workgroup of 4 waves owns (WF*FR*32 features) x (WT*TR*32 tokens) and a
-// range of K-steps; weights go straight from HBM to VGPRs, activations through double-buffered LDS. Epilogues:
+// Data movement. A workgroup owns a (WF*FR*32 features) x (WT*TR*32 tokens) output tile; every K-step of 64 inputs, its
+// weight tiles, their scales and its activation tiles go straight from global memory into one stage of an S-deep LDS
+// ring (global_load_lds, no VGPR staging), S-1 K-steps ahead of the MFMAs. One barrier per K-step: the stage a wave
+// loads into is the one every wave finished reading before that barrier. Weight and activation tiles are both
+// MFMA-step-major (common.h), so every operand read is 8 (or 16) contiguous bytes per lane, free of bank conflicts.
+//
+// Schedule. Workgroups are persistent, one per CU. For outputs that need complete sums the (feature tile, K-step) units
+// are dealt out in equal contiguous ranges (stream-K): a range that ends or starts inside a tile leaves a float32 partial
+// in a slot of `fix`, and the last of the tile's contributors (an arrival counter per tile) adds the partials in K order
+// and runs the epilogue. For EPI_PARTIAL the units are split per tile instead (split-K) and the partials finished by the
+// next row kernel. The token blocks of one workgroup group (same K range) sit on one XCD, so each weight tile is read
+// from HBM once. Epilogues:
 //   EPI_BF16     bf16 store, columns [0, n0) to out0 and [n0, N) to out1 (e.g. in_proj_qkv | in_proj_z)
 //   EPI_SWIGLU   weight tiles interleave gate/up by 32 rows; writes e5m2(bf16(silu(g)) * u) as the down
 //                projection's activation tiles (the chip's fused mlp_up, kernels.py:74-118)
-//   EPI_PARTIAL  float32 partial sums [split][Tpad][N] for split-K; norm.hip finishes them
+//   EPI_PARTIAL  float32 partial sums [split][Tpad][N]
 //   EPI_GROUPMAX largest float32 logit of each 32-row tile per token (the head's group maxima, kernels.py:126-172)
 #include "kernels.h"
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
-template <int WF, int WT, int FR, int TR, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(const GemmArgs a) {
-    constexpr int TT = WT * TR;       // 32-token tiles per workgroup
-    constexpr int STAGE = TT * 4096;  // LDS bytes per K-step of bf16 activations
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+namespace {
+
+// Wait until at most N vector-memory operations of this wave are outstanding, then meet the other waves. The memory
+// clobber keeps the compiler from moving LDS reads across.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Direct global -> LDS load of BYTES per lane: lane l's bytes land at LDS address dst + l * BYTES (dst wave-uniform).
+// Issued as inline assembly, so the compiler neither waits for it before unrelated LDS reads (it cannot tell ring
+// stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the compiler's waits for its own loads only
+// get longer.
+template <int BYTES>
+__device__ __forceinline__ void lds_load(const void* src, uint32_t dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst);
+    if constexpr (BYTES == 16)
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+    else
+        asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+__device__ __forceinline__ uint32_t bits(v2bf v) { return __builtin_bit_cast(uint32_t, v); }
+
+// 8 FP8 e4m3 weights (two words) times 2^(scale byte - 127) as one bf16 MFMA operand. The packed results are used as
+// whole words: element access on them is miscompiled by this hipcc.
+__device__ __forceinline__ v8bf widen_e4m3(uint32_t w0, uint32_t w1, float scale) {
+    u4 r = {bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true))};
+    return __builtin_bit_cast(v8bf, r);
+}
+
+// 8 e5m2 activations (two words) as one bf16 MFMA operand (exact: e5m2 is a subset of bf16).
+__device__ __forceinline__ v8bf widen_e5m2(uint32_t x0, uint32_t x1) {
+    u4 r = {bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(x0, 1.0f, false)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(x0, 1.0f, true)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(x1, 1.0f, false)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(x1, 1.0f, true))};
+    return __builtin_bit_cast(v8bf, r);
+}
+
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI>
+__global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a) {
+    constexpr int NW = WF * WT, NTH = NW * 64;
+    constexpr int TT = WT * TR, FT = WF * FR;  // 32-token and 32-feature tiles per workgroup
+    constexpr int AT = A8 ? 2048 : 4096;       // bytes of one activation tile (32 tokens x 64 inputs)
+    constexpr int ACT_B = TT * AT, W_B = FT * 2048, SC_B = FT * 64;
+    constexpr int STAGE = ACT_B + W_B + SC_B;
+    constexpr int ACT_DMA = ACT_B >= NW * 1024 ? 16 : 4;  // bytes per lane of one activation load
+    constexpr int N_ACT = ACT_B / (NW * 64 * ACT_DMA), N_W = W_B / (NW * 1024), SC_CHUNKS = SC_B / 256;
+    constexpr int OPS = N_ACT + N_W + 1;  // loads per wave per stage
+    static_assert(N_ACT >= 1 && N_ACT * NW * 64 * ACT_DMA == ACT_B, "activation stage splits evenly over the waves");
+    static_assert(N_W >= 1 && N_W * NW * 1024 == W_B, "weight stage splits evenly over the waves");
+    static_assert(SC_CHUNKS >= 1 && NW % SC_CHUNKS == 0, "scale stage splits evenly over the waves");
+    static_assert(OPS * (S - 2) <= 63 && S >= 2, "vmcnt range");
+    static_assert(EPI != EPI_SWIGLU || FR == 2, "gate and up tiles pair up");
+    constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
+    __shared__ int s_arrived;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses stay in scalar registers
     const int wf = wave % WF, wt = wave / WF;
-    // Block order: workgroups are dealt to the 8 XCDs round-robin, so when the feature-tile count allows, the token
-    // tiles of one feature tile get ids 8 apart: same XCD, same L2, launched together, and the weight tile is read
-    // from HBM once.
-    const int nf = a.N / (WF * FR * 32), nt = gridDim.x / nf;
-    int fb, tb;
-    if (nf % 8 == 0) {
-        const int lo = blockIdx.x & 7, rest = blockIdx.x >> 3;
-        tb = rest % nt;
-        fb = (rest / nt) * 8 + lo;
-    } else {
-        fb = blockIdx.x % nf;
-        tb = blockIdx.x / nf;
-    }
-    const int ft0 = fb * (WF * FR) + wf * FR;
-    const int tf0 = tb * TT;
     const int KS = a.K >> 6;
-    const int ks0 = blockIdx.z * a.ksteps, nks = a.ksteps;
+    const int NF = a.N / (FT * 32), NTB = a.Tpad / (TT * 32);
+
+    // Workgroup -> (group, token block). Workgroups are dealt to the 8 XCDs round-robin (workgroup i on XCD i % 8);
+    // when the grid allows, the NTB token blocks of one group get ids 8 apart, so they share an XCD and its L2.
+    const int groups = gridDim.x / NTB;
+    int grp, tb;
+    if (gridDim.x % (8 * NTB) == 0) {
+        const int l = blockIdx.x >> 3;
+        grp = (l / NTB) * 8 + (blockIdx.x & 7);
+        tb = l % NTB;
+    } else {
+        grp = blockIdx.x / NTB;
+        tb = blockIdx.x % NTB;
+    }
+    // Units are (feature tile, K-step) pairs. Split-K: group (fb, z) takes a K range of tile fb. Stream-K: the tiles
+    // fb = x (mod 8) belong to XCD x, and that XCD's groups (grp = 8 gi + x, gi < groups / 8) take equal contiguous
+    // ranges of its units (tile-major), so the contributors of a tile share an L2. Local unit ux is tile
+    // fb = x + 8 (ux / KS), K-step ux % KS.
+    const int xcd = grp & 7, gi = grp >> 3, gx = groups >> 3;
+    const int Ux = ((NF - xcd + 7) >> 3) * KS;
+    int u0, u1, z = 0, fstep = 8, fbase = xcd;
+    if constexpr (EPI == EPI_PARTIAL) {
+        const int fb = grp / a.splits;
+        z = grp % a.splits;
+        u0 = z * KS / a.splits;
+        u1 = (z + 1) * KS / a.splits;
+        fstep = 1;
+        fbase = fb;
+    } else {
+        u0 = (int)((long)gi * Ux / gx);
+        u1 = (int)((long)(gi + 1) * Ux / gx);
+    }
+    const int n = u1 - u0;
+    if (n <= 0) return;
+
+    // Loads of one stage. Each wave moves N_ACT activation chunks, N_W weight chunks of 1 KiB and one scale chunk of
+    // 256 bytes (waves with the same chunk index load identical bytes to the same place).
+    const uint8_t* act_base = (const uint8_t*)a.act + (size_t)tb * TT * KS * AT;
+    const int sc_c = wave % SC_CHUNKS;
+    const uint32_t sc_lane = (uint32_t)((lane >> 4) * KS * 64 + (lane & 15) * 4);
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)LDS_PTR(lds);
+    auto issue = [&](int fb, int k, int st) {
+        const uint32_t sb = lds_addr + st * STAGE;
+#pragma unroll
+        for (int j = 0; j < N_ACT; ++j) {
+            const int off = (j * NW + wave) * (64 * ACT_DMA);
+            const uint8_t* g = act_base + ((size_t)(off / AT) * KS + k) * AT + off % AT;
+            lds_load<ACT_DMA>(g + lane * ACT_DMA, sb + off);
+        }
+#pragma unroll
+        for (int j = 0; j < N_W; ++j) {
+            const int off = (j * NW + wave) * 1024;
+            const uint8_t* g = a.w + ((size_t)(fb * FT + off / 2048) * KS + k) * 2048 + off % 2048;
+            lds_load<16>(g + lane * 16, sb + ACT_B + off);
+        }
+        const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS + k) * 64;
+        lds_load<4>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
+    };
 
     v16f acc[FR][TR];
+    auto zero = [&]() {
 #pragma unroll
-    for (int f = 0; f < FR; ++f)
+        for (int f = 0; f < FR; ++f)
 #pragma unroll
-        for (int t = 0; t < TR; ++t)
+            for (int t = 0; t < TR; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.0f;
+                for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.0f;
+    };
 
-    v4i stage_regs[TT];
-    auto load_act = [&](int ks) {
+    // One K-step: per MFMA step m, each weight fragment and activation fragment is 8 contiguous bytes (16 for bf16
+    // activations) per lane.
+    auto compute = [&](int st) {
+        const uint8_t* sb = lds + st * STAGE;
+        const uint8_t* wl = sb + ACT_B + (wf * FR) * 2048 + lane * 8;
+        const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
+        uint32_t sc[FR];
 #pragma unroll
-        for (int r = 0; r < TT; ++r) {
-            int j = tid + 256 * r, tf = j >> 8, q = j & 255;
-            stage_regs[r] = *(const v4i*)((const uint8_t*)a.act + ((size_t)(tf0 + tf) * KS + ks0 + ks) * 4096 + q * 16);
-        }
-    };
-    auto store_act = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < TT; ++r) {
-            int j = tid + 256 * r, tf = j >> 8, q = j & 255;
-            // Lane q/4 holds 64 bytes; chunk q%4 is MFMA (q%4)'s 8 elements. Chunk-major, so one MFMA's operand read
-            // by a wave is 1 KiB of contiguous LDS.
-            *(v4i*)(lds + buf * STAGE + tf * 4096 + (q & 3) * 1024 + (q >> 2) * 16) = stage_regs[r];
-        }
-    };
-    // Bytes 0-15 of a lane belong to the K-step's first MX block (scale byte in lane half 0), bytes 16-31 to the
-    // second (lane half 1), so each lane reads both scale words. The bytes are extracted only when used: extracting
-    // them at load time would make every K-step wait for the next one's loads.
-    v4i wA[FR][2], wB[FR][2];
-    uint32_t sA[FR][2], sB[FR][2];
-    auto load_w = [&](int ks, v4i (&wr)[FR][2], uint32_t (&sr)[FR][2]) {
-        const int kabs = ks0 + ks;
-#pragma unroll
-        for (int f = 0; f < FR; ++f) {
-            const v4i* p = (const v4i*)(a.w + ((size_t)(ft0 + f) * KS + kabs) * 2048 + lane * 32);
-            wr[f][0] = p[0];
-            wr[f][1] = p[1];
-            const uint32_t* sw = a.ws + ((size_t)(ft0 + f) * (KS >> 2) + (kabs >> 2)) * 64 + (lane & 31);
-            sr[f][0] = sw[0];
-            sr[f][1] = sw[32];
-        }
-    };
-    auto compute = [&](int ks, int buf, v4i (&wr)[FR][2], uint32_t (&sr)[FR][2]) {
-        const int shift = ((ks0 + ks) & 3) * 8;
-        v8bf wb[FR][4];
-#pragma unroll
-        for (int f = 0; f < FR; ++f) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const float scale = __uint_as_float(((sr[f][m >> 1] >> shift) & 0xff) << 23);  // 2^(s - 127)
-                uint32_t w0 = (uint32_t)wr[f][m >> 1][(m & 1) * 2], w1 = (uint32_t)wr[f][m >> 1][(m & 1) * 2 + 1];
-                v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false);
-                v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true);
-                v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false);
-                v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true);
-                wb[f][m] = (v8bf){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-            }
-        }
+        for (int f = 0; f < FR; ++f) sc[f] = *(const uint16_t*)(sl + f * 64);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
+            v8bf wb[FR];
+#pragma unroll
+            for (int f = 0; f < FR; ++f) {
+                // Steps 0-1 are inputs of the K-step's first MX block (scale byte 0), steps 2-3 of its second.
+                const float scale = __uint_as_float((m < 2 ? sc[f] & 0xffu : sc[f] >> 8) << 23);
+                const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
+                wb[f] = widen_e4m3(r[0], r[1], scale);
+            }
 #pragma unroll
             for (int t = 0; t < TR; ++t) {
-                v8bf xb = *(const v8bf*)(lds + buf * STAGE + (wt * TR + t) * 4096 + m * 1024 + lane * 16);
+                v8bf xb;
+                if constexpr (A8) {
+                    const u2 r = *(const u2*)(sb + (wt * TR + t) * 2048 + m * 512 + lane * 8);
+                    xb = widen_e5m2(r[0], r[1]);
+                } else {
+                    xb = *(const v8bf*)(sb + (wt * TR + t) * 4096 + m * 1024 + lane * 16);
+                }
 #pragma unroll
-                for (int f = 0; f < FR; ++f) acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[f][m], xb, acc[f][t], 0, 0, 0);
+                for (int f = 0; f < FR; ++f) acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[f], xb, acc[f][t], 0, 0, 0);
             }
         }
     };
-
-    load_act(0);
-    load_w(0, wA, sA);
-    store_act(0);
-    __syncthreads();
-    for (int ks = 0; ks < nks; ks += 2) {
-        if (ks + 1 < nks) {
-            load_act(ks + 1);
-            load_w(ks + 1, wB, sB);
-        }
-        compute(ks, 0, wA, sA);
-        if (ks + 1 < nks) store_act(1);
-        __syncthreads();
-        if (ks + 1 >= nks) break;
-        if (ks + 2 < nks) {
-            load_act(ks + 2);
-            load_w(ks + 2, wA, sA);
-        }
-        compute(ks + 1, 1, wB, sB);
-        if (ks + 2 < nks) store_act(0);
-        __syncthreads();
-    }
 
     // Accumulator layout of a 32x32 MFMA: lane l holds token column l % 32 and feature rows
     // 8 * (i / 4) + 4 * (l / 32) + i % 4 for i = 0..15.
-    const int rowq = (lane >> 5) * 4;
+    auto epilogue = [&](int fb) {
+        const int rowq = (lane >> 5) * 4;
+        const int ft0 = fb * FT + wf * FR;
 #pragma unroll
-    for (int t = 0; t < TR; ++t) {
-        const int tok = (tf0 + wt * TR + t) * 32 + (lane & 31);
-        if constexpr (EPI == EPI_BF16) {
-            if (tok >= a.T) continue;
+        for (int t = 0; t < TR; ++t) {
+            const int tok = (tb * TT + wt * TR + t) * 32 + (lane & 31);
+            if constexpr (EPI == EPI_BF16) {
+                if (tok >= a.T) continue;
 #pragma unroll
-            for (int f = 0; f < FR; ++f) {
+                for (int f = 0; f < FR; ++f) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = (ft0 + f) * 32 + g * 8 + rowq;
+                        uint32_t lo = (uint32_t)f2bf(acc[f][t][g * 4 + 0]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 1]) << 16);
+                        uint32_t hi = (uint32_t)f2bf(acc[f][t][g * 4 + 2]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 3]) << 16);
+                        bf16_t* dst = col < a.n0 ? (bf16_t*)a.out0 + (size_t)tok * a.ld0 + col
+                                                 : (bf16_t*)a.out1 + (size_t)tok * a.ld1 + (col - a.n0);
+                        *(uint2*)dst = make_uint2(lo, hi);
+                    }
+                }
+            } else if constexpr (EPI == EPI_SWIGLU) {
+                const int inner = a.N >> 1;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    int col = (ft0 + f) * 32 + g * 8 + rowq;
-                    uint32_t lo = (uint32_t)f2bf(acc[f][t][g * 4 + 0]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 1]) << 16);
-                    uint32_t hi = (uint32_t)f2bf(acc[f][t][g * 4 + 2]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 3]) << 16);
-                    bf16_t* dst = col < a.n0 ? (bf16_t*)a.out0 + (size_t)tok * a.ld0 + col
-                                             : (bf16_t*)a.out1 + (size_t)tok * a.ld1 + (col - a.n0);
-                    *(uint2*)dst = make_uint2(lo, hi);
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float gv = rbf(acc[0][t][g * 4 + e]), uv = rbf(acc[1][t][g * 4 + e]);
+                        const float act = rbf(gv * rbf(sigmoidf_(gv)));
+                        packed |= (uint32_t)e5m2_byte(rbf(act * uv)) << (8 * e);
+                    }
+                    const int col = (ft0 >> 1) * 32 + g * 8 + rowq;
+                    *(uint32_t*)((uint8_t*)a.out0 + act_offset(tok, col, inner)) = packed;
+                }
+            } else if constexpr (EPI == EPI_PARTIAL) {
+                float* dst = a.part + ((size_t)z * a.Tpad + tok) * a.N;
+#pragma unroll
+                for (int f = 0; f < FR; ++f)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = (ft0 + f) * 32 + g * 8 + rowq;
+                        *(v4f*)(dst + col) = (v4f){acc[f][t][g * 4 + 0], acc[f][t][g * 4 + 1], acc[f][t][g * 4 + 2],
+                                                   acc[f][t][g * 4 + 3]};
+                    }
+            } else {
+                const int ngroups = a.N >> 5;
+#pragma unroll
+                for (int f = 0; f < FR; ++f) {
+                    float m = acc[f][t][0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) m = fmaxf(m, acc[f][t][i]);
+                    m = fmaxf(m, __shfl_xor(m, 32));
+                    if (lane < 32 && tok < a.T) a.part[(size_t)tok * ngroups + ft0 + f] = m;
                 }
             }
-        } else if constexpr (EPI == EPI_SWIGLU) {
-            static_assert(FR == 2, "gate and up tiles pair up");
-            const int inner = a.N >> 1;
+        }
+    };
+
+    // Stream-K fixup of tile (fb, tb) from a partial range: store this range's sums, count the arrival, and if it was
+    // the last one, add all the tile's partials in K order (contributing groups gi_first..gi_last of this XCD) and
+    // finish the tile. The contributors share this XCD's L2: partials are plain stores (through to L2) completed before
+    // the device-scope arrival count, and the last arrival reads them past its L1 (sc0 buffer loads). Without the
+    // round-robin XCD placement (a.l2_local == 0) the stores are released and the loads acquired at device scope.
+    auto fixup = [&](int fb) {
+        const int t0 = ((fb - xcd) >> 3) * KS;  // first local unit of the tile
+        auto group_of = [&](int u) { return (int)(((long)(u + 1) * gx - 1) / Ux); };
+        auto slot_of = [&](int g) {  // g: group index within the XCD
+            const int start = (int)((long)g * Ux / gx);
+            return ((size_t)((g * 8 + xcd) * NTB + tb) * 2 + (start > t0 ? 0 : 1)) * SLOT;
+        };
+        const int g_first = group_of(t0), g_last = group_of(t0 + KS - 1);
+        v4f* mine = (v4f*)(a.fix + slot_of(gi));
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float v[4];
+        for (int f = 0; f < FR; ++f)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float gv = rbf(acc[0][t][g * 4 + e]), uv = rbf(acc[1][t][g * 4 + e]);
-                    float act = rbf(gv * rbf(sigmoidf_(gv)));
-                    v[e] = e5m2_round(rbf(act * uv));
-                }
-                int col = (ft0 >> 1) * 32 + g * 8 + rowq;
-                *(uint2*)((bf16_t*)a.out0 + act_offset(tok, col, inner)) =
-                    make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16), (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
-            }
-        } else if constexpr (EPI == EPI_PARTIAL) {
-            float* dst = a.part + ((size_t)blockIdx.z * a.Tpad + tok) * a.N;
+            for (int t = 0; t < TR; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    mine[((f * TR + t) * 4 + q) * NTH + tid] =
+                        (v4f){acc[f][t][4 * q], acc[f][t][4 * q + 1], acc[f][t][4 * q + 2], acc[f][t][4 * q + 3]};
+        if (!a.l2_local) __threadfence();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            s_arrived = __hip_atomic_fetch_add(a.counters + fb * NTB + tb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_arrived != g_last - g_first) return;
+        if (!a.l2_local) __threadfence();
+        const __amdgpu_buffer_rsrc_t fix = __builtin_amdgcn_make_buffer_rsrc(a.fix, 0, 0x7fffffff, 0x00020000);
+        for (int g = g_first; g <= g_last; ++g) {
+            const uint32_t base = (uint32_t)(slot_of(g) * 4);
 #pragma unroll
             for (int f = 0; f < FR; ++f)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    int col = (ft0 + f) * 32 + g * 8 + rowq;
-                    *(v4f*)(dst + col) = (v4f){acc[f][t][g * 4 + 0], acc[f][t][g * 4 + 1], acc[f][t][g * 4 + 2], acc[f][t][g * 4 + 3]};
-                }
-        } else {
-            const int groups = a.N >> 5;
+                for (int t = 0; t < TR; ++t)
 #pragma unroll
-            for (int f = 0; f < FR; ++f) {
-                float m = acc[f][t][0];
+                    for (int q = 0; q < 4; ++q) {
+                        const v4f v = __builtin_bit_cast(
+                            v4f, __builtin_amdgcn_raw_buffer_load_b128(fix, base + (((f * TR + t) * 4 + q) * NTH + tid) * 16, 0, 1));
 #pragma unroll
-                for (int i = 1; i < 16; ++i) m = fmaxf(m, acc[f][t][i]);
-                m = fmaxf(m, __shfl_xor(m, 32));
-                if (lane < 32 && tok < a.T) a.part[(size_t)tok * groups + ft0 + f] = m;
-            }
+                        for (int e = 0; e < 4; ++e) acc[f][t][4 * q + e] = g == g_first ? v[e] : acc[f][t][4 * q + e] + v[e];
+                    }
         }
+        epilogue(fb);
+        if (tid == 0) __hip_atomic_store(a.counters + fb * NTB + tb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
+    // Cursors (feature tile, K-step) of the next unit to load and of the unit being computed.
+    int ifb = fbase + fstep * (u0 / KS), ik = u0 % KS;
+    int cfb = ifb, ck = ik;
+    bool partial_start = ik != 0;  // the current tile segment began inside the tile
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+        if (i < n) {
+            issue(ifb, ik, i);
+            if (++ik == KS) ik = 0, ifb += fstep;
+        }
+    zero();
+    int st = 0, ist = S - 1;  // stage computed now, stage loaded next
+    for (int i = 0; i < n; ++i) {
+        if (i + S - 2 < n)
+            wait_and_barrier<OPS*(S - 2)>();
+        else
+            wait_and_barrier<0>();
+        if (i + S - 1 < n) {
+            issue(ifb, ik, ist);
+            if (++ik == KS) ik = 0, ifb += fstep;
+            if (++ist == S) ist = 0;
+        }
+        compute(st);
+        if (++st == S) st = 0;
+        if (ck == KS - 1 || i == n - 1) {
+            if (EPI == EPI_PARTIAL || (!partial_start && ck == KS - 1))
+                epilogue(cfb);
+            else
+                fixup(cfb);
+            zero();
+            partial_start = false;
+        }
+        if (++ck == KS) ck = 0, cfb += fstep;
     }
 }
 
-template <int WF, int WT, int FR, int TR, int EPI>
-static hipError_t launch_gemm(const GemmArgs& a, int splits, hipStream_t stream) {
-    dim3 grid((a.N / (WF * FR * 32)) * (a.Tpad / (WT * TR * 32)), 1, splits);
-    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, EPI>), grid, dim3(256), 0, stream, a);
+constexpr int MIN_UNITS = 8;  // smallest K range worth a stream-K group
+
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI>
+hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
+    GemmArgs a = a0;
+    constexpr int BF = WF * FR * 32, BT = WT * TR * 32, NTH = WF * WT * 64;
+    if (a.N % BF || a.Tpad % BT || a.K % 64 || a.cus < 1) return hipErrorInvalidValue;
+    const int NF = a.N / BF, NTB = a.Tpad / BT, KS = a.K / 64;
+    int grid;
+    if (EPI == EPI_PARTIAL) {
+        int s = a.cus / (NF * NTB);
+        s = s < 1 ? 1 : s;
+        s = s > GEMM_SPLIT_MAX ? GEMM_SPLIT_MAX : s;
+        s = s > KS ? KS : s;
+        if (a.splits_max > 0 && s > a.splits_max) s = a.splits_max;
+        a.splits = s;
+        grid = NF * NTB * s;
+    } else {
+        if ((size_t)NF * NTB > (size_t)a.counters_n) return hipErrorInvalidValue;
+        // Groups: a multiple of 8 (an equal share per XCD), at most one workgroup per CU.
+        long groups = (long)NF * KS / MIN_UNITS;
+        const long most = a.cus / NTB;
+        if (most < 8) return hipErrorInvalidValue;
+        groups = groups > most ? most : groups;
+        groups = groups < 8 ? 8 : groups - groups % 8;
+        grid = (int)groups * NTB;
+        if ((size_t)2 * grid * FR * TR * 16 * NTH > a.fix_floats) return hipErrorInvalidValue;
+        a.splits = 1;
+    }
+    if (splits_out) *splits_out = a.splits;
+    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI>), dim3(grid), dim3(NTH), 0, stream, a);
     return hipGetLastError();
 }
 
-// Shapes are checked by the caller (engine.cpp): N % 256 == 0, K % 256 == 0, Tpad 32, 64 or a multiple of 128,
-// (K / 64) % splits == 0.
-template <int EPI>
-static hipError_t gemm_dispatch(const GemmArgs& a, int splits, hipStream_t stream) {
-    if (a.Tpad >= 128) return launch_gemm<2, 2, 2, 2, EPI>(a, splits, stream);
-    if (a.Tpad == 64) return launch_gemm<4, 1, 2, 2, EPI>(a, splits, stream);
-    return launch_gemm<4, 1, 2, 1, EPI>(a, splits, stream);
+// Tile shape by token count: 256 x 256 outputs per workgroup from 256 tokens up; 512 features x Tpad tokens below,
+// or 256 features when N is not a multiple of 512.
+template <bool A8, int EPI>
+hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
+    constexpr int SB = A8 ? 4 : 3;  // LDS ring depth for the 256 x 256 tile (130 KiB e5m2, 146 KiB bf16)
+    if (a.Tpad % 256 == 0) return launch<4, 2, 2, 4, A8, SB, EPI>(a, splits_out, stream);
+    const bool wide = a.N % 512 == 0;
+    switch (a.Tpad) {
+        case 128:
+            return wide ? launch<8, 1, 2, 4, A8, 3, EPI>(a, splits_out, stream)
+                        : launch<4, 2, 2, 2, A8, 3, EPI>(a, splits_out, stream);
+        case 64:
+            return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI>(a, splits_out, stream)
+                        : launch<4, 2, 2, 1, A8, 4, EPI>(a, splits_out, stream);
+        case 32:
+            return wide ? launch<8, 1, 2, 1, A8, 4, EPI>(a, splits_out, stream)
+                        : launch<4, 1, 2, 1, A8, 4, EPI>(a, splits_out, stream);
+        default:
+            return hipErrorInvalidValue;
+    }
 }
 
-hipError_t q38_gemm(const GemmArgs& a, int epi, int splits, hipStream_t stream) {
+__global__ void xcc_probe_kernel(int* out) {
+    if (threadIdx.x == 0) {
+        uint32_t id;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
+        out[blockIdx.x] = (int)(id & 0xf);
+    }
+}
+
+}  // namespace
+
+// Whether workgroup i of a launch runs on XCD i % 8 on the current device (measured once per device with the
+// XCC_ID hardware register). The stream-K fixup keeps partial sums in one XCD's L2 only when it does.
+int q38_gemm_l2_local() {
+    static int known[64];  // 0 unknown, 1 no, 2 yes
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!known[dev]) {
+        constexpr int n = 64;
+        int* d = nullptr;
+        int h[n];
+        bool ok = hipMalloc(&d, n * sizeof(int)) == hipSuccess;
+        if (ok) {
+            hipLaunchKernelGGL(xcc_probe_kernel, dim3(n), dim3(64), 0, 0, d);
+            ok = hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+            for (int i = 0; ok && i < n; ++i) ok = h[i] == i % 8;
+        }
+        if (d) (void)hipFree(d);
+        (void)hipGetLastError();
+        known[dev] = ok ? 2 : 1;
+    }
+    return known[dev] == 2;
+}
+
+hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream) {
     switch (epi) {
-        case EPI_BF16: return gemm_dispatch<EPI_BF16>(a, splits, stream);
-        case EPI_SWIGLU: return gemm_dispatch<EPI_SWIGLU>(a, splits, stream);
-        case EPI_PARTIAL: return gemm_dispatch<EPI_PARTIAL>(a, splits, stream);
-        default: return gemm_dispatch<EPI_GROUPMAX>(a, splits, stream);
+        case EPI_BF16: return dispatch<true, EPI_BF16>(a, splits_out, stream);
+        case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU>(a, splits_out, stream);
+        case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL>(a, splits_out, stream);
+        case EPI_GROUPMAX: return dispatch<false, EPI_GROUPMAX>(a, splits_out, stream);
+        default: return hipErrorInvalidValue;
     }
 }

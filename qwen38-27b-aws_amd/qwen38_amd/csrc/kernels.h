@@ -5,17 +5,28 @@
 
 enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2, EPI_GROUPMAX = 3 };
 
+constexpr int GEMM_SPLIT_MAX = 32;     // split-K partial buffers (EPI_PARTIAL)
+constexpr int GEMM_COUNTERS = 65536;   // stream-K arrival counters
+constexpr int GEMM_SLOT_FLOATS = 65536;  // floats of one stream-K partial (largest workgroup tile)
+
 struct GemmArgs {
     const uint8_t* w;    // weight tiles [N/32][K/64][64][32] (e4m3)
-    const uint32_t* ws;  // scale words [N/32][K/256][64]: byte j of lane half h's word scales MX block h of K-step 4q+j
-    const bf16_t* act;   // activation tiles [Tpad/32][K/64][64][32] (bf16)
+    const uint8_t* ws;   // scales [N/32][K/64][32][2] (E8M0): row r's bytes for the K-step's two MX blocks
+    const void* act;     // activation tiles [Tpad/32][K/64][4][64][8]: e5m2 bytes, or bf16 for EPI_GROUPMAX
     int K, N, T, Tpad;
-    int ksteps;          // K-steps of 64 per split
     void* out0;
     int ld0, n0;
     void* out1;
     int ld1;
     float* part;         // EPI_PARTIAL: [split][Tpad][N]; EPI_GROUPMAX: maxima [T][N/32]
+    float* fix;          // stream-K partial slots: 2 per workgroup of GEMM_SLOT_FLOATS
+    size_t fix_floats;
+    int* counters;       // stream-K arrival counters, zero between launches (each launch leaves them zero)
+    int counters_n;
+    int cus;             // compute units: one persistent workgroup each
+    int splits_max;      // EPI_PARTIAL: at most this many splits (0: as many as fill the CUs)
+    int l2_local;        // workgroup i runs on XCD i % 8 (q38_gemm_l2_local()): stream-K partials stay in L2
+    int splits;          // EPI_PARTIAL split count (set by the launcher)
 };
 
 struct NormArgs {
@@ -26,7 +37,7 @@ struct NormArgs {
     bf16_t* xout;          // x_new (may alias resid), or null
     const bf16_t* w;       // norm weight, used as (1 + w)
     float eps;
-    bf16_t* act;           // activation tiles (e5m2 values) of width Kact at column act_col0, or null
+    uint8_t* act;          // e5m2 activation tiles of width Kact at column act_col0, or null
     int Kact, act_col0;
     bf16_t* hout;          // bf16 normed rows [T][H], or null
     const bf16_t* div_w;   // MTP tail: hout = bf16(normed / (1 + div_w))
@@ -66,7 +77,7 @@ struct GdnArgs {
     float* delta_new;
     const float* decay_old;  // [B][K][Hv]
     float* decay_new;
-    bf16_t* act;             // activation tiles (e5m2 values) of width Hv*128 for out_proj
+    uint8_t* act;            // e5m2 activation tiles of width Hv*128 for out_proj
     float eps;
 };
 
@@ -84,7 +95,7 @@ struct AttnArgs {
     bf16_t* v_cache;
     float* scores;          // [B*Hkv][64][S]
     bf16_t* weights;        // [B*Hkv][64][S]
-    bf16_t* act;            // activation tiles (e5m2 values) of width Hq*256 for o_proj
+    uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
 };
 
@@ -93,12 +104,13 @@ struct PickArgs {
     int ngroups;
     const float* x32;      // [R][H]
     const uint8_t* w;      // lm_head tiles [V/32][H/64][64][32]
-    const uint32_t* ws;    // lm_head scale words
+    const uint8_t* ws;     // lm_head scales [V/32][H/64][32][2]
     int H, R, groups;
     int* ids;              // [R]
 };
 
-hipError_t q38_gemm(const GemmArgs& a, int epi, int splits, hipStream_t stream);
+hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream);
+int q38_gemm_l2_local();
 hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream);
 hipError_t q38_head_norm(const bf16_t* hidden, const bf16_t* w, float eps, int H, int rows, bf16_t* tiles, float* x32,
                          hipStream_t stream);
@@ -109,9 +121,9 @@ hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream);
 hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream);
 hipError_t q38_accept(const int* picks, const int* drafts, const float* active, int B, int K, int* match, int* accepted,
                       hipStream_t stream);
-hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint32_t* words,
+hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint8_t* tile_scales,
                     hipStream_t stream);
-hipError_t q38_act_tiles(const bf16_t* x, int T, int K, bf16_t* act, hipStream_t stream);
+hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);
 hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
                            hipStream_t s);
 hipError_t q38_select_rows(const bf16_t* rows, const int* idx, int B, int K, int H, bf16_t* out, hipStream_t s);

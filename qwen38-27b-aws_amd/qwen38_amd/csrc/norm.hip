@@ -58,9 +58,8 @@ __global__ __launch_bounds__(256) void residual_norm_kernel(const NormArgs a) {
             *(uint2*)(a.hout + (size_t)t * H + c) =
                 make_uint2((uint32_t)f2bf(h[0]) | ((uint32_t)f2bf(h[1]) << 16), (uint32_t)f2bf(h[2]) | ((uint32_t)f2bf(h[3]) << 16));
         if (a.act)
-            *(uint2*)(a.act + act_offset(t, a.act_col0 + c, a.Kact)) =
-                make_uint2((uint32_t)f2bf(e5m2_round(h[0])) | ((uint32_t)f2bf(e5m2_round(h[1])) << 16),
-                           (uint32_t)f2bf(e5m2_round(h[2])) | ((uint32_t)f2bf(e5m2_round(h[3])) << 16));
+            *(uint32_t*)(a.act + act_offset(t, a.act_col0 + c, a.Kact)) =
+                e5m2_byte(h[0]) | (e5m2_byte(h[1]) << 8) | (e5m2_byte(h[2]) << 16) | (e5m2_byte(h[3]) << 24);
     }
 }
 
@@ -109,18 +108,17 @@ hipError_t q38_embed(const int* ids, int n, const bf16_t* table, int V, int H, b
     return hipGetLastError();
 }
 
-// Activation tiles of bf16 rows [T][K] rounded to e5m2 (the FP8 projection's input rounding, model.py:85-87, 222-225).
-__global__ __launch_bounds__(256) void act_tiles_kernel(const bf16_t* x, int T, int K, bf16_t* act) {
+// e5m2 activation tiles of bf16 rows [T][K] (the FP8 projection's input rounding, model.py:85-87, 222-225).
+__global__ __launch_bounds__(256) void act_tiles_kernel(const bf16_t* x, int T, int K, uint8_t* act) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // group of 4 elements
     if (i >= (size_t)T * K / 4) return;
     const int t = (int)(i / (K / 4)), c = (int)(i % (K / 4)) * 4;
     uint2 r = *(const uint2*)(x + (size_t)t * K + c);
-    *(uint2*)(act + act_offset(t, c, K)) =
-        make_uint2((uint32_t)f2bf(e5m2_round(bf2f(r.x & 0xffff))) | ((uint32_t)f2bf(e5m2_round(bf2f(r.x >> 16))) << 16),
-                   (uint32_t)f2bf(e5m2_round(bf2f(r.y & 0xffff))) | ((uint32_t)f2bf(e5m2_round(bf2f(r.y >> 16))) << 16));
+    *(uint32_t*)(act + act_offset(t, c, K)) = e5m2_byte(bf2f(r.x & 0xffff)) | (e5m2_byte(bf2f(r.x >> 16)) << 8) |
+                                              (e5m2_byte(bf2f(r.y & 0xffff)) << 16) | (e5m2_byte(bf2f(r.y >> 16)) << 24);
 }
 
-hipError_t q38_act_tiles(const bf16_t* x, int T, int K, bf16_t* act, hipStream_t stream) {
+hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream) {
     size_t groups = (size_t)T * K / 4;
     hipLaunchKernelGGL(act_tiles_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream, x, T, K, act);
     return hipGetLastError();

@@ -80,19 +80,22 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
         const int grp = li[0][wave];
         float acc = 0.0f;
         if (grp >= 0 && grp < a.ngroups) {
-            // Lane half h holds inputs [16h, 16h + 16) of the K-step in bytes 0-15 (first MX block, scale byte of
-            // lane half 0) and [32 + 16h, 48 + 16h) in bytes 16-31 (second block, scale byte of lane half 1).
-            const uint8_t* tile = a.w + (size_t)grp * KS * 2048 + lane * 32;
-            const uint32_t* sw = a.ws + (size_t)grp * (KS >> 2) * 64 + (lane & 31);
+            // Lane half h holds inputs [16h, 16h + 16) of the K-step in bytes 0-15 (first MX block) and
+            // [32 + 16h, 48 + 16h) in bytes 16-31 (second block).
+            const uint8_t* tile = a.w + (size_t)grp * KS * 2048 + lane * 8;
+            const uint8_t* sc = a.ws + (size_t)grp * KS * 64 + (lane & 31) * 2;
             const float* xp = xrow + (lane >> 5) * 16;
             for (int ks = 0; ks < KS; ++ks) {
-                const int shift = (ks & 3) * 8;
-                const float s0 = __uint_as_float(((sw[(size_t)(ks >> 2) * 64] >> shift) & 0xff) << 23);
-                const float s1 = __uint_as_float(((sw[(size_t)(ks >> 2) * 64 + 32] >> shift) & 0xff) << 23);
-                const v4i* p = (const v4i*)(tile + (size_t)ks * 2048);
-                v4i lo = p[0], hi = p[1];
-                uint32_t words[8] = {(uint32_t)lo[0], (uint32_t)lo[1], (uint32_t)lo[2], (uint32_t)lo[3],
-                                     (uint32_t)hi[0], (uint32_t)hi[1], (uint32_t)hi[2], (uint32_t)hi[3]};
+                const float s0 = __uint_as_float((uint32_t)sc[(size_t)ks * 64] << 23);
+                const float s1 = __uint_as_float((uint32_t)sc[(size_t)ks * 64 + 1] << 23);
+                // Word w of the lane's 32 bytes: step w / 2 of the tile, at [m][lane][8].
+                uint32_t words[8];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const uint2 r = *(const uint2*)(tile + (size_t)ks * 2048 + m * 512);
+                    words[2 * m] = r.x;
+                    words[2 * m + 1] = r.y;
+                }
 #pragma unroll
                 for (int wi = 0; wi < 8; ++wi) {
                     const float scale = wi < 4 ? s0 : s1;

@@ -169,41 +169,46 @@ class Handle:
 
 
 def pack_weight(coded: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(e4m3 bytes [N, K], E8M0 bytes [N, K/32]) on the GPU -> (tiles, scale words) in the GEMM layout."""
+    """(e4m3 bytes [N, K], E8M0 bytes [N, K/32]) on the GPU -> (tiles, tile scales) in the GEMM layout."""
     n, k = coded.shape
     tiles = torch.empty(n * k, dtype=torch.uint8, device=coded.device)
-    words = torch.empty(n // 32 * (k // 256) * 64, dtype=torch.int32, device=coded.device)
-    check(library().q38_pack_weight(ptr(coded.contiguous()), ptr(scales.contiguous()), n, k, ptr(tiles), ptr(words), stream()))
-    return tiles, words
+    tile_scales = torch.empty(n * k // 32, dtype=torch.uint8, device=coded.device)
+    check(library().q38_pack_weight(ptr(coded.contiguous()), ptr(scales.contiguous()), n, k, ptr(tiles), ptr(tile_scales), stream()))
+    return tiles, tile_scales
 
 
-def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, n: int) -> torch.Tensor:
+def linear_scratch(rows: int, k: int, device="cuda") -> torch.Tensor:
+    """Zero-filled scratch for the standalone projections (input tiles, then the GEMM's counters and partials)."""
+    return torch.zeros(library().q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=device)
+
+
+def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, scratch=None) -> torch.Tensor:
     """`FP8Linear.forward` on the GPU: bf16 x [rows, k] -> bf16 [rows, n] through a packed FP8 weight."""
     rows, k = x.shape
-    lib = library()
-    scratch = torch.empty(lib.q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
+    scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
-    check(lib.q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(words), n, ptr(scratch), ptr(out), stream()))
+    check(library().q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
     return out
 
 
-def fp8_linear_f32(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, n: int) -> torch.Tensor:
+def fp8_linear_f32(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, scratch=None) -> torch.Tensor:
     """The FP8 projection with float32 output (no bf16 rounding): rows in {32, 64, 128} or a multiple of 256."""
     rows, k = x.shape
-    lib = library()
-    scratch = torch.empty(lib.q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
+    scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.float32, device=x.device)
-    check(lib.q38_fp8_linear_f32(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(words), n, ptr(scratch), ptr(out), stream()))
+    check(library().q38_fp8_linear_f32(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
     return out
 
 
-def mlp_up(x: torch.Tensor, tiles: torch.Tensor, words: torch.Tensor, inter: int, scratch=None, out=None) -> torch.Tensor:
-    """The fused gate/up projection with SwiGLU (`mlp_up`): bf16 x [rows, k] -> the down projection's input tiles."""
-    rows, k = x.shape
+def mlp_up(x: torch.Tensor | None, rows: int, k: int, tiles: torch.Tensor, scales: torch.Tensor, inter: int, scratch=None,
+           out=None) -> torch.Tensor:
+    """The fused gate/up projection with SwiGLU (`mlp_up`): bf16 x [rows, k] -> the down projection's e5m2 input tiles.
+    With x None the scratch already holds the input tiles of an earlier call."""
     lib = library()
     if scratch is None:
-        scratch = torch.empty(lib.q38_tiles_size(rows, k), dtype=torch.uint8, device=x.device)
+        scratch = linear_scratch(rows, k)
     if out is None:
-        out = torch.empty(lib.q38_tiles_size(rows, inter), dtype=torch.uint8, device=x.device)
-    check(lib.q38_mlp_up(ptr(x), rows, k, ptr(tiles), ptr(words), inter, ptr(scratch), ptr(out), stream()))
+        out = torch.empty(lib.q38_tiles_size(rows, inter), dtype=torch.uint8, device=scratch.device)
+    xp = None if x is None else ptr(x.contiguous())
+    check(lib.q38_mlp_up(xp, rows, k, ptr(tiles), ptr(scales), inter, ptr(scratch), ptr(out), stream()))
     return out

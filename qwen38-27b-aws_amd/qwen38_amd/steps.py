@@ -81,9 +81,9 @@ class Engine:
     # ------------------------------------------------------------------------------------------------ weights
 
     def _fp8(self, name: str, layer: int, coded: torch.Tensor, scales: torch.Tensor) -> None:
-        tiles, words = ext.pack_weight(coded.to(self.device), scales.to(self.device))
+        tiles, scales_t = ext.pack_weight(coded.to(self.device), scales.to(self.device))
         self.bind(name + ".tiles", layer, tiles)
-        self.bind(name + ".scales", layer, words)
+        self.bind(name + ".scales", layer, scales_t)
 
     def load_layer(self, layer: int, w: dict, kind: str) -> None:
         """One decoder layer's weights by the reference's short names (synth.layer_specs without the prefix)."""
