@@ -86,9 +86,10 @@ struct q38_handle {
     std::map<std::string, Buf> global;
     int parity = 0;
     // workspace carve-up
-    size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_beta, off_g, off_part,
+    size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
         off_scores, off_weights, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
-        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, workspace_bytes;
+        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
+    int gate_groups;  // K ranges of the gated-delta gate projections
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
@@ -251,15 +252,11 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         ga.x = (const bf16_t*)h->ws(h->off_hbf);
         ga.wb = wb;
         ga.wa = wa;
-        ga.a_log = alog;
-        ga.dt_bias = dtb;
-        ga.active = io.active;
         ga.T = h->T;
         ga.H = H;
         ga.Hv = h->Hv;
-        ga.K = h->K;
-        ga.beta = (float*)h->ws(h->off_beta);
-        ga.g = (float*)h->ws(h->off_g);
+        ga.groups = h->gate_groups;
+        ga.part = (float*)h->ws(h->off_gates);
         HIP_TRY(q38_gdn_gates(ga, stream));
         GdnArgs g{};
         g.B = h->B;
@@ -270,8 +267,10 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         g.qkv_new = pin + wr * BKC;
         g.qkv_old = pin + rd * BKC;
         g.z = z;
-        g.beta = ga.beta;
-        g.g = ga.g;
+        g.gate_part = ga.part;
+        g.gate_groups = ga.groups;
+        g.a_log = alog;
+        g.dt_bias = dtb;
         g.conv_w = convw;
         g.norm_w = normw;
         g.position = io.position;
@@ -431,8 +430,9 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_act_ffn = take(Tp * h->I);
     h->off_z = take(Tp * h->Hv * h->dk * 2);
     h->off_qkv = take(Tp * nqkv * 2);
-    h->off_beta = take(Tp * h->Hv * 4);
-    h->off_g = take(Tp * h->Hv * 4);
+    h->gate_groups = 8;
+    while (h->gate_groups > 1 && (h->H % (64 * h->gate_groups) || h->H / (64 * h->gate_groups) > 16)) h->gate_groups /= 2;
+    h->off_gates = take((size_t)h->gate_groups * Tp * 2 * h->Hv * 4);
     h->off_part = take((size_t)GEMM_SPLIT_MAX * Tp * H * 4);
     h->off_scores = take((size_t)h->B * h->Hkv * 64 * h->S * 4);
     h->off_weights = take((size_t)h->B * h->Hkv * 64 * h->S * 2);

@@ -16,64 +16,48 @@
 // `_gates` (model.py:333-337) and the active masks (model.py:411-413): beta = bf16 sigmoid of a bf16 linear, and
 // g = -exp(A_log) * softplus(float(bf16 linear) + dt_bias), both times active. Block: 8 tokens x 16 outputs
 // (output o < Hv is in_proj_b's row o, else in_proj_a's row o - Hv); each wave owns 4 outputs.
+// Beta and decay projections (model.py:145-147): dot products of the bf16 normed hidden rows with the in_proj_b and
+// in_proj_a rows, as partial sums over `groups` K ranges on the bf16 MFMA (float32 accumulation); gdn_verify adds the
+// partials in group order and applies the bf16 rounding, sigmoid and softplus. Workgroup (token tile, output tile,
+// group): 4 waves, each a 32 x 32 tile over H / (4 groups) inputs with all its loads issued up front.
 __global__ __launch_bounds__(256) void gdn_gates_kernel(const GatesArgs a) {
+    constexpr int MAXCH = 16;  // 16-input MFMA steps per wave, at most
+    __shared__ float red[4][16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * 8, o0 = blockIdx.y * 16 + wave * 4;
-    float acc[4][8];
+    const int O = 2 * a.Hv, nto = (O + 31) / 32;
+    const int tt = blockIdx.x / nto, ot = blockIdx.x % nto, grp = blockIdx.y;
+    const int kw = a.H / (4 * a.groups), nch = kw / 16;
+    const int k0 = (grp * 4 + wave) * kw + (lane >> 5) * 8;
+    const int o = min(ot * 32 + (lane & 31), O - 1);
+    const bf16_t* wrow = (o < a.Hv ? a.wb + (size_t)o * a.H : a.wa + (size_t)(o - a.Hv) * a.H) + k0;
+    const bf16_t* xrow = a.x + (size_t)min(tt * 32 + (lane & 31), a.T - 1) * a.H + k0;
+    v4i wv[MAXCH], xv[MAXCH];
 #pragma unroll
-    for (int o = 0; o < 4; ++o)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[o][t] = 0.0f;
-    const bf16_t* wrow[4];
-#pragma unroll
-    for (int o = 0; o < 4; ++o) {
-        int oo = o0 + o;
-        wrow[o] = oo < a.Hv ? a.wb + (size_t)oo * a.H : a.wa + (size_t)(oo - a.Hv) * a.H;
-    }
-    for (int c = lane * 4; c < a.H; c += 256) {
-        float wv[4][4];
-#pragma unroll
-        for (int o = 0; o < 4; ++o) {
-            uint2 r = *(const uint2*)(wrow[o] + c);
-            wv[o][0] = bf2f(r.x & 0xffff);
-            wv[o][1] = bf2f(r.x >> 16);
-            wv[o][2] = bf2f(r.y & 0xffff);
-            wv[o][3] = bf2f(r.y >> 16);
+    for (int c = 0; c < MAXCH; ++c)
+        if (c < nch) {
+            wv[c] = *(const v4i*)(wrow + c * 16);
+            xv[c] = *(const v4i*)(xrow + c * 16);
         }
+    v16f acc;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            int tt = min(t0 + t, a.T - 1);
-            uint2 r = *(const uint2*)(a.x + (size_t)tt * a.H + c);
-            float xv[4] = {bf2f(r.x & 0xffff), bf2f(r.x >> 16), bf2f(r.y & 0xffff), bf2f(r.y >> 16)};
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-            for (int o = 0; o < 4; ++o)
+    for (int c = 0; c < MAXCH; ++c)
+        if (c < nch)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf16, wv[c]), __builtin_bit_cast(v8bf16, xv[c]),
+                                                          acc, 0, 0, 0);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[o][t] += wv[o][e] * xv[e];
-        }
-    }
+    for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (wave) return;
+    // Lane l holds token column l % 32 and output rows 8 * (i / 4) + 4 * (l / 32) + i % 4.
+    const int tok = tt * 32 + (lane & 31);
+    if (tok >= a.T) return;
 #pragma unroll
-    for (int o = 0; o < 4; ++o)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[o][t] = warp_sum(acc[o][t]);
-    if (lane == 0) {
-#pragma unroll
-        for (int o = 0; o < 4; ++o) {
-            int oo = o0 + o;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                int tt = t0 + t;
-                if (tt >= a.T) continue;
-                float on = a.active[tt / a.K];
-                float lin = rbf(acc[o][t]);
-                if (oo < a.Hv) {
-                    a.beta[(size_t)tt * a.Hv + oo] = rbf(sigmoidf_(lin)) * on;
-                } else {
-                    int h = oo - a.Hv;
-                    float decay = -expf(bf2f(a.a_log[h])) * softplusf_(lin + bf2f(a.dt_bias[h]));
-                    a.g[(size_t)tt * a.Hv + h] = decay * on;
-                }
-            }
-        }
+    for (int i = 0; i < 16; ++i) {
+        const int oo = ot * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (oo < O)
+            a.part[((size_t)grp * a.T + tok) * O + oo] = ((red[0][i][lane] + red[1][i][lane]) + red[2][i][lane]) + red[3][i][lane];
     }
 }
 
@@ -96,6 +80,22 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     const bool on = a.active[b] > 0.5f;
     const float keep = (a.position[b] == 0 && on) ? 0.0f : 1.0f;
     const int acc_n = min(max(a.accepted[b], 0), K);
+
+    // This step's gates (model.py:145-147): beta = sigmoid(bf16(x . in_proj_b)), g = -exp(A_log) softplus(bf16(x .
+    // in_proj_a) + dt_bias), both times the row's active flag; the dot products are the gates kernel's partials, added
+    // in group order.
+    __shared__ float s_beta[K], s_g[K];
+    if (tid < 2 * K) {
+        const int t = tid % K, which = tid / K, O = 2 * Hv;
+        const float* p = a.gate_part + ((size_t)b * K + t) * O + (which ? Hv + h : h);
+        float sum = 0.0f;
+        for (int gi = 0; gi < a.gate_groups; ++gi) sum += p[(size_t)gi * a.B * K * O];
+        const float lin = rbf(sum), act = a.active[b];
+        if (which)
+            s_g[t] = -expf(bf2f(a.a_log[h])) * softplusf_(lin + bf2f(a.dt_bias[h])) * act;
+        else
+            s_beta[t] = rbf(sigmoidf_(lin)) * act;
+    }
 
     // Commit coefficients (model.py:386-398): decays of the taken snapshots, the state's scale and each snapshot's
     // weight exp(sum of later decays), all float32 in the reference's order.
@@ -237,8 +237,8 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         float cum[K], beta[K], gl[K], dl[K];
 #pragma unroll
         for (int t = 0; t < K; ++t) {
-            gl[t] = a.g[((size_t)b * K + t) * Hv + h];
-            beta[t] = a.beta[((size_t)b * K + t) * Hv + h];
+            gl[t] = s_g[t];
+            beta[t] = s_beta[t];
             cum[t] = t == 0 ? gl[0] : cum[t - 1] + gl[t];
         }
 #pragma unroll
@@ -288,7 +288,8 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
 }
 
 hipError_t q38_gdn_gates(const GatesArgs& a, hipStream_t stream) {
-    dim3 grid((a.T + 7) / 8, (2 * a.Hv) / 16);
+    if (a.H % (64 * a.groups) || a.H / (64 * a.groups) > 16) return hipErrorInvalidValue;
+    dim3 grid(((a.T + 31) / 32) * ((2 * a.Hv + 31) / 32), a.groups);
     hipLaunchKernelGGL(gdn_gates_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }

@@ -48,12 +48,9 @@ struct GatesArgs {
     const bf16_t* x;       // [T][H] bf16 (the input norm's output)
     const bf16_t* wb;      // in_proj_b [Hv][H]
     const bf16_t* wa;      // in_proj_a [Hv][H]
-    const bf16_t* a_log;   // [Hv]
-    const bf16_t* dt_bias; // [Hv]
-    const float* active;   // [B]
-    int T, H, Hv, K;
-    float* beta;           // [T][Hv]
-    float* g;              // [T][Hv]
+    int T, H, Hv;
+    int groups;            // K ranges (H % (64 * groups) == 0, at most 16 MFMA steps per wave)
+    float* part;           // [groups][T][2 Hv]: x . in_proj_b rows, then x . in_proj_a rows
 };
 
 struct GdnArgs {
@@ -61,8 +58,10 @@ struct GdnArgs {
     const bf16_t* qkv_new;   // [B*K][C]: this step's in_proj_qkv output, also the new pending input snapshot
     const bf16_t* qkv_old;   // [B*K][C]: the last step's (pending_input_state)
     const bf16_t* z;         // [B*K][Hv*128]
-    const float* beta;       // [B*K][Hv]
-    const float* g;          // [B*K][Hv]
+    const float* gate_part;  // [gate_groups][B*K][2 Hv]: partial x . in_proj_b, x . in_proj_a (gates kernel)
+    int gate_groups;
+    const bf16_t* a_log;     // [Hv]
+    const bf16_t* dt_bias;   // [Hv]
     const bf16_t* conv_w;    // [C][4]
     const bf16_t* norm_w;    // [128]
     const int* position;
