@@ -87,7 +87,7 @@ struct q38_handle {
     int parity = 0;
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
-        off_scores, off_weights, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
+        off_scores, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
         off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
     int gate_groups;  // K ranges of the gated-delta gate projections
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
@@ -321,12 +321,12 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         a.k_cache = kc;
         a.v_cache = vc;
         a.scores = (float*)h->ws(h->off_scores);
-        a.weights = (bf16_t*)h->ws(h->off_weights);
         a.act = act_mid;
         a.eps = h->cfg.rms_norm_eps;
         HIP_TRY(q38_attn_verify(a, stream));
         kmid = h->Hq * h->hd;
     }
+    // x += o_proj(mixer): split-K partials, then residual add and the post-mixer norm in one row kernel.
     if (gemm(h, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     auto post = get<uint16_t>(h, "post_attention_layernorm", li, &ok);
     if (!ok) return 1;
@@ -433,9 +433,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->gate_groups = 8;
     while (h->gate_groups > 1 && (h->H % (64 * h->gate_groups) || h->H / (64 * h->gate_groups) > 16)) h->gate_groups /= 2;
     h->off_gates = take((size_t)h->gate_groups * Tp * 2 * h->Hv * 4);
-    h->off_part = take((size_t)GEMM_SPLIT_MAX * Tp * H * 4);
     h->off_scores = take((size_t)h->B * h->Hkv * 64 * h->S * 4);
-    h->off_weights = take((size_t)h->B * h->Hkv * 64 * h->S * 2);
     h->off_htiles = take(Tp * H * 2);
     h->off_x32 = take(Tp * H * 4);
     h->off_maxima = take(Tp * (h->V / 32) * 4);
@@ -449,6 +447,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_sp_at = take(Tp * 4);
     h->off_sp_draft = take(Tp * 4);
     h->off_gemm = take(gemm_scratch_bytes(h->cus));
+    h->off_part = take((size_t)GEMM_SPLIT_MAX * Tp * H * 4);
     h->workspace_bytes = o;
     *out = h;
     return 0;

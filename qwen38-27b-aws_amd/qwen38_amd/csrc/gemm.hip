@@ -384,18 +384,28 @@ hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Tile shape by token count: 256 x 256 outputs per workgroup from 256 tokens up; 512 features x Tpad tokens below,
-// or 256 features when N is not a multiple of 512.
+// Tile shape: 256 tokens per workgroup from 256 tokens up, Tpad tokens below. Features per workgroup: with e5m2
+// activations 128 when N / 128 is a multiple of 8 (an equal share of tiles per XCD; as fast per tile as 256 and twice
+// the tiles), else 256; with bf16 activations (the head) 256, and 512 below 256 tokens when N allows.
 template <bool A8, int EPI>
 hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
-    constexpr int SB = A8 ? 4 : 3;  // LDS ring depth for the 256 x 256 tile (130 KiB e5m2, 146 KiB bf16)
-    if (a.Tpad % 256 == 0) return launch<4, 2, 2, 4, A8, SB, EPI>(a, splits_out, stream);
-    const bool wide = a.N % 512 == 0;
+    auto balanced = [&](int bf) { return a.N % bf == 0 && (a.N / bf) % 8 == 0; };
+    if (a.Tpad % 256 == 0) {
+        if constexpr (A8) {
+            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 5, EPI>(a, splits_out, stream);
+            return launch<4, 2, 2, 4, true, 4, EPI>(a, splits_out, stream);
+        } else {
+            return launch<4, 2, 2, 4, false, 3, EPI>(a, splits_out, stream);
+        }
+    }
+    const bool wide = a.N % 512 == 0 && (balanced(512) || !balanced(256));
     switch (a.Tpad) {
         case 128:
             return wide ? launch<8, 1, 2, 4, A8, 3, EPI>(a, splits_out, stream)
                         : launch<4, 2, 2, 2, A8, 3, EPI>(a, splits_out, stream);
         case 64:
+            if constexpr (A8)
+                if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI>(a, splits_out, stream);
             return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI>(a, splits_out, stream)
                         : launch<4, 2, 2, 1, A8, 4, EPI>(a, splits_out, stream);
         case 32:

@@ -5,7 +5,7 @@
 
 enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2, EPI_GROUPMAX = 3 };
 
-constexpr int GEMM_SPLIT_MAX = 32;     // split-K partial buffers (EPI_PARTIAL)
+constexpr int GEMM_SPLIT_MAX = 8;      // split-K partial buffers (EPI_PARTIAL)
 constexpr int GEMM_COUNTERS = 65536;   // stream-K arrival counters
 constexpr int GEMM_SLOT_FLOATS = 65536;  // floats of one stream-K partial (largest workgroup tile)
 
@@ -93,7 +93,6 @@ struct AttnArgs {
     bf16_t* k_cache;
     bf16_t* v_cache;
     float* scores;          // [B*Hkv][64][S]
-    bf16_t* weights;        // [B*Hkv][64][S]
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
 };

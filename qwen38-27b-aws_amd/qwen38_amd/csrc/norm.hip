@@ -8,63 +8,84 @@
 //   head norm (model.py:890-895, generate.py:196): rms_norm in bf16 for the group max, in float32 for the recheck
 #include "kernels.h"
 
-// One 256-thread block per row; H <= 8192 and H % 256 == 0 (checked by the host).
-__global__ __launch_bounds__(256) void residual_norm_kernel(const NormArgs a) {
-    __shared__ float row[8192];
-    __shared__ float red[4];
+// One workgroup of max(64, H / 8) threads per row (H <= 8192, H % 256 == 0, checked by the host); thread tid owns
+// columns 4 tid + [0, 4) and H / 2 + 4 tid + [0, 4). All of a thread's global loads (every split's partials, the
+// residual, the norm weights) are issued before any arithmetic or store: the partials come from HBM, and a CU reaches
+// its share of HBM bandwidth only with its whole working set in flight.
+__global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
+    __shared__ float red[16];
     const int t = blockIdx.x, tid = threadIdx.x, H = a.H;
+    const bool on = tid * 4 < H / 2;
+    const int col[2] = {tid * 4, H / 2 + tid * 4};
+    v4f p[GEMM_SPLIT_MAX][2];
+    uint2 rr[2], ww[2], dd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        rr[h] = ww[h] = dd[h] = make_uint2(0, 0);
+        if (!on) continue;
+        if (!a.part)
+            rr[h] = *(const uint2*)(a.xin + (size_t)t * H + col[h]);
+        else if (a.resid)
+            rr[h] = *(const uint2*)(a.resid + (size_t)t * H + col[h]);
+        if (a.w) ww[h] = *(const uint2*)(a.w + col[h]);
+        if (a.div_w) dd[h] = *(const uint2*)(a.div_w + col[h]);
+#pragma unroll
+        for (int s = 0; s < GEMM_SPLIT_MAX; ++s)
+            if (a.part && s < a.splits) p[s][h] = *(const v4f*)(a.part + ((size_t)s * a.Tpad + t) * H + col[h]);
+    }
+    float v[2][4];
     float ss = 0.0f;
-    for (int c = tid * 4; c < H; c += 1024) {
-        float v[4];
-        if (a.part) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = 0.0f;
-            for (int s = 0; s < a.splits; ++s) {
-                v4f p = *(const v4f*)(a.part + ((size_t)s * a.Tpad + t) * H + c);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] += p[e];
-            }
-            uint2 r = a.resid ? *(const uint2*)(a.resid + (size_t)t * H + c) : make_uint2(0, 0);
-            bf16_t rb[4] = {(bf16_t)(r.x & 0xffff), (bf16_t)(r.x >> 16), (bf16_t)(r.y & 0xffff), (bf16_t)(r.y >> 16)};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = a.resid ? rbf(bf2f(rb[e]) + rbf(v[e])) : rbf(v[e]);
-        } else {
-            uint2 r = *(const uint2*)(a.xin + (size_t)t * H + c);
-            v[0] = bf2f(r.x & 0xffff);
-            v[1] = bf2f(r.x >> 16);
-            v[2] = bf2f(r.y & 0xffff);
-            v[3] = bf2f(r.y >> 16);
-        }
-        if (a.xout)
-            *(uint2*)(a.xout + (size_t)t * H + c) =
-                make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16), (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
+    for (int h = 0; h < 2; ++h) {
+        const bf16_t rb[4] = {(bf16_t)(rr[h].x & 0xffff), (bf16_t)(rr[h].x >> 16), (bf16_t)(rr[h].y & 0xffff), (bf16_t)(rr[h].y >> 16)};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            row[c + e] = v[e];
-            ss += v[e] * v[e];
+            if (a.part) {
+                float sum = 0.0f;  // split order
+#pragma unroll
+                for (int s = 0; s < GEMM_SPLIT_MAX; ++s)
+                    if (s < a.splits) sum += p[s][h][e];
+                v[h][e] = a.resid ? rbf(bf2f(rb[e]) + rbf(sum)) : rbf(sum);
+            } else {
+                v[h][e] = bf2f(rb[e]);
+            }
+            ss += on ? v[h][e] * v[h][e] : 0.0f;
         }
+        if (on && a.xout)
+            *(uint2*)(a.xout + (size_t)t * H + col[h]) =
+                make_uint2((uint32_t)f2bf(v[h][0]) | ((uint32_t)f2bf(v[h][1]) << 16), (uint32_t)f2bf(v[h][2]) | ((uint32_t)f2bf(v[h][3]) << 16));
     }
     if (!a.act && !a.hout) return;  // residual only (the last layer)
-    ss = block_sum256(ss, red);
-    const float r = 1.0f / sqrtf(ss / (float)H + a.eps);
-    for (int c = tid * 4; c < H; c += 1024) {
-        float h[4];
+    ss = warp_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
+    const float r = 1.0f / sqrtf(tot / (float)H + a.eps);
+    if (!on) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const bf16_t wb[4] = {(bf16_t)(ww[h].x & 0xffff), (bf16_t)(ww[h].x >> 16), (bf16_t)(ww[h].y & 0xffff), (bf16_t)(ww[h].y >> 16)};
+        const bf16_t db[4] = {(bf16_t)(dd[h].x & 0xffff), (bf16_t)(dd[h].x >> 16), (bf16_t)(dd[h].y & 0xffff), (bf16_t)(dd[h].y >> 16)};
+        float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            h[e] = rbf(row[c + e] * r * (1.0f + bf2f(a.w[c + e])));
-            if (a.div_w) h[e] = rbf(h[e] / (1.0f + bf2f(a.div_w[c + e])));
+            o[e] = rbf(v[h][e] * r * (1.0f + bf2f(wb[e])));
+            if (a.div_w) o[e] = rbf(o[e] / (1.0f + bf2f(db[e])));
         }
         if (a.hout)
-            *(uint2*)(a.hout + (size_t)t * H + c) =
-                make_uint2((uint32_t)f2bf(h[0]) | ((uint32_t)f2bf(h[1]) << 16), (uint32_t)f2bf(h[2]) | ((uint32_t)f2bf(h[3]) << 16));
+            *(uint2*)(a.hout + (size_t)t * H + col[h]) =
+                make_uint2((uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16), (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16));
         if (a.act)
-            *(uint32_t*)(a.act + act_offset(t, a.act_col0 + c, a.Kact)) =
-                e5m2_byte(h[0]) | (e5m2_byte(h[1]) << 8) | (e5m2_byte(h[2]) << 16) | (e5m2_byte(h[3]) << 24);
+            *(uint32_t*)(a.act + act_offset(t, a.act_col0 + col[h], a.Kact)) =
+                e5m2_byte(o[0]) | (e5m2_byte(o[1]) << 8) | (e5m2_byte(o[2]) << 16) | (e5m2_byte(o[3]) << 24);
     }
 }
 
 hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(residual_norm_kernel, dim3(a.T), dim3(256), 0, stream, a);
+    if (a.part && (a.splits < 1 || a.splits > GEMM_SPLIT_MAX)) return hipErrorInvalidValue;
+    const int threads = a.H / 8 > 64 ? (a.H / 8 + 63) / 64 * 64 : 64;
+    hipLaunchKernelGGL(residual_norm_kernel, dim3(a.T), dim3(threads), 0, stream, a);
     return hipGetLastError();
 }
 
