@@ -261,7 +261,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_kernel<4,2,2,4,e5m2,4,SWIGLU> (MLP gate/up, 256 x 34816 x 5120)",
+            "kernel": "gemm_kernel<2,4,2,2,e5m2,5,SWIGLU> (MLP gate/up, 256 x 34816 x 5120)",
             "achieved": round(achieved, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
