@@ -470,8 +470,12 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
     if (nbytes != n)
         return fail(std::string("buffer '") + name + "' needs " + std::to_string(n) + " bytes, got " + std::to_string(nbytes));
     if ((uintptr_t)dev_ptr % 16) return fail(std::string("buffer '") + name + "' is not 16-byte aligned");
-    if (layer < 0 && std::string(name) == "workspace")  // the GEMMs' arrival counters start at zero
+    if (layer < 0 && std::string(name) == "workspace") {
+        // The GEMMs' arrival counters start at zero; the one-time XCD placement check (a small allocation) runs
+        // here rather than inside a step.
         HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 4));
+        (void)q38_gemm_l2_local();
+    }
     Buf b;
     b.p = dev_ptr;
     b.n = nbytes;
