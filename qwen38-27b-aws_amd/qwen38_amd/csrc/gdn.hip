@@ -80,16 +80,74 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     const bool on = a.active[b] > 0.5f;
     const float keep = (a.position[b] == 0 && on) ? 0.0f : 1.0f;
     const int acc_n = min(max(a.accepted[b], 0), K);
+    constexpr int GMAX = 8;  // gate groups, at most
+    constexpr int CPT = (3 * D + 255) / 256;  // conv channels per thread
+
+    // Every global load of the block is issued here, before the first store: a load placed after a store would wait
+    // for it (the pointers may alias as far as the compiler knows), and each wait is a memory round trip.
+    float gp[GMAX];
+    if (tid < 2 * K) {
+        const int t = tid % K, which = tid / K, O = 2 * Hv;
+        const float* p = a.gate_part + ((size_t)b * K + t) * O + (which ? Hv + h : h);
+#pragma unroll
+        for (int gi = 0; gi < GMAX; ++gi) gp[gi] = gi < a.gate_groups ? p[(size_t)gi * a.B * K * O] : 0.0f;
+    }
+    float dec_in[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) dec_in[s] = a.decay_old[((size_t)b * K + s) * Hv + h];
+    bf16_t conv_in[CPT][3 + 2 * K + 4];  // old conv state, last step's inputs, this step's inputs, conv weights
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int ci = tid + 256 * u;
+        if (ci >= 3 * D) break;
+        const int grp = ci / D, j = ci % D;
+        const int c = grp == 0 ? kh * D + j : grp == 1 ? Hk * D + kh * D + j : 2 * Hk * D + h * D + j;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) conv_in[u][q] = a.conv_old[((size_t)b * C + c) * 3 + q];
+#pragma unroll
+        for (int s = 0; s < K; ++s) {
+            conv_in[u][3 + s] = a.qkv_old[((size_t)b * K + s) * C + c];
+            conv_in[u][3 + K + s] = a.qkv_new[((size_t)b * K + s) * C + c];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) conv_in[u][3 + 2 * K + q] = a.conv_w[(size_t)c * 4 + q];
+    }
+    constexpr int KPT = (K * D + 255) / 256;  // snapshot key elements per thread
+    float key_in[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+        const int i = tid + 256 * u;
+        key_in[u] = i < K * D ? a.key_old[(((size_t)b * K + i / D) * Hk + kh) * D + i % D] : 0.0f;
+    }
+    const int j0 = lane * 2, i0 = wave * 32;
+    float2 dlt_in[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) dlt_in[s] = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + j0);
+    bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
+    uint32_t sv[32];
+#pragma unroll
+    for (int ii = 0; ii < 32; ++ii) sv[ii] = *(const uint32_t*)(st + (size_t)(i0 + ii) * D + j0);
+    constexpr int ZPW = (K + 3) / 4;  // gated-norm rows per wave
+    bf16_t z_in[ZPW][2];
+#pragma unroll
+    for (int u = 0; u < ZPW; ++u) {
+        const int r = wave + 4 * u;
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+            z_in[u][half] = r < K ? a.z[(size_t)(b * K + r) * Hv * D + h * D + lane + half * 64] : (bf16_t)0;
+    }
+    const float nw_lo = bf2f(a.norm_w[lane]), nw_hi = bf2f(a.norm_w[lane + 64]);
 
     // This step's gates (model.py:145-147): beta = sigmoid(bf16(x . in_proj_b)), g = -exp(A_log) softplus(bf16(x .
     // in_proj_a) + dt_bias), both times the row's active flag; the dot products are the gates kernel's partials, added
     // in group order.
     __shared__ float s_beta[K], s_g[K];
     if (tid < 2 * K) {
-        const int t = tid % K, which = tid / K, O = 2 * Hv;
-        const float* p = a.gate_part + ((size_t)b * K + t) * O + (which ? Hv + h : h);
+        const int t = tid % K, which = tid / K;
         float sum = 0.0f;
-        for (int gi = 0; gi < a.gate_groups; ++gi) sum += p[(size_t)gi * a.B * K * O];
+#pragma unroll
+        for (int gi = 0; gi < GMAX; ++gi)
+            if (gi < a.gate_groups) sum += gp[gi];
         const float lin = rbf(sum), act = a.active[b];
         if (which)
             s_g[t] = -expf(bf2f(a.a_log[h])) * softplusf_(lin + bf2f(a.dt_bias[h])) * act;
@@ -103,7 +161,7 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     float total = 0.0f;
 #pragma unroll
     for (int s = 0; s < K; ++s) {
-        decays[s] = a.decay_old[((size_t)b * K + s) * Hv + h] * (acc_n > s ? 1.0f : 0.0f);
+        decays[s] = dec_in[s] * (acc_n > s ? 1.0f : 0.0f);
         total = total + decays[s];
     }
     const float scale = on ? expf(total) * keep : 1.0f;
@@ -117,16 +175,15 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     }
 
     // Conv history and conv (model.py:399-409). Channel groups: q of key head kh, k of key head kh, v of head h.
-    for (int ci = tid; ci < 3 * D; ci += 256) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const int ci = tid + 256 * u;
+        if (ci >= 3 * D) break;
         const int grp = ci / D, j = ci % D;
         const int c = grp == 0 ? kh * D + j : grp == 1 ? Hk * D + kh * D + j : 2 * Hk * D + h * D + j;
-        const bf16_t* old = a.conv_old + ((size_t)b * C + c) * 3;
         float w_old[3 + K];
-        w_old[0] = bf2f(old[0]);
-        w_old[1] = bf2f(old[1]);
-        w_old[2] = bf2f(old[2]);
 #pragma unroll
-        for (int s = 0; s < K; ++s) w_old[3 + s] = bf2f(a.qkv_old[((size_t)b * K + s) * C + c]);
+        for (int q = 0; q < 3 + K; ++q) w_old[q] = bf2f(conv_in[u][q]);
         float hist[3];
 #pragma unroll
         for (int jj = 0; jj < 3; ++jj) {
@@ -146,9 +203,9 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         win[1] = hist[1];
         win[2] = hist[2];
 #pragma unroll
-        for (int t = 0; t < K; ++t) win[3 + t] = bf2f(a.qkv_new[((size_t)b * K + t) * C + c]);
-        const bf16_t* cw = a.conv_w + (size_t)c * 4;
-        const float w0 = bf2f(cw[0]), w1 = bf2f(cw[1]), w2 = bf2f(cw[2]), w3 = bf2f(cw[3]);
+        for (int t = 0; t < K; ++t) win[3 + t] = bf2f(conv_in[u][3 + K + t]);
+        const float w0 = bf2f(conv_in[u][3 + 2 * K]), w1 = bf2f(conv_in[u][3 + 2 * K + 1]), w2 = bf2f(conv_in[u][3 + 2 * K + 2]),
+                    w3 = bf2f(conv_in[u][3 + 2 * K + 3]);
 #pragma unroll
         for (int t = 0; t < K; ++t) {
             float m = rbf(((rbf(win[t] * w0) + rbf(win[t + 1] * w1)) + rbf(win[t + 2] * w2)) + rbf(win[t + 3] * w3));
@@ -172,12 +229,15 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         }
     }
     // Snapshot keys times their commit weights (model.py:397-398).
-    for (int i = tid; i < K * D; i += 256) {
-        const int s = i / D, j = i % D;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+        const int i = tid + 256 * u;
+        if (i >= K * D) break;
+        const int s = i / D;
         float c = 0.0f;
 #pragma unroll
         for (int r = 0; r < K; ++r) c = s == r ? coef[r] : c;
-        wk[s][j] = a.key_old[(((size_t)b * K + s) * Hk + kh) * D + j] * c;
+        wk[s][i % D] = key_in[u] * c;
     }
     __syncthreads();
 
@@ -192,21 +252,15 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     // State commit and reads (model.py:262-266, 419-429): thread owns columns 2*lane, 2*lane+1 of rows
     // [32*wave, 32*wave+32).
     {
-        const int j0 = lane * 2, i0 = wave * 32;
         float d0[K], d1[K];
 #pragma unroll
         for (int s = 0; s < K; ++s) {
-            const float2 dp = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + j0);
-            d0[s] = dp.x;
-            d1[s] = dp.y;
+            d0[s] = dlt_in[s].x;
+            d1[s] = dlt_in[s].y;
         }
         float p0[2 * K], p1[2 * K];
 #pragma unroll
         for (int r = 0; r < 2 * K; ++r) p0[r] = p1[r] = 0.0f;
-        bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
-        uint32_t sv[32];
-#pragma unroll
-        for (int ii = 0; ii < 32; ++ii) sv[ii] = *(const uint32_t*)(st + (size_t)(i0 + ii) * D + j0);
 #pragma unroll 4
         for (int ii = 0; ii < 32; ++ii) {
             const int i = i0 + ii;
@@ -272,15 +326,17 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         if (lane == 0) rms[t] = 1.0f / sqrtf(ssum / 128.0f + a.eps);
     }
     __syncthreads();
-    const float nw_lo = bf2f(a.norm_w[lane]), nw_hi = bf2f(a.norm_w[lane + 64]);
-    for (int r = wave; r < K; r += 4) {
+#pragma unroll
+    for (int u = 0; u < ZPW; ++u) {
+        const int r = wave + 4 * u;
+        if (r >= K) break;
         const int tok = b * K + r;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const int j = lane + half * 64;
             float hv = rbf(ob[r][j] * rms[r]);
             hv = rbf((half ? nw_hi : nw_lo) * hv);
-            float zf = bf2f(a.z[(size_t)tok * Hv * D + h * D + j]);
+            float zf = bf2f(z_in[u][half]);
             float sz = zf * sigmoidf_(zf);
             a.act[act_offset(tok, h * D + j, Hv * D)] = (uint8_t)e5m2_byte(rbf(hv * sz));
         }
