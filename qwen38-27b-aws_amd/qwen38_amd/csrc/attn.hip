@@ -1,6 +1,6 @@
 // Full attention, multi-token verify form: `FullAttentionStep.verify` with a bf16 cache (reference
-// qwen38_inf2/model.py:641-672, projections and norms model.py:565-577, RoPE model.py:70-82). One workgroup per
-// (row, KV head) holds that head's G query heads x K verify tokens as query rows.
+// qwen38_inf2/model.py:641-672, projections and norms model.py:565-577, RoPE model.py:70-82). The query rows of one
+// (row, KV head) are its G query heads x K verify tokens.
 //
 // Reference arithmetic, kept here: q and k RMS-normed (1 + w) in float32 then bf16; RoPE on the first 64 dims in bf16
 // ops; scores are a bf16 matmul (float32 sums rounded to bf16); cache positions before `position` are visible and the
@@ -8,48 +8,83 @@
 // separate bf16 matmuls added in bf16; times bf16 sigmoid(gate). The masked entries of the reference's full-length
 // softmax contribute exact zeros (exp of about -600 underflows), so only visible positions are read.
 //
+// Two launches, so that every (row, KV head) spreads over several workgroups:
+//   attn_scores (chunk of 512 cached positions, KV head, row): q norm + RoPE, the chunk's scores by MFMA (sixteen
+//       waves, one block of 32 positions each), the chunk's per-row max m_c, probabilities e = exp(s - m_c) (stored as float32) and
+//       their sum s_c. Chunk 0 also normalises and rotates the step's own keys and scores them.
+//   attn_out (quarter of the 256 dims, KV head, row): the row's max M and sum S = sum_c s_c e^(m_c - M) (chunk order)
+//       + own terms; bf16 weights bf16(e * (e^(m_c - M) / S)) formed in registers and multiplied with V by MFMA over
+//       all visible positions (four waves, added in wave order); the own part, the gate, e5m2 activation tiles for
+//       o_proj; then the step's keys and values into the cache. The weights differ from the reference's
+//       bf16(e^(s - M) / S) by a few float32 ulps before the bf16 rounding (the product of two exponentials).
+//
 // Cache layout (this build's): K row-major [B][Hkv][S][256]; V transposed per block of 32 positions,
 // [B][Hkv][S/32][256][32], so both MFMA operands read 16 contiguous bytes per lane:
-//   scores  v_mfma_f32_32x32x16_bf16, A = 32 cached keys x 16 dims, B = 16 dims x 32 query rows
+//   scores  v_mfma_f32_32x32x16_bf16, A = 32 keys x 16 dims, B = 16 dims x 32 query rows
 //   output  v_mfma_f32_32x32x16_bf16, A = 32 query rows x 16 positions (weights), B = 16 positions x 32 dims (V)
-// Scores of a workgroup go through a global scratch (L2-resident at short context) because the bf16 weights need the
-// softmax's final max and sum before any V product; the weights themselves are formed in registers. Loads that feed a
-// phase are issued before that phase's global stores (the pointers may alias as far as the compiler knows).
+// The cache loads of a workgroup are issued first, so their latency overlaps the row-statistics work; loads are issued
+// before global stores (the pointers may alias as far as the compiler knows, and a load issued after a store waits
+// for it).
 #include "kernels.h"
 
-#define ATTN_KMAX 8
-#define ATTN_QMAX 64
 #define QPITCH 264  // bf16 elements per query row in LDS (256 + 8: rows start 4 banks apart)
+#define RPITCH 68   // floats per row of the cross-wave sums in attn_out
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t u4t __attribute__((ext_vector_type(4)));
+
+namespace {
 
 __device__ __forceinline__ v8bf load8(const bf16_t* p) { return *(const v8bf*)p; }
 
+__device__ __forceinline__ int visible(const AttnArgs& a, int b) { return min(max(a.position[b], 0), a.S); }
+
+__device__ __forceinline__ void unpack4(uint2 r, float* v) {
+    v[0] = bf2f(r.x & 0xffff);
+    v[1] = bf2f(r.x >> 16);
+    v[2] = bf2f(r.y & 0xffff);
+    v[3] = bf2f(r.y >> 16);
+}
+
+__device__ __forceinline__ uint2 pack4(const float* v) { return make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])); }
+
+// Row of a 32x32 MFMA accumulator held in element i by `lane` (columns are lane % 32).
+__device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
+
+constexpr int SW = ATTN_CHUNK / 32;  // waves of attn_scores: one block of 32 positions each
+
 template <int QT>
-__global__ __launch_bounds__(256) void attn_verify_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16_t qb[ATTN_QMAX * QPITCH];
-    __shared__ float kown[ATTN_KMAX][256], vown[ATTN_KMAX][256];
-    __shared__ float sown[ATTN_QMAX][ATTN_KMAX];
-    __shared__ float wmax[4][ATTN_QMAX], wsum[4][ATTN_QMAX];
-    __shared__ float mx[ATTN_QMAX], inv[ATTN_QMAX];
+__global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
+    __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];  // own keys (chunk 0)
+    __shared__ float wred[SW][QT * 32], mrow[QT * 32];
 
-    const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
-    const int npos = min(max(a.position[b], 0), S);
-    const int nblk = (npos + 31) >> 5;
+    const int npos = visible(a, b);
+    const int p_lo = c * ATTN_CHUNK, p_hi = min(p_lo + ATTN_CHUNK, npos);
+    const bool first = c == 0;  // also does the step's own keys
+    if (!first && p_lo >= p_hi) return;
     const size_t head = (size_t)b * a.Hkv + kvh;
-    float* sc = a.scores + head * ATTN_QMAX * S;
-    const bf16_t* kc = a.k_cache + head * S * 256;
-    const bf16_t* vc = a.v_cache + head * S * 256;
+    const int blk = (p_lo >> 5) + wave;  // this wave's 32 positions
+    const bool scored = blk * 32 < p_hi;
 
-    // Phase A: normed and rotated q rows (bf16, LDS), own k (normed, rotated) and v. Wave w takes rows w, w + 4, ...;
-    // all its global loads are issued first.
-    constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + 3) / 4;
-    const int nrows = QT * 32 + 2 * K, d0 = lane * 4;
+    // The wave's keys first: lane l holds key l % 32, dims 128 * (l / 32) + 8m .. + 7 in kf[m].
+    v8bf kf[16];
+    if (scored) {
+        const bf16_t* kp = a.k_cache + (head * S + blk * 32 + (lane & 31)) * 256 + (lane >> 5) * 128;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) kf[m] = load8(kp + m * 8);
+    }
+
+    // Phase A: normed and rotated q rows (bf16, LDS); in chunk 0 also the own keys (normed, rotated: LDS as bf16 and
+    // kv_own as float32) and values (kv_own). Wave w takes rows w, w + SW, ...; lane l holds dims 4l .. 4l + 3.
+    constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + SW - 1) / SW;
+    const int nrows = QT * 32 + (first ? 2 * K : 0), d0 = lane * 4;
     uint2 raw[RPW], rc[RPW], rs_[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const int r = wave + 4 * i;
+        const int r = wave + SW * i;
         raw[i] = rc[i] = rs_[i] = make_uint2(0, 0);
         if (r >= nrows || (r >= NQ && r < QT * 32)) continue;
         const bf16_t* src;
@@ -70,146 +105,252 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const AttnArgs a) {
             rs_[i] = *(const uint2*)(a.sin + ((size_t)b * K + t) * 64 + d0);
         }
     }
+    float qn_w[4], kn_w[4];
+    unpack4(*(const uint2*)(a.q_norm + d0), qn_w);
+    unpack4(*(const uint2*)(a.k_norm + d0), kn_w);
+
+    // All rows' sums of squares reduced together (independent shuffle chains), then norm, RoPE and stores.
+    float v[RPW][4], ss[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const int r = wave + 4 * i;
-        if (r >= nrows) break;
-        if (r >= NQ && r < QT * 32) {
-            *(uint2*)(qb + r * QPITCH + d0) = make_uint2(0, 0);
-            continue;
-        }
-        const int kind = r < NQ ? 0 : r < QT * 32 + K ? 1 : 2;
-        const int t = kind == 0 ? r % K : kind == 1 ? r - QT * 32 : r - QT * 32 - K;
-        float v[4] = {bf2f(raw[i].x & 0xffff), bf2f(raw[i].x >> 16), bf2f(raw[i].y & 0xffff), bf2f(raw[i].y >> 16)};
-        if (kind == 2) {
+        unpack4(raw[i], v[i]);
+        ss[i] = v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vown[t][d0 + e] = v[e];
-            continue;
-        }
-        const bf16_t* nw = kind == 0 ? a.q_norm : a.k_norm;
-        float ss = warp_sum(v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3]);
-        const float rsq = 1.0f / sqrtf(ss / 256.0f + a.eps);
-        float hn[4], part[4], out[4];
+    for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hn[e] = rbf(v[e] * rsq * (1.0f + bf2f(nw[d0 + e])));
+        for (int i = 0; i < RPW; ++i) ss[i] += __shfl_xor(ss[i], o);
+    float* kv_own = a.kv_own + head * 2 * ATTN_KMAX * 256;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int r = wave + SW * i;
+        const float* nw = r < QT * 32 ? qn_w : kn_w;
+        const float rsq = 1.0f / sqrtf(ss[i] / 256.0f + a.eps);
+        float hn[4], part[4], cs[4], sn[4], out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hn[e] = rbf(v[i][e] * rsq * (1.0f + nw[e]));
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[e] = __shfl_xor(hn[e], 8);
-        const float cs[4] = {bf2f(rc[i].x & 0xffff), bf2f(rc[i].x >> 16), bf2f(rc[i].y & 0xffff), bf2f(rc[i].y >> 16)};
-        const float sn[4] = {bf2f(rs_[i].x & 0xffff), bf2f(rs_[i].x >> 16), bf2f(rs_[i].y & 0xffff), bf2f(rs_[i].y >> 16)};
+        unpack4(rc[i], cs);
+        unpack4(rs_[i], sn);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int d = d0 + e;
-            if (d < 64) {
-                float rot = d < 32 ? -part[e] : part[e];
-                out[e] = rbf(rbf(hn[e] * cs[e]) + rbf(rot * sn[e]));
-            } else {
-                out[e] = hn[e];
-            }
+            const float rot = d < 32 ? -part[e] : part[e];
+            out[e] = d < 64 ? rbf(rbf(hn[e] * cs[e]) + rbf(rot * sn[e])) : hn[e];
         }
-        if (kind == 0) {
-            *(uint2*)(qb + r * QPITCH + d0) = make_uint2((uint32_t)f2bf(out[0]) | ((uint32_t)f2bf(out[1]) << 16),
-                                                        (uint32_t)f2bf(out[2]) | ((uint32_t)f2bf(out[3]) << 16));
+        if (r < QT * 32) {
+            *(uint2*)(qb + r * QPITCH + d0) = r < NQ ? pack4(out) : make_uint2(0, 0);
+        } else if (r >= nrows) {
+            // rows of own keys and values exist in chunk 0 only
+        } else if (r < QT * 32 + K) {
+            const int t = r - QT * 32;
+            *(uint2*)(kb + t * QPITCH + d0) = pack4(out);
+            *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
         } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) kown[t][d0 + e] = out[e];
+            const int t = r - QT * 32 - K;
+            *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
         }
     }
     __syncthreads();
 
-    // Own scores: query row q = g*K + t sees own tokens t' <= t.
-    for (int p = wave; p < NQ * K; p += 4) {
-        const int q = p / K, tp = p % K, t = q % K;
-        float acc = 0.0f;
+    // Phase B: the wave's block of scores (lane l: query row l % 32 of each 32-row tile, positions acc_row(i, l)).
+    v16f sacc[QT];
+    float lmax[QT];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc += bf2f(qb[q * QPITCH + lane * 4 + e]) * kown[tp][lane * 4 + e];
-        acc = warp_sum(acc);
-        if (lane == 0) sown[q][tp] = tp <= t ? rbf(acc) * 0.0625f : -INFINITY;
-    }
-
-    // Phase B: cached scores by MFMA, blocks of 32 positions spread over the waves.
-    float lmax[2] = {-INFINITY, -INFINITY};
-    {
-        v8bf qf[2][16];
+    for (int qt = 0; qt < QT; ++qt) {
+        lmax[qt] = -INFINITY;
+        if (!scored) continue;
+        const bf16_t* qp = qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128;
+        v16f acc;
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-            if (qt < QT)
+        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-                for (int m = 0; m < 16; ++m) qf[qt][m] = load8(qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128 + m * 8);
-        for (int blk = wave; blk < nblk; blk += 4) {
-            const int p0 = blk * 32;
-            const bf16_t* kp = kc + (size_t)(p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
-            v8bf kf[16];
+        for (int m = 0; m < 16; ++m) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[m], load8(qp + m * 8), acc, 0, 0, 0);
 #pragma unroll
-            for (int m = 0; m < 16; ++m) kf[m] = load8(kp + m * 8);
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                if (qt >= QT) break;
-                v16f acc;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-#pragma unroll
-                for (int m = 0; m < 16; ++m) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[m], qf[qt][m], acc, 0, 0, 0);
-                const int q = qt * 32 + (lane & 31);
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int p = p0 + g * 8 + (lane >> 5) * 4;
-                    v4f s;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        s[e] = p + e < npos ? rbf(acc[g * 4 + e]) * 0.0625f : -INFINITY;
-                        lmax[qt] = fmaxf(lmax[qt], s[e]);
-                    }
-                    *(v4f*)(sc + (size_t)q * S + p) = s;
-                }
-            }
+        for (int i = 0; i < 16; ++i) {
+            acc[i] = blk * 32 + acc_row(i, lane) < p_hi ? rbf(acc[i]) * 0.0625f : -INFINITY;
+            lmax[qt] = fmaxf(lmax[qt], acc[i]);
         }
+        sacc[qt] = acc;
     }
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        float m = fmaxf(lmax[qt], __shfl_xor(lmax[qt], 32));
-        if (lane < 32) wmax[wave][qt * 32 + lane] = m;
-    }
-    __syncthreads();
-    if (tid < ATTN_QMAX) {
-        float m = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
-        if (tid < NQ)
-            for (int tp = 0; tp < K; ++tp) m = fmaxf(m, sown[tid][tp]);
-        mx[tid] = m;
-    }
-    __syncthreads();
 
-    // Phase C: partial sums of exp(s - max), each wave over the blocks it scored (loads only).
-    float lsum[2] = {0.0f, 0.0f};
-    for (int blk = wave; blk < nblk; blk += 4) {
-        const int p0 = blk * 32;
+    // Own scores (chunk 0, last wave): query row q = g*K + t sees own tokens t' <= t. Keys past K read as zero.
+    if (first && wave == SW - 1) {
+        const bool key_row = (lane & 31) < K;
+        v8bf zero;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) zero[e] = (__bf16)0.0f;
+        const bf16_t* kp = kb + min(lane & 31, ATTN_KMAX - 1) * QPITCH + (lane >> 5) * 128;
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
+            const bf16_t* qp = qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128;
+            v16f acc;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 16; ++m)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(key_row ? load8(kp + m * 8) : zero, load8(qp + m * 8), acc,
+                                                              0, 0, 0);
             const int q = qt * 32 + (lane & 31);
-            const float m = mx[q];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const v4f sv = *(const v4f*)(sc + (size_t)q * S + p0 + g * 8 + (lane >> 5) * 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) lsum[qt] += expf(sv[e] - m);
+            for (int i = 0; i < 4; ++i) {  // key rows 0..7
+                const int tp = acc_row(i, lane);
+                if (tp < K && q < NQ)
+                    a.own[(head * ATTN_QMAX + q) * ATTN_KMAX + tp] = tp <= q % K ? rbf(acc[i]) * 0.0625f : -INFINITY;
             }
         }
     }
+
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        float sm = lsum[qt] + __shfl_xor(lsum[qt], 32);
-        if (lane < 32) wsum[wave][qt * 32 + lane] = sm;
+    for (int qt = 0; qt < QT; ++qt) {
+        const float m = fmaxf(lmax[qt], __shfl_xor(lmax[qt], 32));
+        if (lane < 32) wred[wave][qt * 32 + lane] = m;
     }
     __syncthreads();
-    if (tid < ATTN_QMAX) {
-        float sm = (wsum[0][tid] + wsum[1][tid]) + (wsum[2][tid] + wsum[3][tid]);
-        if (tid < NQ)
-            for (int tp = 0; tp < K; ++tp) sm += expf(sown[tid][tp] - mx[tid]);
-        inv[tid] = 1.0f / sm;
+    if (tid < QT * 32) {
+        float m = wred[0][tid];
+#pragma unroll
+        for (int w = 1; w < SW; ++w) m = fmaxf(m, wred[w][tid]);
+        mrow[tid] = m;
     }
     __syncthreads();
 
-    // Phase D: weights x V by MFMA; wave w owns dims [64w, 64w + 64). The bf16 weights, bf16(exp(s - max) / sum), are
-    // formed from the scores as each MFMA needs them; two position blocks' loads are in flight at a time.
+    // Phase C: the chunk's probabilities e = exp(s - m_c) (stored as float32) and their sums.
+    float lsum[QT];
+    float* pr = a.probs + head * ATTN_QMAX * S;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        lsum[qt] = 0.0f;
+        if (!scored) continue;
+        const int q = qt * 32 + (lane & 31);
+        const float m = mrow[q];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const v4f e = {expf(sacc[qt][g * 4] - m), expf(sacc[qt][g * 4 + 1] - m), expf(sacc[qt][g * 4 + 2] - m),
+                           expf(sacc[qt][g * 4 + 3] - m)};
+            lsum[qt] += (e[0] + e[1]) + (e[2] + e[3]);
+            *(v4f*)(pr + (size_t)q * S + blk * 32 + g * 8 + (lane >> 5) * 4) = e;
+        }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float s = lsum[qt] + __shfl_xor(lsum[qt], 32);
+        if (lane < 32) wred[wave][qt * 32 + lane] = s;
+    }
+    __syncthreads();
+    if (tid < QT * 32) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SW; ++w) s += wred[w][tid];
+        float* st = a.stats + ((head * a.nchunks + c) * ATTN_QMAX + tid) * 2;
+        st[0] = mrow[tid];
+        st[1] = mrow[tid] == -INFINITY ? 0.0f : s;
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
+    constexpr int PF = QT == 1 ? 4 : 2;  // blocks of 32 positions whose loads one wave keeps in flight
+    __shared__ float mx[QT * 32], inv[QT * 32];
+    __shared__ float wown[QT * 32][ATTN_KMAX];
+    __shared__ float kq[ATTN_KMAX][64], vq[ATTN_KMAX][64];
+    __shared__ __attribute__((aligned(16))) float red[4][32 * RPITCH];
+
+    // Block -> (quarter, head): the four quarters of one head run on one XCD (they share its probabilities in L2).
+    const int nheads = a.B * a.Hkv, bid = blockIdx.x;
+    int quarter, hh;
+    if (nheads % 8 == 0) {
+        const int l = bid >> 3;
+        quarter = l & 3;
+        hh = (l >> 2) * 8 + (bid & 7);
+    } else {
+        quarter = bid & 3;
+        hh = bid >> 2;
+    }
+    const int b = hh / a.Hkv, kvh = hh % a.Hkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
+    const int npos = visible(a, b), nblk = (npos + 31) >> 5;
+    const size_t head = (size_t)hh;
+    const int dq = quarter * 64;
+    const float* pr = a.probs + head * ATTN_QMAX * S;
+    const float* cmax = a.stats + head * a.nchunks * ATTN_QMAX * 2;
+    const bf16_t* vc = a.v_cache + head * S * 256;
+
+    // V and probability loads of the wave's first blocks (w, w + 4, ...). Lane l: V dims dq + 32 dt + l % 32, positions
+    // 16 (l / 32) .. + 15 of the block; probabilities of query row l % 32 of each tile at the same positions, and that
+    // row's chunk max.
+    v8bf vf[PF][2][2];
+    v4f ef[PF][QT][4];
+    float mc[PF][QT];
+    auto issue = [&](int blk0) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int blk = blk0 + 4 * j;
+            if (blk >= nblk) break;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+                const bf16_t* vp = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
+                vf[j][dt][0] = load8(vp);
+                vf[j][dt][1] = load8(vp + 8);
+            }
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const int q = qt * 32 + (lane & 31);
+                const float* pp = pr + (size_t)q * S + blk * 32 + (lane >> 5) * 16;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) ef[j][qt][g] = *(const v4f*)(pp + 4 * g);
+                mc[j][qt] = cmax[((blk / SW) * ATTN_QMAX + q) * 2];
+            }
+        }
+    };
+    issue(wave);
+
+    // Row statistics, own weights, own keys and values of this quarter, and the gates.
+    if (tid < QT * 32) {
+        const int nch = (npos + ATTN_CHUNK - 1) / ATTN_CHUNK;
+        const float* st = a.stats + head * a.nchunks * ATTN_QMAX * 2 + tid * 2;
+        const float* own = a.own + (head * ATTN_QMAX + tid) * ATTN_KMAX;
+        float so[ATTN_KMAX];
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) so[tp] = tp < K && tid < NQ ? own[tp] : -INFINITY;
+        float m = -INFINITY;
+        for (int c = 0; c < nch; ++c) m = fmaxf(m, st[c * ATTN_QMAX * 2]);
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) m = fmaxf(m, so[tp]);
+        float s = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+            const float sc_ = st[c * ATTN_QMAX * 2 + 1];
+            if (sc_ > 0.0f) s += sc_ * expf(st[c * ATTN_QMAX * 2] - m);
+        }
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp)
+            if (so[tp] > -INFINITY) s += expf(so[tp] - m);
+        const float iv = s > 0.0f ? 1.0f / s : 0.0f;
+        mx[tid] = m;
+        inv[tid] = iv;
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) wown[tid][tp] = so[tp] > -INFINITY ? rbf(expf(so[tp] - m) * iv) : 0.0f;
+    }
+    const float* kv_own = a.kv_own + head * 2 * ATTN_KMAX * 256 + dq;
+    for (int i = tid; i < K * 64; i += 256) {
+        kq[i >> 6][i & 63] = kv_own[(i >> 6) * 256 + (i & 63)];
+        vq[i >> 6][i & 63] = kv_own[(ATTN_KMAX + (i >> 6)) * 256 + (i & 63)];
+    }
+    const int dg = tid & 15;  // finish phase: dims dq + 4 dg .. + 3, rows (tid >> 4) + 16 it of each 32-row tile
+    uint2 gate[QT][2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int q = min(qt * 32 + (tid >> 4) + 16 * it, NQ - 1);
+            gate[qt][it] = *(const uint2*)(a.qkv + (size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 +
+                                           dq + 4 * dg);
+        }
+    __syncthreads();
+
+    // Weights x V over the visible positions.
     v16f acc[QT][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
@@ -223,42 +364,21 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const AttnArgs a) {
         qm[qt] = mx[qt * 32 + (lane & 31)];
         qi[qt] = inv[qt * 32 + (lane & 31)];
     }
-    constexpr int PF = 2;
-    for (int blk0 = 0; blk0 < nblk; blk0 += PF) {
-        v8bf vf[PF][2][2];
-        v4f sf[PF][QT][4];
+    for (int blk0 = wave; blk0 < nblk; blk0 += 4 * PF) {
+        if (blk0 != wave) issue(blk0);
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
-            if (blk0 + j >= nblk) break;
-            const int p0 = (blk0 + j) * 32;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-                const int d = (wave * 2 + dt) * 32 + (lane & 31);
-                const bf16_t* vp = vc + (size_t)(blk0 + j) * 8192 + d * 32 + (lane >> 5) * 16;
-                vf[j][dt][0] = load8(vp);
-                vf[j][dt][1] = load8(vp + 8);
-            }
+            if (blk0 + 4 * j >= nblk) break;
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
-                const float* sp = sc + (size_t)(qt * 32 + (lane & 31)) * S + p0 + (lane >> 5) * 16;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) sf[j][qt][g] = *(const v4f*)(sp + g * 4);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            if (blk0 + j >= nblk) break;
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
+                // bf16(e^(s - m_c) e^(m_c - M) / S): the chunk's probabilities rescaled to the row's softmax.
+                const float f = expf(mc[j][qt] - qm[qt]) * qi[qt];
                 uint32_t wbits[8];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    wbits[2 * g] = (uint32_t)f2bf(expf(sf[j][qt][g][0] - qm[qt]) * qi[qt]) |
-                                   ((uint32_t)f2bf(expf(sf[j][qt][g][1] - qm[qt]) * qi[qt]) << 16);
-                    wbits[2 * g + 1] = (uint32_t)f2bf(expf(sf[j][qt][g][2] - qm[qt]) * qi[qt]) |
-                                       ((uint32_t)f2bf(expf(sf[j][qt][g][3] - qm[qt]) * qi[qt]) << 16);
+                    wbits[2 * g] = pk_bf16(ef[j][qt][g][0] * f, ef[j][qt][g][1] * f);
+                    wbits[2 * g + 1] = pk_bf16(ef[j][qt][g][2] * f, ef[j][qt][g][3] * f);
                 }
-                typedef uint32_t u4t __attribute__((ext_vector_type(4)));
                 const v8bf w0 = __builtin_bit_cast(v8bf, (u4t){wbits[0], wbits[1], wbits[2], wbits[3]});
                 const v8bf w1 = __builtin_bit_cast(v8bf, (u4t){wbits[4], wbits[5], wbits[6], wbits[7]});
 #pragma unroll
@@ -270,56 +390,62 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const AttnArgs a) {
         }
     }
 
-    // Phase E: own part, sum, gate, e5m2 for o_proj. Gate values are loaded before the first store.
+    // Per 32-row tile: the four waves' sums through LDS (lane l holds dim column l % 32 of each 32-dim half and rows
+    // acc_row(i, l)), then own part, gate and e5m2 bytes, four dims per thread.
     const int act_k = a.Hq * 256;
-    float gate[QT][2][16];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-            const int d = (wave * 2 + dt) * 32 + (lane & 31);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int q = min(qt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), NQ - 1);
-                const int tok = b * K + q % K, hq = kvh * G + q / K;
-                gate[qt][dt][i] = bf2f(a.qkv[(size_t)tok * a.ld + (size_t)hq * 512 + 256 + d]);
-            }
-        }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-            const int d = (wave * 2 + dt) * 32 + (lane & 31);
+        for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int q = qt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                if (q >= NQ) continue;
+            for (int i = 0; i < 16; ++i) red[wave][acc_row(i, lane) * RPITCH + dt * 32 + (lane & 31)] = acc[qt][dt][i];
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int row = (tid >> 4) + 16 * it, q = qt * 32 + row;
+            if (q < NQ) {
+                v4f cache = *(const v4f*)&red[0][row * RPITCH + 4 * dg];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) cache += *(const v4f*)&red[w][row * RPITCH + 4 * dg];
+                float gt[4];
+                unpack4(gate[qt][it], gt);
+                uint32_t bytes = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float own = 0.0f;
+                    for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vq[tp][4 * dg + e];
+                    float o = rbf(rbf(cache[e]) + rbf(own));
+                    o = rbf(o * rbf(sigmoidf_(gt[e])));
+                    bytes |= e5m2_byte(o) << (8 * e);
+                }
                 const int g = q / K, t = q % K;
-                float own = 0.0f;
-                for (int tp = 0; tp < K; ++tp) own += rbf(expf(sown[q][tp] - mx[q]) * inv[q]) * vown[tp][d];
-                float o = rbf(rbf(acc[qt][dt][i]) + rbf(own));
-                const int hq = kvh * G + g, tok = b * K + t;
-                o = rbf(o * rbf(sigmoidf_(gate[qt][dt][i])));
-                a.act[act_offset(tok, hq * 256 + d, act_k)] = (uint8_t)e5m2_byte(o);
+                *(uint32_t*)(a.act + act_offset(b * K + t, (kvh * G + g) * 256 + dq + 4 * dg, act_k)) = bytes;
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
 
-    // Phase F: the step's own keys and values into the cache (model.py:603-608, 653-654).
-    for (int i = tid; i < K * 256; i += 256) {
-        const int t = i >> 8, d = i & 255;
-        const int p = a.active[b] > 0.5f ? a.position[b] + t : S - K + t;
+    // The step's own keys and values into the cache (model.py:603-608, 653-654); inactive rows write the tail.
+    const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
+    for (int i = tid; i < K * 64; i += 256) {
+        const int t = i >> 6, d = dq + (i & 63), p = base + t;
         if (p < 0 || p >= S) continue;
-        a.k_cache[(head * S + p) * 256 + d] = f2bf(kown[t][d]);
-        a.v_cache[head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31)] = f2bf(vown[t][d]);
+        a.k_cache[(head * S + p) * 256 + d] = f2bf(kq[t][i & 63]);
+        a.v_cache[head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31)] = f2bf(vq[t][i & 63]);
     }
 }
 
-hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream) {
-    if (a.Hq / a.Hkv * a.K <= 32)
-        hipLaunchKernelGGL(attn_verify_kernel<1>, dim3(a.Hkv, a.B), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(attn_verify_kernel<2>, dim3(a.Hkv, a.B), dim3(256), 0, stream, a);
+template <int QT>
+hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(attn_scores_kernel<QT>, dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+    hipLaunchKernelGGL(attn_out_kernel<QT>, dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream) {
+    const int NQ = a.Hq / a.Hkv * a.K;
+    if (NQ > ATTN_QMAX || a.K > ATTN_KMAX || (long)a.nchunks * ATTN_CHUNK < a.S) return hipErrorInvalidValue;
+    return NQ <= 32 ? launch_attn<1>(a, stream) : launch_attn<2>(a, stream);
 }

@@ -30,12 +30,14 @@ typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// fp32 -> bf16, round to nearest even (c10::BFloat16's rounding); NaN stays NaN.
-__device__ __forceinline__ bf16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+// fp32 -> bf16, round to nearest even (c10::BFloat16's rounding; v_cvt_pk_bf16_f32); NaN stays NaN.
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// Two floats rounded to bf16 and packed, a in the low half (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+    const v2bf p = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, p);
 }
 
 // Round to bf16 and back: the value a torch bf16 op stores.

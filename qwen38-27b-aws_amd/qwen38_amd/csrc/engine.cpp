@@ -87,9 +87,10 @@ struct q38_handle {
     int parity = 0;
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
-        off_scores, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos, off_sp_sin, off_sp_states,
-        off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
+        off_scores, off_astats, off_aown, off_akv, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos,
+        off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
     int gate_groups;  // K ranges of the gated-delta gate projections
+    int attn_nchunks;  // chunks of ATTN_CHUNK cached positions over S
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
@@ -320,7 +321,11 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         a.active = io.active;
         a.k_cache = kc;
         a.v_cache = vc;
-        a.scores = (float*)h->ws(h->off_scores);
+        a.nchunks = h->attn_nchunks;
+        a.probs = (float*)h->ws(h->off_scores);
+        a.stats = (float*)h->ws(h->off_astats);
+        a.own = (float*)h->ws(h->off_aown);
+        a.kv_own = (float*)h->ws(h->off_akv);
         a.act = act_mid;
         a.eps = h->cfg.rms_norm_eps;
         HIP_TRY(q38_attn_verify(a, stream));
@@ -433,7 +438,12 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->gate_groups = 8;
     while (h->gate_groups > 1 && (h->H % (64 * h->gate_groups) || h->H / (64 * h->gate_groups) > 16)) h->gate_groups /= 2;
     h->off_gates = take((size_t)h->gate_groups * Tp * 2 * h->Hv * 4);
-    h->off_scores = take((size_t)h->B * h->Hkv * 64 * h->S * 4);
+    const size_t heads = (size_t)h->B * h->Hkv;
+    h->attn_nchunks = (h->S + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    h->off_scores = take(heads * ATTN_QMAX * h->S * 4);
+    h->off_astats = take(heads * h->attn_nchunks * ATTN_QMAX * 2 * 4);
+    h->off_aown = take(heads * ATTN_QMAX * ATTN_KMAX * 4);
+    h->off_akv = take(heads * 2 * ATTN_KMAX * 256 * 4);
     h->off_htiles = take(Tp * H * 2);
     h->off_x32 = take(Tp * H * 4);
     h->off_maxima = take(Tp * (h->V / 32) * 4);

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
             }
             const float c0 = rbf(bf2f(sv[ii] & 0xffff) * scale + u0);
             const float c1 = rbf(bf2f(sv[ii] >> 16) * scale + u1);
-            *(uint32_t*)(st + (size_t)i * D + j0) = (uint32_t)f2bf(c0) | ((uint32_t)f2bf(c1) << 16);
+            *(uint32_t*)(st + (size_t)i * D + j0) = pk_bf16(c0, c1);
 #pragma unroll
             for (int r = 0; r < 2 * K; ++r) {
                 const float rv = r < K ? kn[r][i] : qn[r - K][i];

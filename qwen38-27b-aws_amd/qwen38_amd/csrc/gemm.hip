@@ -220,8 +220,8 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int col = (ft0 + f) * 32 + g * 8 + rowq;
-                        uint32_t lo = (uint32_t)f2bf(acc[f][t][g * 4 + 0]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 1]) << 16);
-                        uint32_t hi = (uint32_t)f2bf(acc[f][t][g * 4 + 2]) | ((uint32_t)f2bf(acc[f][t][g * 4 + 3]) << 16);
+                        uint32_t lo = pk_bf16(acc[f][t][g * 4 + 0], acc[f][t][g * 4 + 1]);
+                        uint32_t hi = pk_bf16(acc[f][t][g * 4 + 2], acc[f][t][g * 4 + 3]);
                         bf16_t* dst = col < a.n0 ? (bf16_t*)a.out0 + (size_t)tok * a.ld0 + col
                                                  : (bf16_t*)a.out1 + (size_t)tok * a.ld1 + (col - a.n0);
                         *(uint2*)dst = make_uint2(lo, hi);

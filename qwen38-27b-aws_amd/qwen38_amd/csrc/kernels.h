@@ -80,6 +80,10 @@ struct GdnArgs {
     float eps;
 };
 
+#define ATTN_KMAX 8   // verify tokens
+#define ATTN_QMAX 64  // query rows per KV head
+#define ATTN_CHUNK 512  // cached positions per attn_scores workgroup (32 per wave)
+
 struct AttnArgs {
     int B, K, Hq, Hkv, S;
     const bf16_t* qkv;      // [B*K][ld]: per query head [q 256 | gate 256], then k [Hkv][256], then v [Hkv][256]
@@ -92,7 +96,11 @@ struct AttnArgs {
     const float* active;
     bf16_t* k_cache;
     bf16_t* v_cache;
-    float* scores;          // [B*Hkv][64][S]
+    int nchunks;            // chunks of ATTN_CHUNK cached positions over S
+    float* probs;           // [B*Hkv][ATTN_QMAX][S]: exp(score - chunk max)
+    float* stats;           // [B*Hkv][nchunks][ATTN_QMAX][2]: per chunk, max and sum of exp(score - max)
+    float* own;             // [B*Hkv][ATTN_QMAX][ATTN_KMAX]: scores of the step's own keys (-inf where masked)
+    float* kv_own;          // [B*Hkv][2][ATTN_KMAX][256]: the step's keys (normed, rotated) and values
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
 };

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
         }
         if (on && a.xout)
             *(uint2*)(a.xout + (size_t)t * H + col[h]) =
-                make_uint2((uint32_t)f2bf(v[h][0]) | ((uint32_t)f2bf(v[h][1]) << 16), (uint32_t)f2bf(v[h][2]) | ((uint32_t)f2bf(v[h][3]) << 16));
+                make_uint2(pk_bf16(v[h][0], v[h][1]), pk_bf16(v[h][2], v[h][3]));
     }
     if (!a.act && !a.hout) return;  // residual only (the last layer)
     ss = warp_sum(ss);
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
         }
         if (a.hout)
             *(uint2*)(a.hout + (size_t)t * H + col[h]) =
-                make_uint2((uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16), (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16));
+                make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
         if (a.act)
             *(uint32_t*)(a.act + act_offset(t, a.act_col0 + col[h], a.Kact)) =
                 e5m2_byte(o[0]) | (e5m2_byte(o[1]) << 8) | (e5m2_byte(o[2]) << 16) | (e5m2_byte(o[3]) << 24);

@@ -1,0 +1,78 @@
+"""Full attention at long contexts, through the MTP step (one fc + full-attention layer + norm) against the oracle.
+
+The golden scenario's contexts fit in one chunk of cached positions; these cases spread each (row, KV head) over many
+chunks (the tiny block at 2048 positions: 16 chunks of 128), take the 64-query-row path (16 query heads over 2 KV
+heads, 8 tokens), and include an empty cache and an inactive row (which writes the cache tail). Checked: the MTP output
+(one layer, so the north-star 2e-2 per-row bound without a floor factor), the positions the step writes in both caches
+(1e-2: the keys are normed and rotated in bf16 by both sides), and every other cache position unchanged.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import pytest
+import torch
+
+from oracle import model as om
+from qwen38_amd import synth
+from qwen38_amd.config import tiny_config
+from qwen38_amd.generate import mtp_step_inputs
+from qwen38_amd.steps import Engine, MTPStep
+from scenario import oracle_weights
+
+CASES = {
+    # name: (query heads, batch, tokens, max_seq_len, contexts, active)
+    "tiny-2048-16chunks": (8, 4, 4, 2048, [1900, 700, 0, 1500], [True, True, True, False]),
+    "64rows-1024": (16, 2, 8, 1024, [1000, 333], [True, True]),
+    "tail-edge": (8, 2, 4, 512, [507, 511], [True, False]),
+}
+
+
+def row_rel(got: torch.Tensor, want: torch.Tensor) -> float:
+    got, want = got.float().cpu(), want.float().cpu()
+    worst = 0.0
+    for r in range(want.shape[0]):
+        n = float(want[r].norm())
+        worst = max(worst, float((got[r] - want[r]).norm()) / max(n, 1e-30))
+    return worst
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", list(CASES))
+def test_mtp_attention_at_long_context_matches_the_oracle(gpu, case):
+    hq, b, k, s, context, active = CASES[case]
+    print(f"case {case}", flush=True)
+    cfg = dataclasses.replace(tiny_config(1), num_attention_heads=hq)
+    seed = 11
+    values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg), seed))
+    _, mtp_w, _ = oracle_weights(values, cfg)
+    engine = Engine(cfg, b, k, s, mtp=True)
+    engine.load(values.items())
+    mst = synth.kv_states(cfg, b, s, context, seed, "mtp")
+    engine.set_kv(engine.mtp_layer, mst["k_cache"], mst["v_cache"])
+    before = {key: v.clone() for key, v in mst.items()}
+
+    # Positions: each row's context (the step's own tokens go right after it; an inactive row's go to the tail).
+    mi = mtp_step_inputs(cfg, context, k, s, torch.bfloat16, active)
+    mi["position"] = torch.as_tensor(context, dtype=torch.int32)
+    hidden = synth.hidden_states((b, k, cfg.hidden_size), seed, "attn.hidden")
+    ids = torch.randint(0, cfg.vocab_size, (b, k), generator=torch.Generator().manual_seed(seed))
+    embeds = values["embed_tokens"][ids]
+
+    out = MTPStep(engine)(hidden=hidden, inputs_embeds=embeds, **mi)
+    torch.cuda.synchronize()
+    want = om.mtp_forward(cfg, mtp_w, mst, hidden, embeds, mi["cos"], mi["sin"], mi["position"], mi["active"])
+    err = row_rel(out, want)
+    print(f"mtp_out row_rel {err:.3g}", flush=True)
+    assert err <= 2e-2
+
+    kc, vc = engine.get_kv(engine.mtp_layer)
+    for name, got in (("k_cache", kc.cpu()), ("v_cache", vc.cpu())):
+        for row in range(b):
+            start = context[row] if active[row] else s - k
+            own = slice(start, start + k)
+            assert row_rel(got[row, :, own].transpose(0, 1), mst[name][row, :, own].transpose(0, 1)) <= 1e-2, (name, row)
+            keep = torch.ones(s, dtype=torch.bool)
+            keep[own] = False
+            assert torch.equal(got[row, :, keep], before[name][row, :, keep]), (name, row)

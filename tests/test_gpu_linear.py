@@ -69,3 +69,22 @@ def test_fp8_linear_matches_the_oracle_within_rounding_and_accumulation_error(gp
     err = (got.double() - exact).abs()
     assert (err <= 0.5 * bf16_ulp(exact) + 2.0**-20 * abs_sum).all(), float((err / abs_sum).max())
     assert (got.float() == want.float()).float().mean() > 0.999
+
+
+@pytest.mark.gpu
+def test_bf16_outputs_round_to_nearest_even_like_torch(gpu):
+    """Only the first 64 inputs nonzero (one MFMA block: every split of the sum adds exact zeros, so the bf16 and
+    float32 outputs come from the same float32 sums): the bf16 output must be torch's round-to-nearest-even of the
+    float32 output. Products of e5m2 and e4m3 values have at most 7 significant bits, so many sums fall exactly halfway
+    between two bf16 values and the ties are exercised."""
+    g = torch.Generator().manual_seed(3)
+    n, k, rows = 512, 256, 256
+    coded, scales = quantize_e4m3(torch.randn(n, k, generator=g))
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    x[:, 64:] = 0
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    f32 = ext.fp8_linear_f32(x.cuda(), tiles, words, n).cpu()
+    bf = ext.fp8_linear(x.cuda(), tiles, words, n).cpu()
+    ties = (f32.view(torch.int32) & 0xFFFF) == 0x8000
+    assert int(ties.sum()) > 100
+    assert torch.equal(bf.view(torch.int16), f32.to(torch.bfloat16).view(torch.int16))
