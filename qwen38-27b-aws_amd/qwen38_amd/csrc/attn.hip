@@ -409,15 +409,15 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
                 for (int w = 1; w < 4; ++w) cache += *(const v4f*)&red[w][row * RPITCH + 4 * dg];
                 float gt[4];
                 unpack4(gate[qt][it], gt);
-                uint32_t bytes = 0;
+                float o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float own = 0.0f;
                     for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vq[tp][4 * dg + e];
-                    float o = rbf(rbf(cache[e]) + rbf(own));
-                    o = rbf(o * rbf(sigmoidf_(gt[e])));
-                    bytes |= e5m2_byte(o) << (8 * e);
+                    o[e] = rbf(rbf(cache[e]) + rbf(own));
+                    o[e] = rbf(o[e] * rbf(sigmoidf_(gt[e])));
                 }
+                const uint32_t bytes = pk_e5m2(o[0], o[1], o[2], o[3]);
                 const int g = q / K, t = q % K;
                 *(uint32_t*)(a.act + act_offset(b * K + t, (kvh * G + g) * 256 + dq + 4 * dg, act_k)) = bytes;
             }

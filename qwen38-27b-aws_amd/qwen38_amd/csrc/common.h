@@ -43,21 +43,8 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
 // Round to bf16 and back: the value a torch bf16 op stores.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
-// x rounded to FP8 e5m2 and back (torch's cast: round to nearest even, past 57344 to infinity), as a float.
-__device__ __forceinline__ float e5m2_round(float x) {
-    uint32_t u = __float_as_uint(x);
-    uint32_t s = u & 0x80000000u;
-    uint32_t a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return x;
-    if (a >= 0x38800000u) {  // |x| >= 2^-14: normal e5m2, keep 2 mantissa bits
-        uint32_t r = (a + 0xfffffu + ((a >> 21) & 1u)) & ~0x1fffffu;
-        return __uint_as_float(s | (r > 0x47600000u ? 0x7f800000u : r));
-    }
-    // Subnormal e5m2: multiples of 2^-16.
-    return __uint_as_float(s | __float_as_uint(__builtin_rintf(__uint_as_float(a) * 65536.0f) * (1.0f / 65536.0f)));
-}
-
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of a correctly rounded division.
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + expf(-x)); }
 
 // torch.nn.functional.softplus with beta 1, threshold 20.
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
@@ -75,14 +62,15 @@ Q38_HOST_DEVICE size_t act_offset(int t, int k, int K) {
            (size_t)((e >> 3) * 512 + ((t & 31) + kstep_half(k) * 32) * 8 + (e & 7));
 }
 
-// The FP8 e5m2 byte of x rounded to e5m2 (e5m2_round): sign, 5 exponent bits (bias 15), 2 mantissa bits.
-__device__ __forceinline__ uint32_t e5m2_byte(float x) {
-    const uint32_t u = __float_as_uint(e5m2_round(x));
-    const uint32_t s = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return s | 0x7eu;  // NaN
-    if (a == 0x7f800000u) return s | 0x7cu;
-    if (a >= 0x38800000u) return s | ((a >> 21) - (112u << 2));  // normal: exponent rebiased from 127 to 15
-    return s | (uint32_t)(__uint_as_float(a) * 65536.0f);        // subnormal: m * 2^-16, m in 0..3
+// FP8 e5m2 bytes of floats rounded as torch's cast to float8_e5m2 does (round to nearest even, past 57344 to
+// infinity; NaN stays NaN): v_cvt_pk_bf8_f32, which agrees with that rounding bit for bit on every bf16 value (all
+// values converted here are bf16) and on random float32 values, NaN payloads aside.
+__device__ __forceinline__ uint32_t e5m2_byte(float x) { return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(x, x, 0, false) & 0xffu; }
+
+// Four e5m2 bytes packed into a word, a in the lowest byte.
+__device__ __forceinline__ uint32_t pk_e5m2(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, lo, true);
 }
 
 __device__ __forceinline__ float warp_sum(float v) {

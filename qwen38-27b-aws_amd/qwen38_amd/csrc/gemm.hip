@@ -231,13 +231,14 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                 const int inner = a.N >> 1;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    uint32_t packed = 0;
+                    float h[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float gv = rbf(acc[0][t][g * 4 + e]), uv = rbf(acc[1][t][g * 4 + e]);
                         const float act = rbf(gv * rbf(sigmoidf_(gv)));
-                        packed |= (uint32_t)e5m2_byte(rbf(act * uv)) << (8 * e);
+                        h[e] = rbf(act * uv);
                     }
+                    const uint32_t packed = pk_e5m2(h[0], h[1], h[2], h[3]);
                     const int col = (ft0 >> 1) * 32 + g * 8 + rowq;
                     *(uint32_t*)((uint8_t*)a.out0 + act_offset(tok, col, inner)) = packed;
                 }
@@ -265,11 +266,12 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
         }
     };
 
-    // Stream-K fixup of tile (fb, tb) from a partial range: store this range's sums, count the arrival, and if it was
-    // the last one, add all the tile's partials in K order (contributing groups gi_first..gi_last of this XCD) and
-    // finish the tile. The contributors share this XCD's L2: partials are plain stores (through to L2) completed before
-    // the device-scope arrival count, and the last arrival reads them past its L1 (sc0 buffer loads). Without the
-    // round-robin XCD placement (a.l2_local == 0) the stores are released and the loads acquired at device scope.
+    // Stream-K fixup of tile (fb, tb) from a partial range. The contributors (groups g_first..g_last of this XCD, in K
+    // order) share the XCD's L2: a partial is plain stores (through to L2) completed before a device-scope arrival
+    // count, and the last arrival reads the others past its L1 (sc0 buffer loads), adds all partials in K order and
+    // finishes the tile. Fast path: the tile's first contributor, finding every other partial already counted, adds
+    // them to its own sums without storing them (the same additions in the same order). Without the round-robin XCD
+    // placement (a.l2_local == 0) the stores are released and the loads acquired at device scope.
     auto fixup = [&](int fb) {
         const int t0 = ((fb - xcd) >> 3) * KS;  // first local unit of the tile
         auto group_of = [&](int u) { return (int)(((long)(u + 1) * gx - 1) / Ux); };
@@ -278,25 +280,35 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             return ((size_t)((g * 8 + xcd) * NTB + tb) * 2 + (start > t0 ? 0 : 1)) * SLOT;
         };
         const int g_first = group_of(t0), g_last = group_of(t0 + KS - 1);
-        v4f* mine = (v4f*)(a.fix + slot_of(gi));
+        int* const counter = a.counters + fb * NTB + tb;
+        bool fast = false;
+        if (gi == g_first) {
+            if (tid == 0) s_arrived = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            fast = s_arrived == g_last - g_first;
+            __syncthreads();  // s_arrived is read by every thread before it is written again
+        }
+        if (!fast) {
+            v4f* mine = (v4f*)(a.fix + slot_of(gi));
 #pragma unroll
-        for (int f = 0; f < FR; ++f)
+            for (int f = 0; f < FR; ++f)
 #pragma unroll
-            for (int t = 0; t < TR; ++t)
+                for (int t = 0; t < TR; ++t)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    mine[((f * TR + t) * 4 + q) * NTH + tid] =
-                        (v4f){acc[f][t][4 * q], acc[f][t][4 * q + 1], acc[f][t][4 * q + 2], acc[f][t][4 * q + 3]};
+                    for (int q = 0; q < 4; ++q)
+                        mine[((f * TR + t) * 4 + q) * NTH + tid] =
+                            (v4f){acc[f][t][4 * q], acc[f][t][4 * q + 1], acc[f][t][4 * q + 2], acc[f][t][4 * q + 3]};
+            if (!a.l2_local) __threadfence();
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (s_arrived != g_last - g_first) return;
+        }
         if (!a.l2_local) __threadfence();
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0)
-            s_arrived = __hip_atomic_fetch_add(a.counters + fb * NTB + tb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (s_arrived != g_last - g_first) return;
-        if (!a.l2_local) __threadfence();
+        // acc = partial g_first + ... + partial g_last, added in that order (the fast path holds g_first's already).
         const __amdgpu_buffer_rsrc_t fix = __builtin_amdgcn_make_buffer_rsrc(a.fix, 0, 0x7fffffff, 0x00020000);
-        for (int g = g_first; g <= g_last; ++g) {
+        for (int g = fast ? g_first + 1 : g_first; g <= g_last; ++g) {
             const uint32_t base = (uint32_t)(slot_of(g) * 4);
 #pragma unroll
             for (int f = 0; f < FR; ++f)
@@ -311,7 +323,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                     }
         }
         epilogue(fb);
-        if (tid == 0) __hip_atomic_store(a.counters + fb * NTB + tb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
 
     // Cursors (feature tile, K-step) of the next unit to load and of the unit being computed.

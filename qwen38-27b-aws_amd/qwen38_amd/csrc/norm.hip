@@ -78,7 +78,7 @@ __global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
                 make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
         if (a.act)
             *(uint32_t*)(a.act + act_offset(t, a.act_col0 + col[h], a.Kact)) =
-                e5m2_byte(o[0]) | (e5m2_byte(o[1]) << 8) | (e5m2_byte(o[2]) << 16) | (e5m2_byte(o[3]) << 24);
+                pk_e5m2(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -135,8 +135,8 @@ __global__ __launch_bounds__(256) void act_tiles_kernel(const bf16_t* x, int T, 
     if (i >= (size_t)T * K / 4) return;
     const int t = (int)(i / (K / 4)), c = (int)(i % (K / 4)) * 4;
     uint2 r = *(const uint2*)(x + (size_t)t * K + c);
-    *(uint32_t*)(act + act_offset(t, c, K)) = e5m2_byte(bf2f(r.x & 0xffff)) | (e5m2_byte(bf2f(r.x >> 16)) << 8) |
-                                              (e5m2_byte(bf2f(r.y & 0xffff)) << 16) | (e5m2_byte(bf2f(r.y >> 16)) << 24);
+    *(uint32_t*)(act + act_offset(t, c, K)) =
+        pk_e5m2(bf2f(r.x & 0xffff), bf2f(r.x >> 16), bf2f(r.y & 0xffff), bf2f(r.y >> 16));
 }
 
 hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream) {
