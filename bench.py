@@ -115,6 +115,22 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
     return engine, state
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemm_swiglu_256x34816x5120_traffic.md"
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per launch of the roofline kernel from its committed counter summary: FETCH_SIZE and WRITE_SIZE of the
+    same kernel on this workload (rocprofv3 --pmc, one counter per run), each scaled by what the counter reads for a
+    copy of known size in the same run. None when the summary is absent."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def time_dominant_kernel(engine, cfg, rows: int, reps: int = 20) -> float:
     """Average duration (ms) of the MLP gate/up GEMM kernel on layer 0's weights: HIP events on the current stream
     around `reps` launches whose e5m2 input tiles are already in the scratch (so the events bracket the GEMM only)."""
@@ -198,6 +214,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (rows shard across GPUs with no exchange); "
@@ -211,6 +229,14 @@ def main() -> int:
     batch, tokens, context, max_seq_len, seed = 64, 4, 512, 1024, args.seed
     cfg = qwen38_27b_config(16)
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.copy_probe:
+        # A kernel of known HBM traffic (reads and writes MIB MiB once) to scale FETCH_SIZE / WRITE_SIZE counters by.
+        src = torch.full((args.copy_probe << 20,), 0x5A, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe} MiB read and written by one bitwise_not kernel")
+        del src, dst
     engine, st = build(cfg, batch, tokens, max_seq_len, context, seed)
 
     def step():
@@ -266,7 +292,7 @@ def main() -> int:
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
             "avg_ms": round(kernel_ms, 4),
         },
         "step_roofline": {
