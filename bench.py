@@ -12,7 +12,9 @@ checkpoint.
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
-the SwiGLU epilogue, 2 x 17408 x 5120 FP8 weights against 256 tokens), timed with HIP events on the stream it runs on.
+the SwiGLU epilogue, 2 x 17408 x 5120 FP8 weights against 256 tokens): HIP events around each of its launches inside
+`--steps` further speculative steps, on the stream it runs on (q38_kernel_timer); `traffic` is its HBM bytes per
+launch from the committed counter summary in profiles/.
 `step_roofline` is the whole step's algorithmic HBM bytes over its time. `cpu_baseline` is the CPU oracle (this
 repository's restatement of the reference's CPU path) on a bounded sample: one 27B block (3 gated-delta + 1 attention
 layer) of the verify at the same B, K and context, scaled x16 to 64 layers, without the MTP and head passes.
@@ -131,29 +133,6 @@ def profiled_traffic() -> int | None:
     return None
 
 
-def time_dominant_kernel(engine, cfg, rows: int, reps: int = 20) -> float:
-    """Average duration (ms) of the MLP gate/up GEMM kernel on layer 0's weights: HIP events on the current stream
-    around `reps` launches whose e5m2 input tiles are already in the scratch (so the events bracket the GEMM only)."""
-    import torch
-
-    from qwen38_amd import ext
-
-    x = torch.randn(rows, cfg.hidden_size, device="cuda").to(torch.bfloat16)
-    tiles, scales = engine.buffer("mlp.gate_up.tiles", 0), engine.buffer("mlp.gate_up.scales", 0)
-    scratch = ext.linear_scratch(rows, cfg.hidden_size)
-    out = torch.empty(ext.library().q38_tiles_size(rows, cfg.intermediate_size), dtype=torch.uint8, device="cuda")
-    ext.mlp_up(x, rows, cfg.hidden_size, tiles, scales, cfg.intermediate_size, scratch, out)
-    for _ in range(2):
-        ext.mlp_up(None, rows, cfg.hidden_size, tiles, scales, cfg.intermediate_size, scratch, out)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        ext.mlp_up(None, rows, cfg.hidden_size, tiles, scales, cfg.intermediate_size, scratch, out)
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / reps
-
-
 def cpu_baseline(cfg_block, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, accepted_per_step: float,
                  n_blocks: int) -> dict:
     """The CPU oracle on one block of the same verify (bf16, all host threads), timed once after one warm-up."""
@@ -260,7 +239,14 @@ def main() -> int:
     value = accepted / (ms * args.steps / 1000.0)
     log(f"{ms:.3f} ms/step, {accepted} accepted tokens over {args.steps} steps")
 
-    kernel_ms = time_dominant_kernel(engine, cfg, batch * tokens)
+    # The dominant kernel inside real steps: the same number of steps again with HIP events around every gate/up GEMM
+    # launch on the step's stream (64 layers + 3 MTP calls per step).
+    engine.handle.kernel_timer(True)
+    for _ in range(args.steps):
+        step()
+    launches, total_ms = engine.handle.kernel_timer(False)
+    kernel_ms = total_ms / max(launches, 1)
+    log(f"gate/up GEMM inside the steps: {launches} launches, {kernel_ms * 1000:.1f} us each")
     flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
     achieved = flops / (kernel_ms / 1000.0) / 1e12
     alg = algorithmic_bytes(cfg, batch, tokens, context)
@@ -294,6 +280,7 @@ def main() -> int:
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
             "traffic": profiled_traffic(),
             "avg_ms": round(kernel_ms, 4),
+            "launches_timed": launches,
         },
         "step_roofline": {
             "bound": "hbm",

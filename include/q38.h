@@ -145,6 +145,12 @@ int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const
 int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
                   uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
 
+/* Measurement hook, with no counterpart in the reference (for benchmarks that time one kernel inside the step):
+ * on != 0 starts bracketing every gate/up projection GEMM launched by q38_verify, q38_mtp_step and q38_spec_step with
+ * HIP events on the launch's stream (at most 4096 launches); on == 0 stops, waits for the last event and reports the
+ * number of bracketed launches and the sum of their durations in milliseconds. */
+int q38_kernel_timer(q38_handle* h, int on, int* launches, float* total_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,8 @@ void gemm_scratch(GemmArgs& a, uint8_t* base, int cus) {
 
 }  // namespace
 
+static constexpr int TIMER_PAIRS = 4096;  // gate/up GEMM launches q38_kernel_timer can bracket
+
 struct q38_handle {
     q38_config cfg;
     int H, I, V, B, K, S, T, Tpad;
@@ -91,6 +93,10 @@ struct q38_handle {
         off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
     int gate_groups;  // K ranges of the gated-delta gate projections
     int attn_nchunks;  // chunks of ATTN_CHUNK cached positions over S
+    // Kernel timer (q38_kernel_timer): event pairs around the gate/up GEMM launches while on.
+    std::vector<hipEvent_t> timer_events;
+    int timer_used = 0;
+    bool timer_on = false;
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
@@ -351,7 +357,10 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     uint8_t* act_h = h->ws(h->off_act_h);
     uint8_t* act_ffn = h->ws(h->off_act_ffn);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    hipEvent_t* timed = h->timer_on && h->timer_used < TIMER_PAIRS ? &h->timer_events[2 * h->timer_used++] : nullptr;
+    if (timed) HIP_TRY(hipEventRecord(timed[0], stream));
     if (gemm(h, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
+    if (timed) HIP_TRY(hipEventRecord(timed[1], stream));
     int splits = 0;
     if (gemm(h, dn_t, dn_s, act_ffn, I, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     const float* part = (const float*)h->ws(h->off_part);
@@ -463,7 +472,36 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     return 0;
 }
 
-void q38_destroy(q38_handle* h) { delete h; }
+void q38_destroy(q38_handle* h) {
+    if (!h) return;
+    for (hipEvent_t e : h->timer_events) (void)hipEventDestroy(e);
+    delete h;
+}
+
+int q38_kernel_timer(q38_handle* h, int on, int* launches, float* total_ms) {
+    if (!h) return fail("null argument");
+    if (on) {
+        if (h->timer_events.empty()) {
+            h->timer_events.resize(2 * TIMER_PAIRS);
+            for (hipEvent_t& e : h->timer_events)
+                if (hipEventCreate(&e) != hipSuccess) return fail("hipEventCreate failed");
+        }
+        h->timer_used = 0;
+        h->timer_on = true;
+        return 0;
+    }
+    h->timer_on = false;
+    float total = 0.0f;
+    for (int i = 0; i < h->timer_used; ++i) {
+        HIP_TRY(hipEventSynchronize(h->timer_events[2 * i + 1]));
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, h->timer_events[2 * i], h->timer_events[2 * i + 1]));
+        total += ms;
+    }
+    if (launches) *launches = h->timer_used;
+    if (total_ms) *total_ms = total;
+    return 0;
+}
 
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes) {
     if (!h || !name || !nbytes) return fail("null argument");

@@ -19,6 +19,7 @@ MAX_LAYERS = 128
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
     "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_kernel_timer",
 )
 
 
@@ -62,6 +63,7 @@ def library() -> ctypes.CDLL:
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_mlp_up.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_tiles_size.argtypes = [i, i]
+    lib.q38_kernel_timer.argtypes = [p, i, ctypes.POINTER(i), ctypes.POINTER(ctypes.c_float)]
     lib.q38_verify.argtypes = [p] * 8 + [p]
     lib.q38_mtp_step.argtypes = [p] * 8 + [p]
     lib.q38_head_groupmax.argtypes = [p, p, i, p, p]
@@ -166,6 +168,13 @@ class Handle:
 
     def spec_step(self, position, index, match, accepted, active, hidden, picks, drafts) -> None:
         check(self.lib.q38_spec_step(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
+
+    def kernel_timer(self, on: bool) -> tuple[int, float]:
+        """Start (on) or stop bracketing the gate/up GEMM launches with HIP events; stopping returns (launches, total
+        milliseconds)."""
+        n, ms = ctypes.c_int(0), ctypes.c_float(0.0)
+        check(self.lib.q38_kernel_timer(self.h, int(on), ctypes.byref(n), ctypes.byref(ms)))
+        return n.value, ms.value
 
 
 def pack_weight(coded: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
