@@ -8,7 +8,10 @@
 // separate bf16 matmuls added in bf16; times bf16 sigmoid(gate). The masked entries of the reference's full-length
 // softmax contribute exact zeros (exp of about -600 underflows), so only visible positions are read.
 //
-// Two launches, so that every (row, KV head) spreads over several workgroups:
+// Rows whose visible context is at most 512 positions (one chunk) take one launch, attn_fused (KV head, row): sixteen
+// waves score 32 positions each, the softmax completes in the workgroup, and each wave then multiplies the weights
+// with 16 dims of V. Longer contexts take two launches, so that every (row, KV head) spreads over several
+// workgroups (each kernel skips the rows the other path takes):
 //   attn_scores (chunk of 512 cached positions, KV head, row): q norm + RoPE, the chunk's scores by MFMA (sixteen
 //       waves, one block of 32 positions each), the chunk's per-row max m_c, probabilities e = exp(s - m_c) (stored as float32) and
 //       their sum s_c. Chunk 0 also normalises and rotates the step's own keys and scores them.
@@ -51,40 +54,29 @@ __device__ __forceinline__ uint2 pack4(const float* v) { return make_uint2(pk_bf
 // Row of a 32x32 MFMA accumulator held in element i by `lane` (columns are lane % 32).
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-constexpr int SW = ATTN_CHUNK / 32;  // waves of attn_scores: one block of 32 positions each
+constexpr int SW = ATTN_CHUNK / 32;  // waves of the 1024-thread kernels: one block of 32 positions each
 
-template <int QT>
-__global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
-    __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];  // own keys (chunk 0)
-    __shared__ float wred[SW][QT * 32], mrow[QT * 32];
-
-    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
-    const int npos = visible(a, b);
-    const int p_lo = c * ATTN_CHUNK, p_hi = min(p_lo + ATTN_CHUNK, npos);
-    const bool first = c == 0;  // also does the step's own keys
-    if (!first && p_lo >= p_hi) return;
-    const size_t head = (size_t)b * a.Hkv + kvh;
-    const int blk = (p_lo >> 5) + wave;  // this wave's 32 positions
-    const bool scored = blk * 32 < p_hi;
-
-    // The wave's keys first: lane l holds key l % 32, dims 128 * (l / 32) + 8m .. + 7 in kf[m].
-    v8bf kf[16];
-    if (scored) {
-        const bf16_t* kp = a.k_cache + (head * S + blk * 32 + (lane & 31)) * 256 + (lane >> 5) * 128;
+// This wave's 32 keys of the cache, positions p0 .. p0 + 31: lane l holds key l % 32, dims 128 (l / 32) + 8m .. + 7
+// in kf[m].
+__device__ __forceinline__ void load_keys(const AttnArgs& a, size_t head, int p0, int lane, v8bf (&kf)[16]) {
+    const bf16_t* kp = a.k_cache + (head * a.S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
 #pragma unroll
-        for (int m = 0; m < 16; ++m) kf[m] = load8(kp + m * 8);
-    }
+    for (int m = 0; m < 16; ++m) kf[m] = load8(kp + m * 8);
+}
 
-    // Phase A: normed and rotated q rows (bf16, LDS); in chunk 0 also the own keys (normed, rotated: LDS as bf16 and
-    // kv_own as float32) and values (kv_own). Wave w takes rows w, w + SW, ...; lane l holds dims 4l .. 4l + 3.
-    constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + SW - 1) / SW;
-    const int nrows = QT * 32 + (first ? 2 * K : 0), d0 = lane * 4;
+// q rows normed and rotated (bf16, qb; rows NQ .. QT*32 - 1 zero) and, with `own`, the step's keys normed and rotated
+// (bf16, kb) and values: to kv_own (float32, global) and/or vown (float32, LDS), where given. NWV waves; wave w takes
+// rows w, w + NWV, ...; lane l holds dims 4l .. 4l + 3. Loads are issued before any store.
+template <int QT, int NWV>
+__device__ __forceinline__ void project_rows(const AttnArgs& a, int b, int kvh, int wave, int lane, bool own,
+                                             bf16_t* qb, bf16_t* kb, float* kv_own, float (*vown)[256]) {
+    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K;
+    constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + NWV - 1) / NWV;
+    const int nrows = QT * 32 + (own ? 2 * K : 0), d0 = lane * 4;
     uint2 raw[RPW], rc[RPW], rs_[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const int r = wave + SW * i;
+        const int r = wave + NWV * i;
         raw[i] = rc[i] = rs_[i] = make_uint2(0, 0);
         if (r >= nrows || (r >= NQ && r < QT * 32)) continue;
         const bf16_t* src;
@@ -120,10 +112,9 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
         for (int i = 0; i < RPW; ++i) ss[i] += __shfl_xor(ss[i], o);
-    float* kv_own = a.kv_own + head * 2 * ATTN_KMAX * 256;
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const int r = wave + SW * i;
+        const int r = wave + NWV * i;
         const float* nw = r < QT * 32 ? qn_w : kn_w;
         const float rsq = 1.0f / sqrtf(ss[i] / 256.0f + a.eps);
         float hn[4], part[4], cs[4], sn[4], out[4];
@@ -142,25 +133,26 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
         if (r < QT * 32) {
             *(uint2*)(qb + r * QPITCH + d0) = r < NQ ? pack4(out) : make_uint2(0, 0);
         } else if (r >= nrows) {
-            // rows of own keys and values exist in chunk 0 only
+            // rows of own keys and values exist only with `own`
         } else if (r < QT * 32 + K) {
             const int t = r - QT * 32;
             *(uint2*)(kb + t * QPITCH + d0) = pack4(out);
-            *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
+            if (kv_own) *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
         } else {
             const int t = r - QT * 32 - K;
-            *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
+            if (kv_own) *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
+            if (vown) *(v4f*)&vown[t][d0] = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
         }
     }
-    __syncthreads();
+}
 
-    // Phase B: the wave's block of scores (lane l: query row l % 32 of each 32-row tile, positions acc_row(i, l)).
-    v16f sacc[QT];
-    float lmax[QT];
+// Scores of 32 keys against the query tiles (lane l: query row l % 32 of each 32-row tile, positions p0 +
+// acc_row(i, l)), as rbf(q.k) / 16, -inf at positions p_hi and beyond; lmax takes their maximum.
+template <int QT>
+__device__ __forceinline__ void score_block(const v8bf (&kf)[16], const bf16_t* qb, int lane, int p0, int p_hi,
+                                            v16f (&sacc)[QT], float (&lmax)[QT]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        lmax[qt] = -INFINITY;
-        if (!scored) continue;
         const bf16_t* qp = qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128;
         v16f acc;
 #pragma unroll
@@ -169,38 +161,223 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
         for (int m = 0; m < 16; ++m) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[m], load8(qp + m * 8), acc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            acc[i] = blk * 32 + acc_row(i, lane) < p_hi ? rbf(acc[i]) * 0.0625f : -INFINITY;
+            acc[i] = p0 + acc_row(i, lane) < p_hi ? rbf(acc[i]) * 0.0625f : -INFINITY;
             lmax[qt] = fmaxf(lmax[qt], acc[i]);
         }
         sacc[qt] = acc;
     }
+}
 
-    // Own scores (chunk 0, last wave): query row q = g*K + t sees own tokens t' <= t. Keys past K read as zero.
-    if (first && wave == SW - 1) {
-        const bool key_row = (lane & 31) < K;
-        v8bf zero;
+// Scores of the step's own keys (kb rows 0..K-1; rows past K read as zero): query row q = g*K + t sees own tokens
+// t' <= t. Calls f(q, t', score) for q < NQ, t' < K.
+template <int QT, typename F>
+__device__ __forceinline__ void own_scores(const bf16_t* qb, const bf16_t* kb, int lane, int K, int NQ, F f) {
+    const bool key_row = (lane & 31) < K;
+    v8bf zero;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) zero[e] = (__bf16)0.0f;
-        const bf16_t* kp = kb + min(lane & 31, ATTN_KMAX - 1) * QPITCH + (lane >> 5) * 128;
+    for (int e = 0; e < 8; ++e) zero[e] = (__bf16)0.0f;
+    const bf16_t* kp = kb + min(lane & 31, ATTN_KMAX - 1) * QPITCH + (lane >> 5) * 128;
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const bf16_t* qp = qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128;
-            v16f acc;
+    for (int qt = 0; qt < QT; ++qt) {
+        const bf16_t* qp = qb + (qt * 32 + (lane & 31)) * QPITCH + (lane >> 5) * 128;
+        v16f acc;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-            for (int m = 0; m < 16; ++m)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(key_row ? load8(kp + m * 8) : zero, load8(qp + m * 8), acc,
-                                                              0, 0, 0);
-            const int q = qt * 32 + (lane & 31);
+        for (int m = 0; m < 16; ++m)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(key_row ? load8(kp + m * 8) : zero, load8(qp + m * 8), acc, 0, 0, 0);
+        const int q = qt * 32 + (lane & 31);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {  // key rows 0..7
-                const int tp = acc_row(i, lane);
-                if (tp < K && q < NQ)
-                    a.own[(head * ATTN_QMAX + q) * ATTN_KMAX + tp] = tp <= q % K ? rbf(acc[i]) * 0.0625f : -INFINITY;
-            }
+        for (int i = 0; i < 4; ++i) {  // key rows 0..7
+            const int tp = acc_row(i, lane);
+            if (tp < K && q < NQ) f(q, tp, tp <= q % K ? rbf(acc[i]) * 0.0625f : -INFINITY);
         }
     }
+}
+
+// Whole verify attention of one (row, KV head) whose visible context fits one chunk (at most ATTN_CHUNK positions):
+// 16 waves; wave w scores positions 32w .. 32w + 31, then takes dims 16w .. 16w + 15 of the output. The softmax is
+// complete inside the workgroup, so the weights are the reference's bf16(e^(s - M) / S) exactly; they go through LDS
+// to the weights x V product (v_mfma_f32_16x16x32_bf16: A = 16 query rows x 32 positions, B = 32 positions x 16 dims).
+template <int QT>
+__global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
+    constexpr int RT = QT * 2;                 // 16-row tiles of query rows
+    constexpr int WPITCH = ATTN_CHUNK + 8;     // bf16 per weight row in LDS (rows start 4 banks apart)
+    __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
+    __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];
+    __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX][256];
+    __shared__ float sown[QT * 32][ATTN_KMAX], wown[QT * 32][ATTN_KMAX];
+    __shared__ float wred[SW][QT * 32], mrow[QT * 32], irow[QT * 32];
+    __shared__ __attribute__((aligned(16))) bf16_t wts[QT * 32 * WPITCH];
+
+    const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
+    const int npos = visible(a, b);
+    if (npos > ATTN_CHUNK) return;  // the chunked kernels take this row
+    const size_t head = (size_t)b * a.Hkv + kvh;
+    const bool scored = wave * 32 < npos;
+    const int dcol = wave * 16 + (lane & 15);  // output dim of this lane
+
+    v8bf kf[16];
+    if (scored) load_keys(a, head, wave * 32, lane, kf);
+    uint32_t gate[RT][4];  // gates of this lane's output rows rt*16 + 4 (l / 16) + i, dim dcol
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = min(rt * 16 + 4 * (lane >> 4) + i, NQ - 1);
+            gate[rt][i] = a.qkv[(size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + dcol];
+        }
+    project_rows<QT, SW>(a, b, kvh, wave, lane, true, qb, kb, nullptr, vown);
+    __syncthreads();
+
+    v16f sacc[QT];
+    float lmax[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) lmax[qt] = -INFINITY;
+    if (scored) score_block<QT>(kf, qb, lane, wave * 32, npos, sacc, lmax);
+    if (wave == SW - 1) own_scores<QT>(qb, kb, lane, K, NQ, [&](int q, int tp, float v) { sown[q][tp] = v; });
+
+    // This wave's V columns over the visible positions: lane l holds dim dcol, positions 32j + 8 (l / 16) .. + 7.
+    // Issued only once the keys are consumed (the compiler barrier keeps both out of registers at once).
+    asm volatile("" ::: "memory");
+    const int nblk = (npos + 31) >> 5;
+    v8bf vf[SW];
+    const bf16_t* vp = a.v_cache + head * S * 256 + dcol * 32 + 8 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < SW; ++j) vf[j] = load8(vp + (size_t)max(min(j, nblk - 1), 0) * 8192);  // past nblk: unused
+
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float m = fmaxf(lmax[qt], __shfl_xor(lmax[qt], 32));
+        if (lane < 32) wred[wave][qt * 32 + lane] = m;
+    }
+    __syncthreads();
+    if (tid < QT * 32) {
+        float m = wred[0][tid];
+#pragma unroll
+        for (int w = 1; w < SW; ++w) m = fmaxf(m, wred[w][tid]);
+        if (tid < NQ)
+            for (int tp = 0; tp < K; ++tp) m = fmaxf(m, sown[tid][tp]);
+        mrow[tid] = m;
+    }
+    __syncthreads();
+
+    // e = exp(s - M); the row sums over the cache positions, then the own terms.
+    float lsum[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        lsum[qt] = 0.0f;
+        if (!scored) continue;
+        const float m = mrow[qt * 32 + (lane & 31)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sacc[qt][i] = expf(sacc[qt][i] - m);
+            lsum[qt] += sacc[qt][i];
+        }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float s = lsum[qt] + __shfl_xor(lsum[qt], 32);
+        if (lane < 32) wred[wave][qt * 32 + lane] = s;
+    }
+    __syncthreads();
+    if (tid < QT * 32) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SW; ++w) s += wred[w][tid];
+        const float m = mrow[tid];
+        for (int tp = 0; tp < K; ++tp)
+            if (tid < NQ && sown[tid][tp] > -INFINITY) s += expf(sown[tid][tp] - m);
+        const float iv = s > 0.0f ? 1.0f / s : 0.0f;
+        irow[tid] = iv;
+        for (int tp = 0; tp < ATTN_KMAX; ++tp)
+            wown[tid][tp] = tid < NQ && tp < K && sown[tid][tp] > -INFINITY ? rbf(expf(sown[tid][tp] - m) * iv) : 0.0f;
+    }
+    __syncthreads();
+
+    // bf16 weights of this wave's positions into LDS (rows of WPITCH), four consecutive positions per store.
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        if (!scored) continue;
+        const int q = qt * 32 + (lane & 31);
+        const float iv = irow[q];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *(uint2*)(wts + q * WPITCH + wave * 32 + g * 8 + (lane >> 5) * 4) =
+                make_uint2(pk_bf16(sacc[qt][4 * g] * iv, sacc[qt][4 * g + 1] * iv),
+                           pk_bf16(sacc[qt][4 * g + 2] * iv, sacc[qt][4 * g + 3] * iv));
+    }
+    __syncthreads();
+
+    // Weights x V for this wave's 16 dims; then the own part, the gate and the e5m2 activation bytes.
+    v4f acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < SW; ++j)
+        if (j < nblk)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    load8(wts + (rt * 16 + (lane & 15)) * WPITCH + j * 32 + 8 * (lane >> 4)), vf[j], acc[rt], 0, 0, 0);
+    const int act_k = a.Hq * 256;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = rt * 16 + 4 * (lane >> 4) + i;
+            if (q >= NQ) continue;
+            float own = 0.0f;
+            for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vown[tp][dcol];
+            float o = rbf(rbf(acc[rt][i]) + rbf(own));
+            o = rbf(o * rbf(sigmoidf_(bf2f((bf16_t)gate[rt][i]))));
+            a.act[act_offset(b * K + q % K, (kvh * G + q / K) * 256 + dcol, act_k)] = (uint8_t)e5m2_byte(o);
+        }
+
+    // The step's own keys and values into the cache (model.py:603-608, 653-654) once every wave has read its V;
+    // inactive rows write the tail.
+    __syncthreads();
+    const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
+    for (int i = tid; i < K * 256; i += SW * 64) {
+        const int t = i >> 8, d = i & 255, p = base + t;
+        if (p < 0 || p >= S) continue;
+        a.k_cache[(head * S + p) * 256 + d] = kb[t * QPITCH + d];
+        a.v_cache[head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31)] = f2bf(vown[t][d]);
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
+    __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];  // own keys (chunk 0)
+    __shared__ float wred[SW][QT * 32], mrow[QT * 32];
+
+    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
+    const int npos = visible(a, b);
+    if (npos <= ATTN_CHUNK) return;  // attn_fused takes this row
+    const int p_lo = c * ATTN_CHUNK, p_hi = min(p_lo + ATTN_CHUNK, npos);
+    const bool first = c == 0;  // also does the step's own keys
+    if (!first && p_lo >= p_hi) return;
+    const size_t head = (size_t)b * a.Hkv + kvh;
+    const int blk = (p_lo >> 5) + wave;  // this wave's 32 positions
+    const bool scored = blk * 32 < p_hi;
+
+    v8bf kf[16];
+    if (scored) load_keys(a, head, blk * 32, lane, kf);
+    project_rows<QT, SW>(a, b, kvh, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
+    __syncthreads();
+
+    // The wave's block of scores, kept in registers; chunk 0's last wave also scores the own keys.
+    v16f sacc[QT];
+    float lmax[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) lmax[qt] = -INFINITY;
+    if (scored) score_block<QT>(kf, qb, lane, blk * 32, p_hi, sacc, lmax);
+    if (first && wave == SW - 1)
+        own_scores<QT>(qb, kb, lane, K, NQ,
+                       [&](int q, int tp, float v) { a.own[(head * ATTN_QMAX + q) * ATTN_KMAX + tp] = v; });
 
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -272,6 +449,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b), nblk = (npos + 31) >> 5;
+    if (npos <= ATTN_CHUNK) return;  // attn_fused takes this row
     const size_t head = (size_t)hh;
     const int dq = quarter * 64;
     const float* pr = a.probs + head * ATTN_QMAX * S;
@@ -437,8 +615,11 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
 
 template <int QT>
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_scores_kernel<QT>, dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
-    hipLaunchKernelGGL(attn_out_kernel<QT>, dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(attn_fused_kernel<QT>, dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+    if (a.S > ATTN_CHUNK) {
+        hipLaunchKernelGGL(attn_scores_kernel<QT>, dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+        hipLaunchKernelGGL(attn_out_kernel<QT>, dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
