@@ -177,16 +177,20 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
         const uint8_t* sb = lds + st * STAGE;
         const uint8_t* wl = sb + ACT_B + (wf * FR) * 2048 + lane * 8;
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
-        uint32_t sc[FR];
+        float scl[FR][2];  // 2^(scale byte - 127) of the K-step's two MX blocks (inputs 0-31, 32-63)
 #pragma unroll
-        for (int f = 0; f < FR; ++f) sc[f] = *(const uint16_t*)(sl + f * 64);
+        for (int f = 0; f < FR; ++f) {
+            const uint32_t sc = *(const uint16_t*)(sl + f * 64);
+            scl[f][0] = __uint_as_float((sc & 0xffu) << 23);
+            scl[f][1] = __uint_as_float((sc >> 8) << 23);
+        }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             v8bf wb[FR];
 #pragma unroll
             for (int f = 0; f < FR; ++f) {
-                // Steps 0-1 are inputs of the K-step's first MX block (scale byte 0), steps 2-3 of its second.
-                const float scale = __uint_as_float((m < 2 ? sc[f] & 0xffu : sc[f] >> 8) << 23);
+                // Steps 0-1 are inputs of the K-step's first MX block, steps 2-3 of its second.
+                const float scale = scl[f][m >> 1];
                 const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
                 wb[f] = widen_e4m3(r[0], r[1], scale);
             }

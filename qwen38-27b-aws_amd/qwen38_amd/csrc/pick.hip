@@ -19,15 +19,21 @@ __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
     return a > b || (a == b && ia < ib);
 }
 
-__global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
-    __shared__ float lv[256][PICK_GMAX];
-    __shared__ int li[256][PICK_GMAX];
+constexpr int PICK_THREADS = 1024;  // 16 waves: the recheck splits each group's K range over 16 / G waves
+
+__global__ __launch_bounds__(PICK_THREADS) void head_pick_kernel(const PickArgs a) {
+    constexpr int NWAVE = PICK_THREADS / 64;
+    __shared__ float lv[PICK_THREADS][PICK_GMAX];
+    __shared__ int li[PICK_THREADS][PICK_GMAX];
     __shared__ float xrow[8192];
+    __shared__ float part[NWAVE][32];
     __shared__ float glogit[PICK_GMAX];
     __shared__ int gtoken[PICK_GMAX];
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.groups;
 
+    // 1. The G best groups: each thread's share of the group maxima (eight loads in flight at a time; the ranking does
+    //    not depend on the order candidates are seen in), then a merge tree over the threads.
     float bv[PICK_GMAX];
     int bi[PICK_GMAX];
 #pragma unroll
@@ -36,26 +42,34 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
         bi[k] = 0x7fffffff;
     }
     const float* mrow = a.maxima + (size_t)r * a.ngroups;
-    for (int i = tid; i < a.ngroups; i += 256) {
-        float v = mrow[i];
-        if (!ranks_before(v, i, bv[G - 1], bi[G - 1])) continue;
-        int k = G - 1;
-        while (k > 0 && ranks_before(v, i, bv[k - 1], bi[k - 1])) {
-            bv[k] = bv[k - 1];
-            bi[k] = bi[k - 1];
-            --k;
+    constexpr int CH = 8;
+    for (int i0 = tid; i0 < a.ngroups; i0 += PICK_THREADS * CH) {
+        float vv[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) vv[c] = i0 + c * PICK_THREADS < a.ngroups ? mrow[i0 + c * PICK_THREADS] : 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int i = i0 + c * PICK_THREADS;
+            const float v = vv[c];
+            if (i >= a.ngroups || !ranks_before(v, i, bv[G - 1], bi[G - 1])) continue;
+            int k = G - 1;
+            while (k > 0 && ranks_before(v, i, bv[k - 1], bi[k - 1])) {
+                bv[k] = bv[k - 1];
+                bi[k] = bi[k - 1];
+                --k;
+            }
+            bv[k] = v;
+            bi[k] = i;
         }
-        bv[k] = v;
-        bi[k] = i;
     }
 #pragma unroll
     for (int k = 0; k < PICK_GMAX; ++k) {
         lv[tid][k] = bv[k];
         li[tid][k] = bi[k];
     }
-    for (int c = tid; c < a.H; c += 256) xrow[c] = a.x32[(size_t)r * a.H + c];
+    for (int c = tid; c < a.H; c += PICK_THREADS) xrow[c] = a.x32[(size_t)r * a.H + c];
     __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
+    for (int stride = PICK_THREADS / 2; stride > 0; stride >>= 1) {
         if (tid < stride) {
             float mv[PICK_GMAX];
             int mi[PICK_GMAX];
@@ -74,27 +88,30 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
         __syncthreads();
     }
 
-    // Exact logits: wave w rechecks the w-th best group, which is one 32-row weight tile.
-    const int KS = a.H >> 6;
-    if (wave < G) {
-        const int grp = li[0][wave];
+    // 2. Exact float32 logits of the G groups' rows: group k's K-steps split into SPL ranges, one wave each; lane l
+    //    accumulates row l % 32 over its half of each K-step's inputs. Lane half h holds inputs [16h, 16h + 16) of the
+    //    K-step in bytes 0-15 (first MX block) and [32 + 16h, 48 + 16h) in bytes 16-31 (second block).
+    const int KS = a.H >> 6, SPL = NWAVE / G;
+    const int gk = wave / SPL, sp = wave % SPL;
+    if (gk < G) {
+        const int grp = li[0][gk];
         float acc = 0.0f;
         if (grp >= 0 && grp < a.ngroups) {
-            // Lane half h holds inputs [16h, 16h + 16) of the K-step in bytes 0-15 (first MX block) and
-            // [32 + 16h, 48 + 16h) in bytes 16-31 (second block).
             const uint8_t* tile = a.w + (size_t)grp * KS * 2048 + lane * 8;
             const uint8_t* sc = a.ws + (size_t)grp * KS * 64 + (lane & 31) * 2;
             const float* xp = xrow + (lane >> 5) * 16;
-            for (int ks = 0; ks < KS; ++ks) {
+            const int k0 = sp * KS / SPL, k1 = (sp + 1) * KS / SPL;
+#pragma unroll 4
+            for (int ks = k0; ks < k1; ++ks) {
                 const float s0 = __uint_as_float((uint32_t)sc[(size_t)ks * 64] << 23);
                 const float s1 = __uint_as_float((uint32_t)sc[(size_t)ks * 64 + 1] << 23);
                 // Word w of the lane's 32 bytes: step w / 2 of the tile, at [m][lane][8].
                 uint32_t words[8];
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    const uint2 r = *(const uint2*)(tile + (size_t)ks * 2048 + m * 512);
-                    words[2 * m] = r.x;
-                    words[2 * m + 1] = r.y;
+                    const uint2 rw = *(const uint2*)(tile + (size_t)ks * 2048 + m * 512);
+                    words[2 * m] = rw.x;
+                    words[2 * m + 1] = rw.y;
                 }
 #pragma unroll
                 for (int wi = 0; wi < 8; ++wi) {
@@ -110,9 +127,15 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
             }
         }
         acc += __shfl_xor(acc, 32);
-        // Largest logit of the group, first index on ties; NaN propagates as torch.max does.
-        float v = acc;
-        int idx = lane & 31;
+        if (lane < 32) part[wave][lane] = acc;
+    }
+    __syncthreads();
+    // 3. Per group: the K ranges added in order, the largest logit of its 32 rows (first index on ties; NaN propagates
+    //    as torch.max does); then across groups the first strictly larger in top-k order.
+    if (wave < G && lane < 32) {
+        float v = part[wave * SPL][lane];
+        for (int s2 = 1; s2 < SPL; ++s2) v += part[wave * SPL + s2][lane];
+        int idx = lane;
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) {
             float ov = __shfl_xor(v, o);
@@ -124,6 +147,7 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
             }
         }
         if (lane == 0) {
+            const int grp = li[0][wave];
             glogit[wave] = v;
             gtoken[wave] = grp * 32 + idx;
         }
@@ -143,7 +167,8 @@ __global__ __launch_bounds__(256) void head_pick_kernel(const PickArgs a) {
 }
 
 hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(head_pick_kernel, dim3(a.R), dim3(256), 0, stream, a);
+    if (a.groups < 1 || a.groups > PICK_GMAX || a.H > 8192 || a.H % 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(head_pick_kernel, dim3(a.R), dim3(PICK_THREADS), 0, stream, a);
     return hipGetLastError();
 }
 
