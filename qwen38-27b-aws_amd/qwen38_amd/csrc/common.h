@@ -30,6 +30,10 @@ typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
+// The bf16 in the low / high half of a word, widened.
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 // fp32 -> bf16, round to nearest even (c10::BFloat16's rounding; v_cvt_pk_bf16_f32); NaN stays NaN.
 __device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
@@ -77,6 +81,19 @@ __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
+}
+
+// Sum over each aligned group of 8 (16) lanes with DPP moves (lane ^ 1, lane ^ 2, then the mirrored half row and row);
+// every lane of a group ends with the same total, the same additions in the same order.
+__device__ __forceinline__ float group8_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return v;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+    v = group8_sum(v);
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
 }
 
 __device__ __forceinline__ float warp_max(float v) {

@@ -63,12 +63,17 @@ __global__ __launch_bounds__(256) void gdn_gates_kernel(const GatesArgs a) {
 
 // K (tokens per row) is a template parameter so that every per-token array lives in registers.
 template <int K>
-__global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 : 1))) void gdn_verify_kernel(const GdnArgs a) {
     constexpr int D = 128;
+    constexpr int RS = (2 * K + 7) / 8 * 8;  // rows between the three bf16 parts of [k; q] (a multiple of 8)
+    constexpr int MB = (3 * RS + 31) / 32;   // 32-row MFMA blocks holding them
     __shared__ float mixed[K][3 * D];   // SiLU(conv) of this head's q, k, v channels
     __shared__ float qn[K][D], kn[K][D];
-    __shared__ float wk[K][D];          // committed snapshot keys times their decay weights
-    __shared__ float part[4][2 * K][D]; // reads, one partial per row quarter
+    __shared__ float wk[D][K];          // committed snapshot keys times their decay weights, input-major
+    __shared__ float part[2][2 * K][D]; // reads, one partial per half of the state rows
+    // [k_0..k_K-1, q_0..q_K-1] as three bf16 parts (rows r, RS + r, 2 RS + r) whose sum is the float32 value to 2^-27:
+    // the A operand of the reads on the bf16 MFMA (products exact, float32 sums). Rows past them are never read out.
+    __shared__ __attribute__((aligned(16))) bf16_t kq3[32 * MB][D + 8];
     __shared__ float kk[K][K], qk[K][K];
     __shared__ float ob[K][D];
     __shared__ float rms[K];
@@ -81,7 +86,11 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     const float keep = (a.position[b] == 0 && on) ? 0.0f : 1.0f;
     const int acc_n = min(max(a.accepted[b], 0), K);
     constexpr int GMAX = 8;  // gate groups, at most
-    constexpr int CPT = (3 * D + 255) / 256;  // conv channels per thread
+    // Conv channels: thread tid < 3 D / 2 owns channels cc, cc + 1 of one group (q of key head kh, k of key head kh,
+    // v of head h), so that every conv load and store is a word or wider.
+    const bool conv_thread = tid < 3 * D / 2;
+    const int cgrp = (2 * tid) / D, cj = (2 * tid) % D;
+    const int cc = cgrp == 0 ? kh * D + cj : cgrp == 1 ? Hk * D + kh * D + cj : 2 * Hk * D + h * D + cj;
 
     // Every global load of the block is issued here, before the first store: a load placed after a store would wait
     // for it (the pointers may alias as far as the compiler knows), and each wait is a memory round trip.
@@ -89,28 +98,27 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     if (tid < 2 * K) {
         const int t = tid % K, which = tid / K, O = 2 * Hv;
         const float* p = a.gate_part + ((size_t)b * K + t) * O + (which ? Hv + h : h);
+        // Unconditional loads (group indices clamped to valid ones), so that none waits for another.
 #pragma unroll
-        for (int gi = 0; gi < GMAX; ++gi) gp[gi] = gi < a.gate_groups ? p[(size_t)gi * a.B * K * O] : 0.0f;
+        for (int gi = 0; gi < GMAX; ++gi) gp[gi] = p[(size_t)min(gi, a.gate_groups - 1) * a.B * K * O];
     }
     float dec_in[K];
 #pragma unroll
     for (int s = 0; s < K; ++s) dec_in[s] = a.decay_old[((size_t)b * K + s) * Hv + h];
-    bf16_t conv_in[CPT][3 + 2 * K + 4];  // old conv state, last step's inputs, this step's inputs, conv weights
+    // Old conv state (3 bf16 per channel, so 3 words for the pair), last step's and this step's inputs (a word per
+    // token), conv weights (4 bf16 per channel: 16 bytes).
+    uint32_t cv_old[3], cv_prev[K], cv_new[K];
+    uint4 cv_w;
+    if (conv_thread) {
+        const uint32_t* po = (const uint32_t*)(a.conv_old + ((size_t)b * C + cc) * 3);
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-        const int ci = tid + 256 * u;
-        if (ci >= 3 * D) break;
-        const int grp = ci / D, j = ci % D;
-        const int c = grp == 0 ? kh * D + j : grp == 1 ? Hk * D + kh * D + j : 2 * Hk * D + h * D + j;
-#pragma unroll
-        for (int q = 0; q < 3; ++q) conv_in[u][q] = a.conv_old[((size_t)b * C + c) * 3 + q];
+        for (int q = 0; q < 3; ++q) cv_old[q] = po[q];
 #pragma unroll
         for (int s = 0; s < K; ++s) {
-            conv_in[u][3 + s] = a.qkv_old[((size_t)b * K + s) * C + c];
-            conv_in[u][3 + K + s] = a.qkv_new[((size_t)b * K + s) * C + c];
+            cv_prev[s] = *(const uint32_t*)(a.qkv_old + ((size_t)b * K + s) * C + cc);
+            cv_new[s] = *(const uint32_t*)(a.qkv_new + ((size_t)b * K + s) * C + cc);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) conv_in[u][3 + 2 * K + q] = a.conv_w[(size_t)c * 4 + q];
+        cv_w = *(const uint4*)(a.conv_w + (size_t)cc * 4);
     }
     constexpr int KPT = (K * D + 255) / 256;  // snapshot key elements per thread
     float key_in[KPT];
@@ -119,14 +127,19 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         const int i = tid + 256 * u;
         key_in[u] = i < K * D ? a.key_old[(((size_t)b * K + i / D) * Hk + kh) * D + i % D] : 0.0f;
     }
-    const int j0 = lane * 2, i0 = wave * 32;
+    // State ownership: wave w holds columns [64 (w & 1), +64) and rows [64 (w >> 1), +64); lane l the two columns jc,
+    // jc + 1 and, in each of 4 MFMA K-steps ks, the 8 rows ir + 16 ks + [0, 8), as the bf16 MFMA's B operand wants
+    // them (column l % 32, inputs 8 (l / 32) + [0, 8)); even and odd columns go to two MFMAs.
+    const int jc = 64 * (wave & 1) + 2 * (lane & 31), ir = 64 * (wave >> 1) + 8 * (lane >> 5);
     float2 dlt_in[K];
 #pragma unroll
-    for (int s = 0; s < K; ++s) dlt_in[s] = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + j0);
+    for (int s = 0; s < K; ++s) dlt_in[s] = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + jc);
     bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
-    uint32_t sv[32];
+    uint32_t sv[4][8];
 #pragma unroll
-    for (int ii = 0; ii < 32; ++ii) sv[ii] = *(const uint32_t*)(st + (size_t)(i0 + ii) * D + j0);
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[ks][e] = *(const uint32_t*)(st + (size_t)(ir + 16 * ks + e) * D + jc);
     constexpr int ZPW = (K + 3) / 4;  // gated-norm rows per wave
     bf16_t z_in[ZPW][2];
 #pragma unroll
@@ -175,41 +188,44 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
     }
 
     // Conv history and conv (model.py:399-409). Channel groups: q of key head kh, k of key head kh, v of head h.
+    if (conv_thread) {
+        const float old6[6] = {lo_bf(cv_old[0]), hi_bf(cv_old[0]), lo_bf(cv_old[1]),
+                               hi_bf(cv_old[1]), lo_bf(cv_old[2]), hi_bf(cv_old[2])};
+        const uint32_t cw[4] = {cv_w.x, cv_w.y, cv_w.z, cv_w.w};
+        float hist2[2][3];
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-        const int ci = tid + 256 * u;
-        if (ci >= 3 * D) break;
-        const int grp = ci / D, j = ci % D;
-        const int c = grp == 0 ? kh * D + j : grp == 1 ? Hk * D + kh * D + j : 2 * Hk * D + h * D + j;
-        float w_old[3 + K];
+        for (int ch = 0; ch < 2; ++ch) {
+            float w_old[3 + K];  // the channel's old conv state, then the last step's inputs
 #pragma unroll
-        for (int q = 0; q < 3 + K; ++q) w_old[q] = bf2f(conv_in[u][q]);
-        float hist[3];
+            for (int q = 0; q < 3; ++q) w_old[q] = old6[3 * ch + q];
 #pragma unroll
-        for (int jj = 0; jj < 3; ++jj) {
-            float v = w_old[jj];
+            for (int s = 0; s < K; ++s) w_old[3 + s] = ch ? hi_bf(cv_prev[s]) : lo_bf(cv_prev[s]);
+            float hist[3];
 #pragma unroll
-            for (int s = 1; s <= K; ++s) v = acc_n == s ? w_old[s + jj] : v;
-            hist[jj] = on ? v * keep : w_old[jj];
+            for (int jj = 0; jj < 3; ++jj) {
+                float v = w_old[jj];
+#pragma unroll
+                for (int s = 1; s <= K; ++s) v = acc_n == s ? w_old[s + jj] : v;
+                hist[jj] = hist2[ch][jj] = on ? v * keep : w_old[jj];
+            }
+            float win[3 + K];
+            win[0] = hist[0];
+            win[1] = hist[1];
+            win[2] = hist[2];
+#pragma unroll
+            for (int t = 0; t < K; ++t) win[3 + t] = ch ? hi_bf(cv_new[t]) : lo_bf(cv_new[t]);
+            const float w0 = lo_bf(cw[2 * ch]), w1 = hi_bf(cw[2 * ch]), w2 = lo_bf(cw[2 * ch + 1]), w3 = hi_bf(cw[2 * ch + 1]);
+#pragma unroll
+            for (int t = 0; t < K; ++t) {
+                float m = rbf(((rbf(win[t] * w0) + rbf(win[t + 1] * w1)) + rbf(win[t + 2] * w2)) + rbf(win[t + 3] * w3));
+                mixed[t][2 * tid + ch] = rbf(m * rbf(sigmoidf_(m)));
+            }
         }
-        if (grp == 2 || owner) {
-            bf16_t* dst = a.conv_new + ((size_t)b * C + c) * 3;
-            dst[0] = f2bf(hist[0]);
-            dst[1] = f2bf(hist[1]);
-            dst[2] = f2bf(hist[2]);
-        }
-        float win[3 + K];
-        win[0] = hist[0];
-        win[1] = hist[1];
-        win[2] = hist[2];
-#pragma unroll
-        for (int t = 0; t < K; ++t) win[3 + t] = bf2f(conv_in[u][3 + K + t]);
-        const float w0 = bf2f(conv_in[u][3 + 2 * K]), w1 = bf2f(conv_in[u][3 + 2 * K + 1]), w2 = bf2f(conv_in[u][3 + 2 * K + 2]),
-                    w3 = bf2f(conv_in[u][3 + 2 * K + 3]);
-#pragma unroll
-        for (int t = 0; t < K; ++t) {
-            float m = rbf(((rbf(win[t] * w0) + rbf(win[t + 1] * w1)) + rbf(win[t + 2] * w2)) + rbf(win[t + 3] * w3));
-            mixed[t][ci] = rbf(m * rbf(sigmoidf_(m)));
+        if (cgrp == 2 || owner) {
+            uint32_t* dst = (uint32_t*)(a.conv_new + ((size_t)b * C + cc) * 3);
+            dst[0] = pk_bf16(hist2[0][0], hist2[0][1]);
+            dst[1] = pk_bf16(hist2[0][2], hist2[1][0]);
+            dst[2] = pk_bf16(hist2[1][1], hist2[1][2]);
         }
     }
     __syncthreads();
@@ -220,12 +236,24 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         float x0 = mixed[t][isk * D + lane], x1 = mixed[t][isk * D + lane + 64];
         float ssum = warp_sum(x0 * x0 + x1 * x1);
         float rs = 1.0f / sqrtf(ssum + 1e-6f);
+        float y0, y1;
         if (isk) {
-            kn[t][lane] = x0 * rs;
-            kn[t][lane + 64] = x1 * rs;
+            y0 = kn[t][lane] = x0 * rs;
+            y1 = kn[t][lane + 64] = x1 * rs;
         } else {
-            qn[t][lane] = (x0 * rs) / 11.313708498984761f;
-            qn[t][lane + 64] = (x1 * rs) / 11.313708498984761f;
+            y0 = qn[t][lane] = (x0 * rs) / 11.313708498984761f;
+            y1 = qn[t][lane + 64] = (x1 * rs) / 11.313708498984761f;
+        }
+        const int row = isk ? t : K + t;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const float y = half ? y1 : y0;
+            const bf16_t hi = f2bf(y);
+            const float r1 = y - bf2f(hi);  // exact
+            const bf16_t mid = f2bf(r1);
+            kq3[row][lane + 64 * half] = hi;
+            kq3[RS + row][lane + 64 * half] = mid;
+            kq3[2 * RS + row][lane + 64 * half] = f2bf(r1 - bf2f(mid));
         }
     }
     // Snapshot keys times their commit weights (model.py:397-398).
@@ -237,20 +265,31 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         float c = 0.0f;
 #pragma unroll
         for (int r = 0; r < K; ++r) c = s == r ? coef[r] : c;
-        wk[s][i % D] = key_in[u] * c;
+        wk[i % D][s] = key_in[u] * c;
     }
     __syncthreads();
 
-    // In-step dot products k_t.k_s and q_t.k_s (model.py:438, 444).
-    for (int r = wave; r < 2 * K * K; r += 4) {
-        const int isq = r / (K * K), t = (r % (K * K)) / K, s = r % K;
-        const float* x = isq ? qn[t] : kn[t];
-        float v = warp_sum(x[lane] * kn[s][lane] + x[lane + 64] * kn[s][lane + 64]);
-        if (lane == 0) (isq ? qk : kk)[t][s] = v;
+    // In-step dot products k_t.k_s and q_t.k_s (model.py:438, 444): 8 lanes per product, 16 inputs each.
+    for (int p = tid >> 3; p < 2 * K * K; p += 32) {
+        const int isq = p / (K * K), t = (p % (K * K)) / K, s = p % K;
+        const float* x = (isq ? qn[t] : kn[t]) + (tid & 7) * 16;
+        const float* y = kn[s] + (tid & 7) * 16;
+        float v = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+            const float4 xv = *(const float4*)(x + e), yv = *(const float4*)(y + e);
+            v += xv.x * yv.x;
+            v += xv.y * yv.y;
+            v += xv.z * yv.z;
+            v += xv.w * yv.w;
+        }
+        v = group8_sum(v);
+        if ((tid & 7) == 0) (isq ? qk : kk)[t][s] = v;
     }
 
-    // State commit and reads (model.py:262-266, 419-429): thread owns columns 2*lane, 2*lane+1 of rows
-    // [32*wave, 32*wave+32).
+    // State commit and reads (model.py:262-266, 419-429). Commit on the VALU: S' = bf16(S * scale + sum_s wk_s d_s),
+    // stored; reads [k; q] S' on the MFMA, S' (exact in bf16) against the three bf16 parts of [k; q], so every product
+    // is exact and the sums are float32. Each wave sums its 64 rows; the two row halves are added in the solve.
     {
         float d0[K], d1[K];
 #pragma unroll
@@ -258,30 +297,57 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
             d0[s] = dlt_in[s].x;
             d1[s] = dlt_in[s].y;
         }
-        float p0[2 * K], p1[2 * K];
+        v16f acc[MB][2];
 #pragma unroll
-        for (int r = 0; r < 2 * K; ++r) p0[r] = p1[r] = 0.0f;
-#pragma unroll 4
-        for (int ii = 0; ii < 32; ++ii) {
-            const int i = i0 + ii;
-            float u0 = 0.0f, u1 = 0.0f;
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int s = 0; s < K; ++s) {
-                u0 += wk[s][i] * d0[s];
-                u1 += wk[s][i] * d1[s];
+            for (int q = 0; q < 16; ++q) acc[mb][0][q] = acc[mb][1][q] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int i = ir + 16 * ks;
+            uint32_t pk[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float u0 = 0.0f, u1 = 0.0f;
+#pragma unroll
+                for (int s = 0; s < K; ++s) {
+                    u0 += wk[i + e][s] * d0[s];
+                    u1 += wk[i + e][s] * d1[s];
+                }
+                pk[e] = pk_bf16(__uint_as_float(sv[ks][e] << 16) * scale + u0,
+                                __uint_as_float(sv[ks][e] & 0xffff0000u) * scale + u1);
+                *(uint32_t*)(st + (size_t)(i + e) * D + jc) = pk[e];
             }
-            const float c0 = rbf(bf2f(sv[ii] & 0xffff) * scale + u0);
-            const float c1 = rbf(bf2f(sv[ii] >> 16) * scale + u1);
-            *(uint32_t*)(st + (size_t)i * D + j0) = pk_bf16(c0, c1);
+            v4i be, bo;  // column jc (low halves) and jc + 1 (high halves), rows i .. i + 7
 #pragma unroll
-            for (int r = 0; r < 2 * K; ++r) {
-                const float rv = r < K ? kn[r][i] : qn[r - K][i];
-                p0[r] += rv * c0;
-                p1[r] += rv * c1;
+            for (int q = 0; q < 4; ++q) {
+                be[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x05040100u);
+                bo[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x07060302u);
+            }
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const v8bf16 av = *(const v8bf16*)&kq3[32 * mb + (lane & 31)][i];
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, be), acc[mb][0], 0, 0, 0);
+                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, bo), acc[mb][1], 0, 0, 0);
             }
         }
+        // Accumulator register 4 q + t of block mb holds row 32 mb + 8 q + 4 (lane / 32) + t; row r of [k; q] is the
+        // sum of rows r, RS + r and 2 RS + r, which all sit in this lane (RS is a multiple of 8).
 #pragma unroll
-        for (int r = 0; r < 2 * K; ++r) *(float2*)&part[wave][r][j0] = make_float2(p0[r], p1[r]);
+        for (int a8 = 0; a8 < (2 * K + 7) / 8; ++a8)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int r = 8 * a8 + 4 * (lane >> 5) + t;
+                float ve = 0.0f, vo = 0.0f;
+#pragma unroll
+                for (int sp = 0; sp < 3; ++sp) {
+                    const int base = sp * RS + 8 * a8;  // multiple of 8
+                    const int mb = base / 32, reg = 4 * ((base % 32) / 8) + t;
+                    ve += acc[mb][0][reg];
+                    vo += acc[mb][1][reg];
+                }
+                if (r < 2 * K) *(float2*)&part[wave >> 1][r][jc] = make_float2(ve, vo);
+            }
     }
     __syncthreads();
 
@@ -297,8 +363,8 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(const GdnArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < K; ++t) {
-            const float ks = ((part[0][t][j] + part[1][t][j]) + part[2][t][j]) + part[3][t][j];
-            const float qs = ((part[0][K + t][j] + part[1][K + t][j]) + part[2][K + t][j]) + part[3][K + t][j];
+            const float ks = part[0][t][j] + part[1][t][j];
+            const float qs = part[0][K + t][j] + part[1][K + t][j];
             float delta = mixed[t][2 * D + j] - expf(cum[t]) * ks;
 #pragma unroll
             for (int s = 0; s < t; ++s) delta = delta - (expf(cum[t] - cum[s]) * kk[t][s]) * dl[s];
@@ -357,6 +423,8 @@ static hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
 }
 
 hipError_t q38_gdn_verify(const GdnArgs& a, hipStream_t stream) {
+    if (a.gate_groups < 1 || a.gate_groups > 8 || a.K < 1 || a.K > 8 || a.Hv % a.Hk || a.C != 2 * a.Hk * 128 + a.Hv * 128)
+        return hipErrorInvalidValue;
     switch (a.K) {
         case 1: return launch_gdn<1>(a, stream);
         case 2: return launch_gdn<2>(a, stream);
