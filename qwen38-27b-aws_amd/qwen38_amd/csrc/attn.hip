@@ -8,10 +8,11 @@
 // separate bf16 matmuls added in bf16; times bf16 sigmoid(gate). The masked entries of the reference's full-length
 // softmax contribute exact zeros (exp of about -600 underflows), so only visible positions are read.
 //
-// Rows whose visible context is at most 512 positions (one chunk) take one launch, attn_fused (KV head, row): sixteen
-// waves score 32 positions each, the softmax completes in the workgroup, and each wave then multiplies the weights
-// with 16 dims of V. Longer contexts take two launches, so that every (row, KV head) spreads over several
-// workgroups (each kernel skips the rows the other path takes):
+// Rows whose visible context is at most NB * 512 positions take one launch, attn_fused (KV head, row): sixteen
+// waves score NB blocks of 32 positions each, the softmax completes in the workgroup, and each wave then multiplies
+// the weights with 16 dims of V (NB = 2 for up to 32 query rows per KV head, else 1). Longer contexts take two
+// launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the other path
+// takes):
 //   attn_scores (chunk of 512 cached positions, KV head, row): q norm + RoPE, the chunk's scores by MFMA (sixteen
 //       waves, one block of 32 positions each), the chunk's per-row max m_c, probabilities e = exp(s - m_c) (stored as float32) and
 //       their sum s_c. Chunk 0 also normalises and rotates the step's own keys and scores them.
@@ -195,14 +196,15 @@ __device__ __forceinline__ void own_scores(const bf16_t* qb, const bf16_t* kb, i
     }
 }
 
-// Whole verify attention of one (row, KV head) whose visible context fits one chunk (at most ATTN_CHUNK positions):
-// 16 waves; wave w scores positions 32w .. 32w + 31, then takes dims 16w .. 16w + 15 of the output. The softmax is
-// complete inside the workgroup, so the weights are the reference's bf16(e^(s - M) / S) exactly; they go through LDS
-// to the weights x V product (v_mfma_f32_16x16x32_bf16: A = 16 query rows x 32 positions, B = 32 positions x 16 dims).
-template <int QT>
+// Whole verify attention of one (row, KV head) whose visible context is at most NB * ATTN_CHUNK positions: 16 waves;
+// wave w scores the blocks of positions 32 (16 nb + w) + [0, 32), nb < NB, then takes dims 16w .. 16w + 15 of the
+// output. The softmax is complete inside the workgroup, so the weights are the reference's bf16(e^(s - M) / S) exactly;
+// they go through LDS to the weights x V product (v_mfma_f32_16x16x32_bf16: A = 16 query rows x 32 positions, B = 32
+// positions x 16 dims), one pass of 16 position blocks per nb.
+template <int QT, int NB>
 __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
-    constexpr int RT = QT * 2;                 // 16-row tiles of query rows
-    constexpr int WPITCH = ATTN_CHUNK + 8;     // bf16 per weight row in LDS (rows start 4 banks apart)
+    constexpr int RT = QT * 2;                   // 16-row tiles of query rows
+    constexpr int WPITCH = NB * ATTN_CHUNK + 8;  // bf16 per weight row in LDS (rows start 4 banks apart)
     __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
     __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];
     __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX][256];
@@ -213,13 +215,13 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b);
-    if (npos > ATTN_CHUNK) return;  // the chunked kernels take this row
+    if (npos > NB * ATTN_CHUNK) return;  // the chunked kernels take this row
     const size_t head = (size_t)b * a.Hkv + kvh;
-    const bool scored = wave * 32 < npos;
+    auto scored = [&](int nb) { return (nb * SW + wave) * 32 < npos; };
     const int dcol = wave * 16 + (lane & 15);  // output dim of this lane
 
     v8bf kf[16];
-    if (scored) load_keys(a, head, wave * 32, lane, kf);
+    if (scored(0)) load_keys(a, head, wave * 32, lane, kf);
     uint32_t gate[RT][4];  // gates of this lane's output rows rt*16 + 4 (l / 16) + i, dim dcol
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -231,21 +233,30 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     project_rows<QT, SW>(a, b, kvh, wave, lane, true, qb, kb, nullptr, vown);
     __syncthreads();
 
-    v16f sacc[QT];
+    v16f sacc[NB][QT];
     float lmax[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) lmax[qt] = -INFINITY;
-    if (scored) score_block<QT>(kf, qb, lane, wave * 32, npos, sacc, lmax);
+    if (scored(0)) score_block<QT>(kf, qb, lane, wave * 32, npos, sacc[0], lmax);
+#pragma unroll
+    for (int nb = 1; nb < NB; ++nb)
+        if (scored(nb)) {
+            load_keys(a, head, (nb * SW + wave) * 32, lane, kf);
+            score_block<QT>(kf, qb, lane, (nb * SW + wave) * 32, npos, sacc[nb], lmax);
+        }
     if (wave == SW - 1) own_scores<QT>(qb, kb, lane, K, NQ, [&](int q, int tp, float v) { sown[q][tp] = v; });
 
-    // This wave's V columns over the visible positions: lane l holds dim dcol, positions 32j + 8 (l / 16) .. + 7.
-    // Issued only once the keys are consumed (the compiler barrier keeps both out of registers at once).
+    // This wave's V columns over the first 16 position blocks: lane l holds dim dcol, positions 32j + 8 (l / 16) ..
+    // + 7. Issued only once the keys are consumed (the compiler barrier keeps both out of registers at once).
     asm volatile("" ::: "memory");
     const int nblk = (npos + 31) >> 5;
     v8bf vf[SW];
     const bf16_t* vp = a.v_cache + head * S * 256 + dcol * 32 + 8 * (lane >> 4);
+    auto load_v = [&](int nb) {
 #pragma unroll
-    for (int j = 0; j < SW; ++j) vf[j] = load8(vp + (size_t)max(min(j, nblk - 1), 0) * 8192);  // past nblk: unused
+        for (int j = 0; j < SW; ++j) vf[j] = load8(vp + (size_t)max(min(nb * SW + j, nblk - 1), 0) * 8192);  // past nblk: unused
+    };
+    load_v(0);
 
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -268,12 +279,15 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         lsum[qt] = 0.0f;
-        if (!scored) continue;
         const float m = mrow[qt * 32 + (lane & 31)];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            sacc[qt][i] = expf(sacc[qt][i] - m);
-            lsum[qt] += sacc[qt][i];
+        for (int nb = 0; nb < NB; ++nb) {
+            if (!scored(nb)) continue;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sacc[nb][qt][i] = expf(sacc[nb][qt][i] - m);
+                lsum[qt] += sacc[nb][qt][i];
+            }
         }
     }
 #pragma unroll
@@ -298,16 +312,18 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
 
     // bf16 weights of this wave's positions into LDS (rows of WPITCH), four consecutive positions per store.
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        if (!scored) continue;
-        const int q = qt * 32 + (lane & 31);
-        const float iv = irow[q];
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            *(uint2*)(wts + q * WPITCH + wave * 32 + g * 8 + (lane >> 5) * 4) =
-                make_uint2(pk_bf16(sacc[qt][4 * g] * iv, sacc[qt][4 * g + 1] * iv),
-                           pk_bf16(sacc[qt][4 * g + 2] * iv, sacc[qt][4 * g + 3] * iv));
-    }
+        for (int qt = 0; qt < QT; ++qt) {
+            if (!scored(nb)) continue;
+            const int q = qt * 32 + (lane & 31);
+            const float iv = irow[q];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(uint2*)(wts + q * WPITCH + (nb * SW + wave) * 32 + g * 8 + (lane >> 5) * 4) =
+                    make_uint2(pk_bf16(sacc[nb][qt][4 * g] * iv, sacc[nb][qt][4 * g + 1] * iv),
+                               pk_bf16(sacc[nb][qt][4 * g + 2] * iv, sacc[nb][qt][4 * g + 3] * iv));
+        }
     __syncthreads();
 
     // Weights x V for this wave's 16 dims; then the own part, the gate and the e5m2 activation bytes.
@@ -315,12 +331,19 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < SW; ++j)
-        if (j < nblk)
+    for (int nb = 0; nb < NB; ++nb) {
+        if (nb > 0) {
+            if (nb * SW >= nblk) break;
+            load_v(nb);
+        }
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    load8(wts + (rt * 16 + (lane & 15)) * WPITCH + j * 32 + 8 * (lane >> 4)), vf[j], acc[rt], 0, 0, 0);
+        for (int j = 0; j < SW; ++j)
+            if (nb * SW + j < nblk)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        load8(wts + (rt * 16 + (lane & 15)) * WPITCH + (nb * SW + j) * 32 + 8 * (lane >> 4)), vf[j], acc[rt], 0, 0, 0);
+    }
     const int act_k = a.Hq * 256;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -356,7 +379,7 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b);
-    if (npos <= ATTN_CHUNK) return;  // attn_fused takes this row
+    if (npos <= a.fused_max) return;  // attn_fused takes this row
     const int p_lo = c * ATTN_CHUNK, p_hi = min(p_lo + ATTN_CHUNK, npos);
     const bool first = c == 0;  // also does the step's own keys
     if (!first && p_lo >= p_hi) return;
@@ -449,7 +472,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b), nblk = (npos + 31) >> 5;
-    if (npos <= ATTN_CHUNK) return;  // attn_fused takes this row
+    if (npos <= a.fused_max) return;  // attn_fused takes this row
     const size_t head = (size_t)hh;
     const int dq = quarter * 64;
     const float* pr = a.probs + head * ATTN_QMAX * S;
@@ -613,10 +636,11 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
     }
 }
 
-template <int QT>
-hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_fused_kernel<QT>, dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
-    if (a.S > ATTN_CHUNK) {
+template <int QT, int NB>
+hipError_t launch_attn(AttnArgs a, hipStream_t stream) {
+    a.fused_max = NB * ATTN_CHUNK;
+    hipLaunchKernelGGL((attn_fused_kernel<QT, NB>), dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+    if (a.S > a.fused_max) {
         hipLaunchKernelGGL(attn_scores_kernel<QT>, dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
         hipLaunchKernelGGL(attn_out_kernel<QT>, dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
     }
@@ -628,5 +652,6 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
 hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream) {
     const int NQ = a.Hq / a.Hkv * a.K;
     if (NQ > ATTN_QMAX || a.K > ATTN_KMAX || (long)a.nchunks * ATTN_CHUNK < a.S) return hipErrorInvalidValue;
-    return NQ <= 32 ? launch_attn<1>(a, stream) : launch_attn<2>(a, stream);
+    // Two position blocks per wave need 66 KB of bf16 weights in LDS at 32 query rows; 64 rows keep one.
+    return NQ <= 32 ? launch_attn<1, 2>(a, stream) : launch_attn<2, 1>(a, stream);
 }

@@ -103,6 +103,7 @@ struct AttnArgs {
     float* kv_own;          // [B*Hkv][2][ATTN_KMAX][256]: the step's keys (normed, rotated) and values
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
+    int fused_max;          // set by the launcher: rows with at most this many visible positions take attn_fused
 };
 
 struct PickArgs {

@@ -1,10 +1,11 @@
 """Full attention at long contexts, through the MTP step (one fc + full-attention layer + norm) against the oracle.
 
-The golden scenario's contexts fit in one chunk of cached positions; these cases spread each (row, KV head) over many
-chunks (the tiny block at 2048 positions: 16 chunks of 128), take the 64-query-row path (16 query heads over 2 KV
-heads, 8 tokens), and include an empty cache and an inactive row (which writes the cache tail). Checked: the MTP output
-(one layer, so the north-star 2e-2 per-row bound without a floor factor), the positions the step writes in both caches
-(1e-2: the keys are normed and rotated in bf16 by both sides), and every other cache position unchanged.
+The golden scenario's contexts are short; these cases spread each (row, KV head) over many chunks (the tiny block at
+2048 positions), take the one-launch path with one and with two blocks of 512 positions per wave, take the
+64-query-row path (16 query heads over 2 KV heads, 8 tokens), and include an empty cache and an inactive row (which
+writes the cache tail). Checked: the MTP output (one layer, so the north-star 2e-2 per-row bound without a floor
+factor), the positions the step writes in both caches (1e-2: the keys are normed and rotated in bf16 by both sides),
+and every other cache position unchanged.
 """
 
 from __future__ import annotations
@@ -26,6 +27,8 @@ CASES = {
     "tiny-2048-16chunks": (8, 4, 4, 2048, [1900, 700, 0, 1500], [True, True, True, False]),
     "64rows-1024": (16, 2, 8, 1024, [1000, 333], [True, True]),
     "tail-edge": (8, 2, 4, 512, [507, 511], [True, False]),
+    # contexts between one and two blocks of 512 positions per wave (the one-launch path up to 1024)
+    "fused-two-blocks": (8, 4, 4, 1024, [1019, 513, 767, 1000], [True, True, True, False]),
 }
 
 
