@@ -4,6 +4,10 @@
  * Neuron graphs and the CPU path that stands in for them:
  *   q38_verify       <- `verify(**verify_inputs(...))`, the K-token graph: Qwen38Step.forward with `accepted`
  *                       (reference qwen38_inf2/model.py:933-995; call site scheduler.py:288; inputs generate.py:72-87)
+ *   q38_decode       <- `step(**batch_step_inputs(...))`, the one-token graph: Qwen38Step.forward's decode form
+ *                       (model.py:983-995; call sites generate.py:251,258,290; inputs generate.py:34-60)
+ *   q38_copy_states  <- the same graph with save_slot / restore_slot (model.py:988-992, GatedDeltaNetStep.copy_states
+ *                       model.py:456-464; call sites scheduler.py:119,133; inputs generate.py:110-116)
  *   q38_mtp_step     <- `mtp(hidden=..., inputs_embeds=..., **mtp_step_inputs(...))`, MTPStep.forward
  *                       (model.py:843-860; call sites scheduler.py:179,192)
  *   q38_head_groupmax<- the head graph `run_graph(hidden=...)`, HeadStep.forward (model.py:890-900;
@@ -46,6 +50,7 @@ typedef struct q38_config {
     int linear_conv_kernel_dim;
     float rms_norm_eps;
     int batch_size, verify_tokens, max_seq_len, mtp;
+    int saved_states; /* a saved recurrent and conv state per row, for q38_copy_states (reference saved_states) */
 } q38_config;
 
 const char* q38_last_error(void);
@@ -73,6 +78,7 @@ void q38_destroy(q38_handle* h);
  *   linear_attn.pending_delta f32 [2][B][K][Hv][128], linear_attn.pending_decay f32 [2][B][K][Hv],
  *   linear_attn.pending_input bf16 [2][B][K][C]: two halves, the current one given by q38_parity
  *   self_attn.k_cache bf16 [B][Hkv][S][hd]; self_attn.v_cache bf16 [B][Hkv][S/32][hd][32] (transposed per 32 positions)
+ *   with saved_states: linear_attn.saved_state bf16 [B][Hv][128][128], linear_attn.saved_conv bf16 [B][C][3]
  * Scratch: workspace (model-wide; its GEMM counters are zeroed when it is bound). */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
 int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
@@ -115,6 +121,20 @@ size_t q38_tiles_size(int rows, int k);
  * commits each row's `accepted` tokens of the previous step, and flips the parity. */
 int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
                const float* active, const int32_t* accepted, uint16_t* out_hidden, void* stream);
+
+/* One decode step over all B rows, one token each: embeds bf16 [B][1][H]; cos, sin bf16 [B][1][rotary_dim];
+ * position int32 [B] (0 starts a new sequence: the row's gated-delta states restart from zero); active f32 [B] (0 keeps
+ * the row's states and cache exactly). Writes the last layer's hidden state bf16 [B][1][H] and flips the parity (the
+ * conv states go to the other half). The gated-delta layers run the recurrent form (GatedDeltaNetStep.forward,
+ * model.py:347-374), the attention layers FullAttentionStep.forward (model.py:610-639). A verify step after it takes
+ * accepted = 0, as in the reference. */
+int q38_decode(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
+               const float* active, uint16_t* out_hidden, void* stream);
+
+/* Save (to_saved != 0) or restore one row's gated-delta recurrent and conv states in every gated-delta layer; slot is
+ * int32 [1] on the device (a slot outside [0, B) copies nothing). Needs saved_states in the config and the saved
+ * buffers bound. */
+int q38_copy_states(q38_handle* h, const int32_t* slot, int to_saved, void* stream);
 
 /* One MTP step: hidden, embeds bf16 [B][K][H]; cos, sin [B][K][rotary_dim]; position, active [B]. Writes bf16
  * [B][K][H]. */

@@ -142,6 +142,8 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
         if (name == "linear_attn.pending_delta") return 2 * B * K * Hv * dk * 4;
         if (name == "linear_attn.pending_decay") return 2 * B * K * Hv * 4;
         if (name == "linear_attn.pending_input") return 2 * B * K * C * 2;
+        if (h->cfg.saved_states && name == "linear_attn.saved_state") return B * Hv * dk * dk * 2;
+        if (h->cfg.saved_states && name == "linear_attn.saved_conv") return B * C * 3 * 2;
         return 0;
     }
     if ((r = fp8("self_attn.qkv", Hq * hd * 2 + 2 * Hkv * hd, H))) return r;
@@ -220,6 +222,23 @@ struct StepIO {
     const int32_t* position;
     const float* active;
     const int32_t* accepted;
+    bool decode = false;  // one token per row, the gated-delta layers' recurrent form
+};
+
+// Tokens per row of the call in progress: the verify width by default, 1 for a decode step (restored on exit).
+struct TokensScope {
+    q38_handle* h;
+    int K, T, Tpad;
+    TokensScope(q38_handle* h_, int k) : h(h_), K(h_->K), T(h_->T), Tpad(h_->Tpad) {
+        h->K = k;
+        h->T = h->B * k;
+        h->Tpad = pad_tokens(h->T);
+    }
+    ~TokensScope() {
+        h->K = K;
+        h->T = T;
+        h->Tpad = Tpad;
+    }
 };
 
 // Mixer of layer `li` on act_h; leaves x += mixer and act_h = e5m2(post_attention_layernorm(x)).
@@ -252,8 +271,9 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         if (!ok) return 1;
         const size_t BKC = (size_t)h->B * h->K * h->C;
         uint16_t* z = (uint16_t*)h->ws(h->off_z);
-        if (gemm(h, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, pin + wr * BKC, h->C, h->C, z, h->Hv * h->dk,
-                 stream))
+        // A verify step's qkv output is also its pending input snapshot; a decode step's goes to scratch.
+        uint16_t* qkv_out = io.decode ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
+        if (gemm(h, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
             return 1;
         GatesArgs ga{};
         ga.x = (const bf16_t*)h->ws(h->off_hbf);
@@ -271,7 +291,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         g.Hk = h->Hk;
         g.Hv = h->Hv;
         g.C = h->C;
-        g.qkv_new = pin + wr * BKC;
+        g.qkv_new = qkv_out;
         g.qkv_old = pin + rd * BKC;
         g.z = z;
         g.gate_part = ga.part;
@@ -296,7 +316,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         g.decay_new = pdecay + wr * decayn;
         g.act = act_mid;
         g.eps = h->cfg.rms_norm_eps;
-        HIP_TRY(q38_gdn_verify(g, stream));
+        HIP_TRY(io.decode ? q38_gdn_decode(g, stream) : q38_gdn_verify(g, stream));
         kmid = h->Hv * h->dk;
     } else {
         auto qkv_t = get<uint8_t>(h, "self_attn.qkv.tiles", li, &ok);
@@ -622,6 +642,61 @@ int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const
     }
     h->parity = wr;
     return 0;
+}
+
+int q38_decode(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
+               const float* active, uint16_t* out_hidden, void* stream_) {
+    if (!h || !embeds || !cos || !sin || !position || !active || !out_hidden) return fail("null argument");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto in0 = get<uint16_t>(h, "input_layernorm", 0, &ok);
+    if (!ok) return 1;
+    TokensScope one(h, 1);
+    const int L = h->cfg.num_layers, rd = h->parity, wr = 1 - h->parity;
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    uint16_t* hbf = is_linear(h, 0) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
+    StepIO io{cos, sin, position, active, nullptr, true};
+    for (int li = 0; li < L; ++li) {
+        if (run_mixer(h, li, io, rd, wr, stream)) return 1;
+        if (run_mlp(h, li, li + 1 < L ? li + 1 : -1, out_hidden, false, stream)) return 1;
+    }
+    h->parity = wr;  // the conv states were written to the other half
+    return 0;
+}
+
+int q38_copy_states(q38_handle* h, const int32_t* slot, int to_saved, void* stream_) {
+    if (!h || !slot) return fail("null argument");
+    if (!h->cfg.saved_states) return fail("this handle keeps no saved states (config saved_states is 0)");
+    hipStream_t stream = (hipStream_t)stream_;
+    CopyStatesArgs a{};
+    a.state_row = (size_t)h->Hv * h->dk * h->dk;
+    a.conv_row = (size_t)h->C * 3;
+    a.slot = slot;
+    a.rows = h->B;
+    a.to_saved = to_saved ? 1 : 0;
+    const size_t convn = (size_t)h->B * h->C * 3;
+    bool ok = true;
+    auto flush = [&]() -> int {
+        if (a.n) HIP_TRY(q38_copy_states(a, stream));
+        a.n = 0;
+        return 0;
+    };
+    for (int li = 0; li < h->cfg.num_layers; ++li) {
+        if (!is_linear(h, li)) continue;
+        auto st = get<uint16_t>(h, "linear_attn.recurrent_state", li, &ok);
+        auto conv = get<uint16_t>(h, "linear_attn.conv_state", li, &ok);
+        auto sst = get<uint16_t>(h, "linear_attn.saved_state", li, &ok);
+        auto sconv = get<uint16_t>(h, "linear_attn.saved_conv", li, &ok);
+        if (!ok) return 1;
+        a.state[a.n] = st;
+        a.conv[a.n] = conv + h->parity * convn;  // the current half
+        a.saved_state[a.n] = sst;
+        a.saved_conv[a.n] = sconv;
+        if (++a.n == COPY_STATES_MAX && flush()) return 1;
+    }
+    return flush();
 }
 
 int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin,

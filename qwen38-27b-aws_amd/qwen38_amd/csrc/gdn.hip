@@ -409,6 +409,189 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     }
 }
 
+// `GatedDeltaNetStep.forward` (model.py:347-374): one token per row, the recurrent form. One workgroup per (row, value
+// head), 4 waves; wave w holds state rows [32w, 32w + 32), lane l columns 2l, 2l + 1.
+//   keep = 0 for an active row at position 0; the conv window is [conv_state * keep, qkv], the new conv state its last
+//   three entries (the old one for an inactive row); mixed = bf16 sum of bf16 tap products, SiLU in bf16.
+//   S = float(S) * keep * e^g; delta = (v - S^T k) * beta; S += k delta^T (product, then sum: two roundings, as torch
+//   computes them); S stored in bf16; out = S^T q from the float32 S; then the gated RMS norm times SiLU(z), e5m2.
+__global__ __launch_bounds__(256) void gdn_decode_kernel(const GdnArgs a) {
+    constexpr int D = 128, GMAX = 8;
+    __shared__ float mixed[3 * D];
+    __shared__ float qn[D], kn[D];
+    __shared__ float part[4][D];
+    __shared__ float dl[D], ob[D];
+    __shared__ float s_gate[2];
+
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int Hv = a.Hv, Hk = a.Hk, C = a.C;
+    const int rep = Hv / Hk, kh = h / rep;
+    const bool owner = (h % rep) == 0;  // writes the shared key-head conv channels
+    const bool on = a.active[b] > 0.5f;
+    const float keep = (a.position[b] == 0 && on) ? 0.0f : 1.0f;
+
+    // Every global load first (see gdn_verify_kernel).
+    float gp[GMAX];
+    if (tid < 2) {
+        const float* p = a.gate_part + (size_t)b * 2 * Hv + (tid ? Hv + h : h);
+#pragma unroll
+        for (int gi = 0; gi < GMAX; ++gi) gp[gi] = p[(size_t)min(gi, a.gate_groups - 1) * a.B * 2 * Hv];
+    }
+    const bool conv_thread = tid < 3 * D / 2;
+    const int cgrp = (2 * tid) / D, cj = (2 * tid) % D;
+    const int cc = cgrp == 0 ? kh * D + cj : cgrp == 1 ? Hk * D + kh * D + cj : 2 * Hk * D + h * D + cj;
+    uint32_t cv_old[3], cv_new = 0;
+    uint4 cv_w = make_uint4(0, 0, 0, 0);
+    if (conv_thread) {
+        const uint32_t* po = (const uint32_t*)(a.conv_old + ((size_t)b * C + cc) * 3);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) cv_old[q] = po[q];
+        cv_new = *(const uint32_t*)(a.qkv_new + (size_t)b * C + cc);
+        cv_w = *(const uint4*)(a.conv_w + (size_t)cc * 4);
+    }
+    const int j0 = 2 * lane, i0 = 32 * wave;
+    bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
+    uint32_t sv[32];
+#pragma unroll
+    for (int ii = 0; ii < 32; ++ii) sv[ii] = *(const uint32_t*)(st + (size_t)(i0 + ii) * D + j0);
+    bf16_t z_in[2] = {0, 0};
+    if (wave == 0) {
+        z_in[0] = a.z[(size_t)b * Hv * D + h * D + lane];
+        z_in[1] = a.z[(size_t)b * Hv * D + h * D + lane + 64];
+    }
+    const float nw_lo = bf2f(a.norm_w[lane]), nw_hi = bf2f(a.norm_w[lane + 64]);
+
+    // Gates (model.py:333-337, 366-368), as in gdn_verify_kernel.
+    if (tid < 2) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GMAX; ++gi)
+            if (gi < a.gate_groups) sum += gp[gi];
+        const float lin = rbf(sum), act = a.active[b];
+        s_gate[tid] = tid ? -expf(bf2f(a.a_log[h])) * softplusf_(lin + bf2f(a.dt_bias[h])) * act : rbf(sigmoidf_(lin)) * act;
+    }
+
+    // Conv (model.py:357-361).
+    if (conv_thread) {
+        const float old6[6] = {lo_bf(cv_old[0]), hi_bf(cv_old[0]), lo_bf(cv_old[1]),
+                               hi_bf(cv_old[1]), lo_bf(cv_old[2]), hi_bf(cv_old[2])};
+        const uint32_t cw[4] = {cv_w.x, cv_w.y, cv_w.z, cv_w.w};
+        float next[2][3];
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            const float x = ch ? hi_bf(cv_new) : lo_bf(cv_new);
+            const float win[4] = {old6[3 * ch] * keep, old6[3 * ch + 1] * keep, old6[3 * ch + 2] * keep, x};
+#pragma unroll
+            for (int q = 0; q < 3; ++q) next[ch][q] = on ? win[q + 1] : old6[3 * ch + q];
+            const float w0 = lo_bf(cw[2 * ch]), w1 = hi_bf(cw[2 * ch]), w2 = lo_bf(cw[2 * ch + 1]), w3 = hi_bf(cw[2 * ch + 1]);
+            const float m = rbf(((rbf(win[0] * w0) + rbf(win[1] * w1)) + rbf(win[2] * w2)) + rbf(win[3] * w3));
+            mixed[2 * tid + ch] = rbf(m * rbf(sigmoidf_(m)));
+        }
+        if (cgrp == 2 || owner) {
+            uint32_t* dst = (uint32_t*)(a.conv_new + ((size_t)b * C + cc) * 3);
+            dst[0] = pk_bf16(next[0][0], next[0][1]);
+            dst[1] = pk_bf16(next[0][2], next[1][0]);
+            dst[2] = pk_bf16(next[1][1], next[1][2]);
+        }
+    }
+    __syncthreads();
+
+    // l2 norms of q and k (model.py:60-61, 322-331): waves 0 and 1.
+    if (wave < 2) {
+        const float x0 = mixed[wave * D + lane], x1 = mixed[wave * D + lane + 64];
+        const float rs = 1.0f / sqrtf(warp_sum(x0 * x0 + x1 * x1) + 1e-6f);
+        if (wave) {
+            kn[lane] = x0 * rs;
+            kn[lane + 64] = x1 * rs;
+        } else {
+            qn[lane] = (x0 * rs) / 11.313708498984761f;
+            qn[lane + 64] = (x1 * rs) / 11.313708498984761f;
+        }
+    }
+    __syncthreads();
+
+    // Decayed state and its read with k.
+    const float eg = expf(s_gate[1]);
+    float s0[32], s1[32];
+    float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < 32; ++ii) {
+        s0[ii] = (lo_bf(sv[ii]) * keep) * eg;
+        s1[ii] = (hi_bf(sv[ii]) * keep) * eg;
+        const float k = kn[i0 + ii];
+        p0 += s0[ii] * k;
+        p1 += s1[ii] * k;
+    }
+    *(float2*)&part[wave][j0] = make_float2(p0, p1);
+    __syncthreads();
+    if (tid < D) dl[tid] = (mixed[2 * D + tid] - (((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid])) * s_gate[0];
+    __syncthreads();
+
+    // S += k delta^T, stored in bf16; out = S^T q from the float32 state.
+    {
+        const float d0 = dl[j0], d1 = dl[j0 + 1];
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 32; ++ii) {
+            const float k = kn[i0 + ii], q = qn[i0 + ii];
+            const float n0 = __fadd_rn(s0[ii], __fmul_rn(k, d0)), n1 = __fadd_rn(s1[ii], __fmul_rn(k, d1));
+            *(uint32_t*)(st + (size_t)(i0 + ii) * D + j0) = pk_bf16(n0, n1);
+            o0 += n0 * q;
+            o1 += n1 * q;
+        }
+        __syncthreads();  // part's first use is read
+        *(float2*)&part[wave][j0] = make_float2(o0, o1);
+    }
+    __syncthreads();
+    if (tid < D) ob[tid] = rbf(((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid]);
+    __syncthreads();
+
+    // Gated RMS norm (model.py:339-345) and the e5m2 input of out_proj.
+    if (wave == 0) {
+        const float x0 = ob[lane], x1 = ob[lane + 64];
+        const float r = 1.0f / sqrtf(warp_sum(x0 * x0 + x1 * x1) / 128.0f + a.eps);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int j = lane + half * 64;
+            float hv = rbf((half ? x1 : x0) * r);
+            hv = rbf((half ? nw_hi : nw_lo) * hv);
+            const float zf = bf2f(z_in[half]);
+            a.act[act_offset(b, h * D + j, Hv * D)] = (uint8_t)e5m2_byte(rbf(hv * (zf * sigmoidf_(zf))));
+        }
+    }
+}
+
+hipError_t q38_gdn_decode(const GdnArgs& a, hipStream_t stream) {
+    if (a.gate_groups < 1 || a.gate_groups > 8 || a.K != 1 || a.Hv % a.Hk || a.C != 2 * a.Hk * 128 + a.Hv * 128)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_decode_kernel, dim3(a.Hv, a.B), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+// Row `slot` of each layer's recurrent and conv state, live <-> saved (GatedDeltaNetStep.copy_states, model.py:456-464).
+// Grid (workgroups per layer, layers); 16-byte copies.
+__global__ __launch_bounds__(256) void copy_states_kernel(const CopyStatesArgs a) {
+    const int layer = blockIdx.y, slot = *a.slot;
+    if (slot < 0 || slot >= a.rows) return;
+    const bf16_t* src_s = a.to_saved ? a.state[layer] : a.saved_state[layer];
+    bf16_t* dst_s = a.to_saved ? a.saved_state[layer] : a.state[layer];
+    const size_t n16 = a.state_row / 8;  // 16-byte chunks of the row
+    const uint4* src = (const uint4*)(src_s + (size_t)slot * a.state_row);
+    uint4* dst = (uint4*)(dst_s + (size_t)slot * a.state_row);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+    if (blockIdx.x == 0) {
+        const bf16_t* src_c = (a.to_saved ? a.conv[layer] : a.saved_conv[layer]) + (size_t)slot * a.conv_row;
+        bf16_t* dst_c = (a.to_saved ? a.saved_conv[layer] : a.conv[layer]) + (size_t)slot * a.conv_row;
+        for (size_t i = threadIdx.x; i < a.conv_row; i += 256) dst_c[i] = src_c[i];
+    }
+}
+
+hipError_t q38_copy_states(const CopyStatesArgs& a, hipStream_t stream) {
+    if (a.n < 1 || a.n > COPY_STATES_MAX || a.state_row % 8 || a.rows < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(copy_states_kernel, dim3(64, a.n), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t q38_gdn_gates(const GatesArgs& a, hipStream_t stream) {
     if (a.H % (64 * a.groups) || a.H / (64 * a.groups) > 16) return hipErrorInvalidValue;
     dim3 grid(((a.T + 31) / 32) * ((2 * a.Hv + 31) / 32), a.groups);

@@ -124,6 +124,24 @@ hipError_t q38_head_norm(const bf16_t* hidden, const bf16_t* w, float eps, int H
 hipError_t q38_embed(const int* ids, int n, const bf16_t* table, int V, int H, bf16_t* out, hipStream_t stream);
 hipError_t q38_gdn_gates(const GatesArgs& a, hipStream_t stream);
 hipError_t q38_gdn_verify(const GdnArgs& a, hipStream_t stream);
+// One decode token per row (a.K == 1): reads qkv_new, z, the gate partials, conv_old and the state; writes conv_new,
+// the state in place and act. The snapshot fields are unused.
+hipError_t q38_gdn_decode(const GdnArgs& a, hipStream_t stream);
+// Copy one row of every listed gated-delta layer's recurrent state ([rows][Hv][128][128] bf16) and conv state
+// ([rows][C][3] bf16) between the live buffers and the saved ones; the row is read from `slot` on the device.
+#define COPY_STATES_MAX 64  // layers per launch (the pointer tables keep the arguments at 2 KiB)
+struct CopyStatesArgs {
+    int n;                       // layers
+    bf16_t* state[COPY_STATES_MAX];
+    bf16_t* saved_state[COPY_STATES_MAX];
+    bf16_t* conv[COPY_STATES_MAX];
+    bf16_t* saved_conv[COPY_STATES_MAX];
+    size_t state_row, conv_row;  // bf16 elements per row
+    const int* slot;
+    int rows;                    // live rows (slot must be below)
+    int to_saved;
+};
+hipError_t q38_copy_states(const CopyStatesArgs& a, hipStream_t stream);
 hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream);
 hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream);
 hipError_t q38_accept(const int* picks, const int* drafts, const float* active, int B, int K, int* match, int* accepted,

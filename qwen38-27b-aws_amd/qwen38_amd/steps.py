@@ -2,6 +2,10 @@
 
 * `VerifyStep.__call__(inputs_embeds, cos, sin, position, active, accepted)` -> hidden ``[B, K, H]``: the reference's
   verify graph, `Qwen38Step.forward` with `accepted` (qwen38_inf2/model.py:933-995, called at scheduler.py:288).
+* `StepGraph.__call__(inputs_embeds, cos, sin, position, active)` -> hidden ``[B, 1, H]``: the one-token decode graph
+  (`Qwen38Step.forward`'s decode form, called at generate.py:251,258,290); with ``save_slot`` or ``restore_slot``
+  instead, it saves or restores one row's gated-delta states and returns ``inputs_embeds`` (model.py:988-992, called
+  at scheduler.py:119,133); with ``accepted`` it is the verify graph.
 * `MTPStep.__call__(hidden, inputs_embeds, cos, sin, position, active)` -> ``[B, K, H]``: `MTPStep.forward`
   (model.py:843-860, called at scheduler.py:179,192).
 * `HeadGraph.__call__(hidden=[R, 1, H])` -> group maxima ``[R, V/32]`` float32: the head graph `run_graph`
@@ -37,12 +41,14 @@ def _cat_fp8(parts: Sequence[tuple[torch.Tensor, torch.Tensor]]):
 class Engine:
     """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
 
-    def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda"):
+    def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda",
+                 saved_states: bool = False):
         if not torch.cuda.is_available():
             raise RuntimeError("the verify path runs on the GPU only")
         self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
+        self.saved_states = saved_states
         self.device = torch.device(device)
-        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp)
+        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states)
         self.buffers: dict[tuple[str, int], torch.Tensor] = {}
         self.mtp_layer = cfg.num_hidden_layers
         self._bind_zeros("workspace", -1, torch.uint8)
@@ -54,6 +60,9 @@ class Engine:
                 self._bind_zeros("linear_attn.pending_delta", i, torch.float32)
                 self._bind_zeros("linear_attn.pending_decay", i, torch.float32)
                 self._bind_zeros("linear_attn.pending_input", i, DTYPE)
+                if saved_states:
+                    self._bind_zeros("linear_attn.saved_state", i, DTYPE)
+                    self._bind_zeros("linear_attn.saved_conv", i, DTYPE)
             else:
                 self._bind_zeros("self_attn.k_cache", i, DTYPE)
                 self._bind_zeros("self_attn.v_cache", i, DTYPE)
@@ -224,6 +233,39 @@ class VerifyStep:
             _dev(inputs_embeds, DTYPE, dev), _dev(inputs["cos"], DTYPE, dev), _dev(inputs["sin"], DTYPE, dev),
             _dev(inputs["position"], torch.int32, dev), _dev(inputs["active"], torch.float32, dev),
             _dev(inputs["accepted"], torch.int32, dev), out,
+        )
+        return out
+
+
+class StepGraph:
+    """The step graph's other calls over the engine's B rows (the reference's `Qwen38Step.forward`, model.py:983-995):
+    one-token decode, saving or restoring one row's gated-delta states, and (with ``accepted``) verify."""
+
+    def __init__(self, engine: Engine):
+        self.engine = engine
+        self.verify = VerifyStep(engine)
+
+    def __call__(self, inputs_embeds: torch.Tensor, cos=None, sin=None, position=None, active=None, slot=None, start=None,
+                 n_valid=None, save_slot=None, restore_slot=None, accepted=None) -> torch.Tensor:
+        e = self.engine
+        if save_slot is not None or restore_slot is not None:
+            if not e.saved_states:
+                raise ValueError("this layer keeps no saved states")
+            which = save_slot if save_slot is not None else restore_slot
+            e.handle.copy_states(_dev(torch.as_tensor(which).reshape(1), torch.int32, e.device), save_slot is not None)
+            return inputs_embeds
+        if slot is not None:
+            raise NotImplementedError("the prefill form is not part of this build")
+        if accepted is not None:
+            return self.verify(inputs_embeds, cos=cos, sin=sin, position=position, active=active, accepted=accepted)
+        b, h = e.batch_size, e.cfg.hidden_size
+        if tuple(inputs_embeds.shape) != (b, 1, h):
+            raise ValueError(f"inputs_embeds must be [{b}, 1, {h}], got {list(inputs_embeds.shape)}")
+        dev = e.device
+        out = torch.empty(b, 1, h, dtype=DTYPE, device=dev)
+        e.handle.decode(
+            _dev(inputs_embeds, DTYPE, dev), _dev(cos, DTYPE, dev), _dev(sin, DTYPE, dev), _dev(position, torch.int32, dev),
+            _dev(active, torch.float32, dev), out,
         )
         return out
 

@@ -23,3 +23,12 @@ def gpu():
     from qwen38_amd import ext
 
     return ext.library()
+
+
+@pytest.fixture(scope="session")
+def references():
+    """The oracle on the golden scenario here (AVX512 kernels where the host has them) and the scalar build of it
+    (tests/floor.py), computed once per session."""
+    import floor
+
+    return floor.run_scenario(), floor.scalar_build()

@@ -8,8 +8,8 @@ further from the AVX512 oracle than the scalar build of the same oracle is.
 
     python tests/floor.py OUT.pt      (run with the environment that selects the CPU kernels)
 
-writes the scenario's outputs (both verify steps' hidden states, the state after step 2, head maxima and the MTP
-output) computed by the oracle in this process.
+writes the scenario's outputs (both verify steps' hidden states, the state after step 2, head maxima, the MTP output,
+and the decode scenario's hidden states and states) computed by the oracle in this process.
 """
 
 from __future__ import annotations
@@ -31,8 +31,10 @@ import torch  # noqa: E402
 from oracle import model as om  # noqa: E402
 from qwen38_amd import synth  # noqa: E402
 from qwen38_amd.config import tiny_config  # noqa: E402
-from qwen38_amd.generate import mtp_step_inputs, verify_inputs  # noqa: E402
-from scenario import golden_meta, golden_tensors, oracle_weights, tiny_states  # noqa: E402
+from qwen38_amd.generate import batch_step_inputs, mtp_step_inputs, verify_inputs  # noqa: E402
+from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states  # noqa: E402
+
+DECODE_STEPS = 3
 
 
 def run_scenario() -> dict:
@@ -60,6 +62,24 @@ def run_scenario() -> dict:
     mi = mtp_step_inputs(cfg, meta["positions_2"], k, s, torch.bfloat16, meta["active"])
     picks = gold["picks4"].long().reshape(b, k)
     out["mtp_out"] = om.mtp_forward(cfg, mtp_w, mst, gold["hidden2"], embed[picks], mi["cos"], mi["sin"], mi["position"], mi["active"])
+
+    # Decode: DECODE_STEPS one-token steps from the scenario's starting states at positions_1 (row 2 starts a
+    # sequence at position 0, row 3 is inactive), token t of each row's first verify tokens; then a verify step with
+    # accepted = 0 over the second verify tokens.
+    dst = tiny_states(cfg, meta, meta["seed"])
+    pos = list(meta["positions_1"])
+    for t in range(DECODE_STEPS):
+        di = batch_step_inputs(cfg, pos, s, torch.bfloat16, meta["active"])
+        out[f"decode.hidden{t}"] = om.step_decode(cfg, layers, dst, embed[ids[0][:, t]].unsqueeze(1), di["cos"], di["sin"],
+                                                  di["position"], di["active"])
+        pos = [p + 1 if a else p for p, a in zip(pos, meta["active"])]
+    for i, st in enumerate(clone_states(dst)):
+        for key in ("recurrent_state", "conv_state", "k_cache", "v_cache"):
+            if key in st:
+                out[f"decode.state.{i}.{key}"] = st[key]
+    vi = verify_inputs(cfg, pos, k, s, torch.bfloat16, meta["active"], [0] * b)
+    out["decode.verify"] = om.step_verify(cfg, layers, dst, embed[ids[1]], vi["cos"], vi["sin"], vi["position"], vi["active"],
+                                          vi["accepted"])
     return out
 
 

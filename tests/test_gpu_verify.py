@@ -51,12 +51,6 @@ def scenario(gpu):
     return cfg, meta, values, engine
 
 
-@pytest.fixture(scope="module")
-def references():
-    """The oracle here (AVX512 kernels where the host has them) and the scalar build of it."""
-    return floor.run_scenario(), floor.scalar_build()
-
-
 @pytest.mark.gpu
 def test_head_picks_and_maxima_from_the_references_hidden_states(scenario):
     cfg, meta, values, engine = scenario
