@@ -8,7 +8,7 @@ the state advance. It runs as one library call, `q38_spec_step`, on torch's curr
 resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode]
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
@@ -18,6 +18,12 @@ launch from the committed counter summary in profiles/.
 `step_roofline` is the whole step's algorithmic HBM bytes over its time. `cpu_baseline` is the CPU oracle (this
 repository's restatement of the reference's CPU path) on a bounded sample: one 27B block (3 gated-delta + 1 attention
 layer) of the verify at the same B, K and context, scaled x16 to 64 layers, without the MTP and head passes.
+
+`--decode` measures the one-token decode graph instead (`q38_decode`: the reference's step graph in its decode form,
+model.py:983-995 with GatedDeltaNetStep.forward and FullAttentionStep.forward) over the same 64 rows from 512-token
+contexts, one token per row per step: `value` is tokens per second, `roofline` the step's algorithmic HBM bytes
+(weights, scales, gated-delta and conv state read + written, KV read over the context, inputs and outputs) over its
+time, and `cpu_baseline` the CPU oracle's decode of one block, x16.
 """
 
 from __future__ import annotations
@@ -70,6 +76,12 @@ def algorithmic_bytes(cfg, batch: int, tokens: int, context: int) -> dict:
     mtp = 3 * (mtp_w + kv_read + t * hkv * hd * 2 * 2 + 3 * t * h * 2)
     total = weights + state + kv + io + head + mtp
     return {"total": total, "weights": weights, "state": state, "kv": kv, "head": head, "mtp": mtp, "io": io}
+
+
+def decode_bytes(cfg, batch: int, context: int) -> int:
+    """Compulsory HBM bytes of one decode step (no head, no MTP): as `algorithmic_bytes` with one token per row."""
+    b = algorithmic_bytes(cfg, batch, 1, context)
+    return b["weights"] + b["state"] + b["kv"] + b["io"]
 
 
 def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int):
@@ -186,6 +198,97 @@ def cpu_baseline(cfg_block, batch: int, tokens: int, max_seq_len: int, context: 
     }
 
 
+def cpu_decode_baseline(cfg_block, batch: int, max_seq_len: int, context: int, seed: int, n_blocks: int) -> dict:
+    """The CPU oracle's decode step on one block (bf16, all host threads), timed once after one warm-up."""
+    import torch
+
+    from oracle import model as om
+    from qwen38_amd import synth
+    from qwen38_amd.generate import batch_step_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    layers = []
+    for i in range(cfg_block.num_hidden_layers):
+        prefix = f"layers.{i}."
+        w = {}
+        for spec in synth.layer_specs(cfg_block, i):
+            v = synth.make(spec, seed, "cuda")
+            w[spec.name[len(prefix):]] = om.FP8Weight(*(x.cpu() for x in v)) if isinstance(v, tuple) else v.cpu()
+        layers.append(w)
+    states = []
+    for i, kind in enumerate(cfg_block.layer_types):
+        if kind == "linear_attention":
+            states.append({k: v.cpu() for k, v in synth.gdn_states(cfg_block, batch, 1, seed, f"cpu.{i}", "cuda").items()})
+        else:
+            states.append({k: v.cpu() for k, v in synth.kv_states(cfg_block, batch, max_seq_len, [context] * batch, seed, f"cpu.{i}", "cuda").items()})
+    x = synth.hidden_states((batch, 1, cfg_block.hidden_size), seed, "cpu.decode.x")
+    inp = batch_step_inputs(cfg_block, [context] * batch, max_seq_len, torch.bfloat16)
+    times = []
+    for _ in range(2):
+        started = time.perf_counter()
+        om.step_decode(cfg_block, layers, states, x, inp["cos"], inp["sin"], inp["position"], inp["active"])
+        times.append(time.perf_counter() - started)
+        log(f"cpu decode block {times[-1]:.2f}s")
+    step = times[-1] * n_blocks
+    return {
+        "value": batch / step,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one block (3 gated-delta + 1 attention layer) of the B={batch} decode at context {context} on the CPU "
+        f"oracle in bf16 ({times[-1]:.2f} s after one warm-up), x{n_blocks} for 64 layers",
+    }
+
+
+def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -> dict:
+    """Decode steps of all rows, one token each, from `context` on; inputs prepared before the timed region."""
+    import torch
+
+    from qwen38_amd import synth
+    from qwen38_amd.generate import batch_step_inputs
+    from qwen38_amd.steps import StepGraph
+
+    step = StepGraph(engine)
+    n = args.warmup + args.steps
+    embeds = synth.hidden_states((batch, 1, cfg.hidden_size), args.seed, "bench.decode", "cuda")
+    inputs = []
+    for i in range(n):
+        raw = batch_step_inputs(cfg, [context + i] * batch, max_seq_len, torch.bfloat16)
+        inputs.append({k: v.cuda() for k, v in raw.items()})
+    for i in range(args.warmup):
+        step(inputs_embeds=embeds, **inputs[i])
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.warmup, n):
+        step(inputs_embeds=embeds, **inputs[i])
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    log(f"decode: {ms:.3f} ms/step")
+    alg = decode_bytes(cfg, batch, context + args.warmup + args.steps // 2)
+    gbs = alg / (ms / 1000.0) / 1e9
+    return {
+        "metric": "decode tokens/s/GPU, 64-layer one-token step, batch 64",
+        "value": round(batch / (ms / 1000.0), 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
+        "config": {"workload": "27b-64L-b64-decode-ctx512", "global_batch": batch, "tokens_per_row": 1, "context": context,
+                   "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": alg},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,6 +296,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode", action="store_true", help="time the one-token decode graph instead of the speculative step")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -217,6 +321,16 @@ def main() -> int:
         log(f"copy probe: {args.copy_probe} MiB read and written by one bitwise_not kernel")
         del src, dst
     engine, st = build(cfg, batch, tokens, max_seq_len, context, seed)
+    if args.decode:
+        result = decode_main(args, cfg, engine, batch, context, max_seq_len)
+        if not args.no_cpu_baseline:
+            from qwen38_amd.config import qwen38_27b_config as big
+
+            del engine
+            torch.cuda.empty_cache()
+            result["cpu_baseline"] = cpu_decode_baseline(big(1), batch, max_seq_len, context, seed, 16)
+        print(json.dumps(result), flush=True)
+        return 0
 
     def step():
         engine.handle.spec_step(st["position"], st["index"], st["match"], st["accepted"], st["active"], st["hidden"],
