@@ -1,4 +1,5 @@
-"""CPU restatement of the reference's verify-step semantics. TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""CPU restatement of the reference's verify, decode and prefill semantics. TEST INFRASTRUCTURE ONLY (see
+oracle/__init__.py).
 
 Every function follows the reference CPU path op for op, in torch CPU, at the same rounding points (dtype bf16 in
 production; float32 for the invariant tests, as the reference's own tests do). The one deliberate difference is the
@@ -9,7 +10,14 @@ Pinning of each function (what fixes it besides this text):
 * tests/golden/verify_tiny.safetensors, written by tests/golden/make_golden.py from the reference's own CPU path
   (imported in the build container): pins `gdn_verify`, `attention_verify`, `mlp`, `decoder_layer`, `step_verify`,
   `mtp_forward`, `head_group_maxima`, `chip_next_tokens`, `accept` bit for bit on config 0 shapes.
-* invariants in tests/test_oracle.py: verify with every token accepted equals sequential `gdn_decode`/`attention_decode`
+* tests/golden/prefill_tiny.safetensors, written by tests/golden/make_golden_prefill.py from the reference's CPU path:
+  pins `gdn_prefill`, `chunked_gated_delta`, `unit_lower_inverse`, `attention_prefill`, `blocked_attention`,
+  `_write_chunk`, `attention_cache_chunk`, `step_prefill` and `mtp_prefill` bit for bit (two chunks of one row, the
+  second padded, and the MTP layer's prefill form).
+* invariants in tests/test_oracle.py: prefill then decode equals decoding every token (float32, reference
+  tests/test_prefill.py:143-166); the chunked rule equals the recurrence in float64 with correlated keys and padding;
+  `unit_lower_inverse` equals a dense inverse; blocked attention equals one softmax;
+  verify with every token accepted equals sequential `gdn_decode`/`attention_decode`
   steps (reference tests/test_prefill.py:235-263); the textbook recurrence in float64; full-softmax attention by brute
   force; ChipHead equals HostHead (reference tests/test_model_parity.py:280-309); e4m3 dequantization against its bit
   fields; e5m2 rounding against an exhaustive bf16 table.
@@ -24,6 +32,10 @@ import torch.nn.functional as F
 
 # Added to the scores of unfilled cache slots (model.py:30-32).
 MASKED_SCORE = -1e4
+# Tokens per piece of the chunked gated delta rule (model.py:34) and cache positions per block of prefill attention
+# (model.py:36).
+DELTA_CHUNK = 128
+ATTENTION_BLOCK = 2048
 # The reference rounds every FP8 projection's input to e5m2 (model.py:85-87, 222-225). Tests that compare two float32
 # forms of the same computation switch it off, as reference tests/test_model_parity.py:255-260 does.
 ROUND_E5M2 = True
@@ -340,11 +352,18 @@ def attention_decode(cfg, w: dict, st: dict, x, cos, sin, position, active):
 # ----------------------------------------------------------------------------------------------- layers and step
 
 
-def decoder_layer(cfg, layer_type: str, w: dict, st: dict, x, cos, sin, position, active, accepted=None):
-    """`DecoderLayer.forward` (model.py:918-930): verify when ``accepted`` is given, else decode."""
+def decoder_layer(cfg, layer_type: str, w: dict, st: dict, x, cos, sin, position, active, accepted=None, slot=None,
+                  start=None, n_valid=None):
+    """`DecoderLayer.forward` (model.py:918-930): verify when ``accepted`` is given, prefill when ``slot`` is, else
+    decode."""
     eps = cfg.rms_norm_eps
     h = rms_norm(x, w["input_layernorm_weight"], eps)
-    if layer_type == "linear_attention":
+    if slot is not None and accepted is None:
+        if layer_type == "linear_attention":
+            mixer = gdn_prefill(cfg, w, st, h, slot, start, n_valid)
+        else:
+            mixer = attention_prefill(cfg, w, st, h, cos, sin, slot, start, n_valid)
+    elif layer_type == "linear_attention":
         if accepted is not None:
             mixer = gdn_verify(cfg, w, st, h, position, active, accepted)
         else:
@@ -363,6 +382,14 @@ def step_verify(cfg, layers: list, states: list, inputs_embeds, cos, sin, positi
     x = inputs_embeds
     for layer_type, w, st in zip(cfg.layer_types, layers, states):
         x = decoder_layer(cfg, layer_type, w, st, x, cos, sin, position, active, accepted)
+    return x
+
+
+def step_prefill(cfg, layers: list, states: list, inputs_embeds, cos, sin, slot, start, n_valid):
+    """`Qwen38Step.forward` prefill form (model.py:983-995): one chunk ``[1, L, H]`` of row ``slot`` from ``start``."""
+    x = inputs_embeds
+    for layer_type, w, st in zip(cfg.layer_types, layers, states):
+        x = decoder_layer(cfg, layer_type, w, st, x, cos, sin, None, None, slot=slot, start=start, n_valid=n_valid)
     return x
 
 
@@ -386,6 +413,169 @@ def mtp_forward(cfg, w: dict, st: dict, hidden, inputs_embeds, cos, sin, positio
     x = decoder_layer(cfg, "full_attention", layer_w, st, x, cos, sin, position, active, accepted=active)
     out = rms_norm(x, w["norm_weight"], eps)
     return (out.float() / (1.0 + w["final_norm_weight"].float())).to(x.dtype)
+
+
+def mtp_prefill(cfg, w: dict, st: dict, hidden, inputs_embeds, cos, sin, slot, start, n_valid):
+    """`MTPStep.forward` prefill form (model.py:843-855): only the layer's cache for the chunk is written
+    (`cache_chunk`); returns ``x[:, :1]`` as the reference does."""
+    eps = cfg.rms_norm_eps
+    embedded = rms_norm(inputs_embeds, w["embedding_norm_weight"], eps)
+    state = rms_norm(rms_norm(hidden, w["final_norm_weight"], eps), w["hidden_norm_weight"], eps)
+    x = linear_fp8(torch.cat((embedded, state), dim=-1), w["fc"])
+    layer_w = {name[len("layer.") :]: t for name, t in w.items() if name.startswith("layer.")}
+    attention_cache_chunk(cfg, layer_w, st, rms_norm(x, layer_w["input_layernorm_weight"], eps), cos, sin, slot, start)
+    return x[:, :1]
+
+
+# ----------------------------------------------------------------------------------------------- prefill
+
+
+def unit_lower_inverse(lower: torch.Tensor, base: int = 8) -> torch.Tensor:
+    """`unit_lower_inverse` (model.py:127-153): ``(I - lower)^-1`` for strictly lower triangular ``lower``
+    ``[..., n, n]``. Diagonal blocks of ``base`` as ``(I + L)(I + L^2)(I + L^4)`` (exact: ``L^base = 0`` there), then
+    neighbouring blocks merged, the merged inverse's lower block being ``B^-1 C A^-1`` for ``[[A, 0], [C, B]]``."""
+    n = lower.shape[-1]
+    block_of = torch.arange(n) // base
+    local = lower * (block_of.unsqueeze(-1) == block_of)
+    inverse = torch.eye(n, dtype=lower.dtype) + local
+    power = local
+    for _ in range(int(math.log2(base)) - 1):
+        power = power @ power
+        inverse = inverse + inverse @ power
+    size = base
+    while size < n:
+        merged = inverse.clone()
+        for first in range(0, n, 2 * size):
+            top, bottom = slice(first, first + size), slice(first + size, first + 2 * size)
+            merged[..., bottom, top] = inverse[..., bottom, bottom] @ lower[..., bottom, top] @ inverse[..., top, top]
+        inverse, size = merged, 2 * size
+    return inverse
+
+
+def chunked_gated_delta(query, key, value, log_decay, beta, state, chunk: int = DELTA_CHUNK):
+    """`chunked_gated_delta` (model.py:88-124): the gated delta rule over ``tokens`` in pieces of ``chunk``.
+    ``query``, ``key`` ``[heads, tokens, dk]`` (normed, query scaled), ``value`` ``[heads, tokens, dv]``,
+    ``log_decay``, ``beta`` ``[heads, tokens]``, ``state`` ``[heads, dk, dv]``, all float32. Within a piece the
+    cumulative log decay g, the decay matrix e^(g_i - g_j) (i >= j), the unit-lower solve of the in-piece coupling
+    and its products; across pieces the state recurrence. Returns (outputs ``[heads, tokens, dv]``, final state)."""
+    heads, tokens, dk = key.shape
+    pieces = tokens // chunk
+    q = query.reshape(heads, pieces, chunk, dk)
+    k = key.reshape(heads, pieces, chunk, dk)
+    v = value.reshape(heads, pieces, chunk, -1)
+    g = log_decay.reshape(heads, pieces, chunk).cumsum(-1)
+    b = beta.reshape(heads, pieces, chunk, 1)
+    i = torch.arange(chunk)
+    causal = (i.unsqueeze(-1) >= i.unsqueeze(0)).float()
+    below = (i.unsqueeze(-1) > i.unsqueeze(0)).float()
+    decay = ((g.unsqueeze(-1) - g.unsqueeze(-2)) * causal).exp() * causal
+    k_beta = k * b
+    inverse = unit_lower_inverse(-(k_beta @ k.transpose(-1, -2)) * decay * below)
+    new_values = inverse @ (v * b)
+    cumulative_keys = inverse @ (k_beta * g.exp().unsqueeze(-1))
+    outputs = []
+    for p in range(pieces):
+        attn = (q[:, p] @ k[:, p].transpose(-1, -2)) * decay[:, p]
+        v_new = new_values[:, p] - cumulative_keys[:, p] @ state
+        outputs.append((q[:, p] * g[:, p].exp().unsqueeze(-1)) @ state + attn @ v_new)
+        last = g[:, p, -1]
+        carried = (k[:, p] * (last.unsqueeze(-1) - g[:, p]).exp().unsqueeze(-1)).transpose(-1, -2) @ v_new
+        state = state * last.exp().reshape(heads, 1, 1) + carried
+    return torch.cat(outputs, dim=1), state
+
+
+def gdn_prefill(cfg, w: dict, st: dict, x, slot, start, n_valid):
+    """`GatedDeltaNetStep.prefill` CPU branch (model.py:476-521): a chunk ``x`` ``[1, L, H]`` of row ``slot`` from
+    ``start`` (0 restarts the row's states), tokens from ``n_valid`` on padding. Conv taps are bf16 products summed by
+    bf16 additions; the chunked rule runs in float32 from the row's state; the new conv state is the last three real
+    inputs. ``st`` entries of row ``slot`` are replaced."""
+    dtype = x.dtype
+    tokens = x.shape[1]
+    kernel = cfg.linear_conv_kernel_dim
+    slot, keep = slot.long(), (start > 0).to(dtype)
+    valid = (torch.arange(tokens) < n_valid).float()
+    qkv = linear_fp8(x, w["linear_attn.in_proj_qkv"])[0]
+    history = st["conv_state"].index_select(0, slot)[0] * keep
+    window = torch.cat((history.transpose(0, 1), qkv))
+    carried = window.index_select(0, n_valid.long() + torch.arange(kernel - 1)).transpose(0, 1)
+    st["conv_state"] = st["conv_state"].index_copy(0, slot, carried.unsqueeze(0))
+    z = linear_fp8(x, w["linear_attn.in_proj_z"])[0]
+    beta, log_decay = _gdn_gates(w, x[0])
+    beta, log_decay = beta * valid.unsqueeze(-1), log_decay * valid.unsqueeze(-1)
+    state = st["recurrent_state"].index_select(0, slot)[0].float() * keep.float()
+    taps = window.transpose(0, 1)
+    conv_weight = w["linear_attn.conv_weight"]
+    conv = sum(taps[:, j : j + tokens] * conv_weight[:, j : j + 1] for j in range(kernel))
+    query, key, value = _gdn_split(cfg, silu(conv).transpose(0, 1))
+    out, state = chunked_gated_delta(
+        query.transpose(0, 1), key.transpose(0, 1), value.transpose(0, 1), log_decay.transpose(0, 1), beta.transpose(0, 1),
+        state, min(DELTA_CHUNK, tokens),
+    )
+    st["recurrent_state"] = st["recurrent_state"].index_copy(0, slot, state.unsqueeze(0).to(st["recurrent_state"].dtype))
+    z = z.reshape(tokens, cfg.linear_num_value_heads, -1)
+    return _gdn_finish(cfg, w, out.transpose(0, 1).to(dtype), z, dtype).reshape(1, tokens, -1)
+
+
+def blocked_attention(query, keys, values, visible, block: int):
+    """`blocked_attention` (model.py:170-191): softmax attention over positions in blocks of ``block`` with a running
+    maximum and sum. ``query`` ``[kv_heads, queries, head]`` (scaled), ``keys``/``values`` ``[kv_heads, positions,
+    head]``, ``visible`` bool ``[queries, positions]``. Scores are a bf16 matmul; each block's unnormalised weights
+    go to bf16 for their matmul with the values, whose bf16 result is added in float32."""
+    best = torch.full((*query.shape[:2], 1), 2 * MASKED_SCORE)
+    total = torch.zeros(*query.shape[:2], 1)
+    out = torch.zeros(*query.shape[:2], values.shape[-1])
+    for first in range(0, keys.shape[1], block):
+        scores = (query @ keys[:, first : first + block].transpose(-1, -2)).float()
+        scores = scores + torch.where(visible[:, first : first + block], 0.0, MASKED_SCORE)
+        new_best = torch.maximum(best, scores.amax(dim=-1, keepdim=True))
+        weights = (scores - new_best).exp()
+        rescale = (best - new_best).exp()
+        total = total * rescale + weights.sum(dim=-1, keepdim=True)
+        out = out * rescale + (weights.to(values.dtype) @ values[:, first : first + block]).float()
+        best = new_best
+    return out / total
+
+
+def _write_chunk(st: dict, key, value, slot, start):
+    """`FullAttentionStep._write_chunk` (model.py:791-799) for a bf16 cache: row ``slot`` at ``start`` onward, every
+    other row at the cache's last ``L`` positions (junk, never read before overwritten)."""
+    rows, max_seq_len = st["k_cache"].shape[0], st["k_cache"].shape[2]
+    tokens = key.shape[2]
+    positions = start.long() + torch.arange(tokens)
+    junk = max_seq_len - tokens + torch.arange(tokens)
+    others = torch.arange(rows) != slot.long()
+    where = torch.where(others.unsqueeze(-1), junk.unsqueeze(0), positions.unsqueeze(0))
+    _write_both(st, key.expand(rows, -1, -1, -1), value.expand(rows, -1, -1, -1), where)
+
+
+def attention_prefill(cfg, w: dict, st: dict, x, cos, sin, slot, start, n_valid):
+    """`FullAttentionStep.prefill` CPU branch with a bf16 cache (model.py:704-783): the chunk's queries against row
+    ``slot``'s cached positions before ``start`` and the chunk's own tokens causally, by `blocked_attention`; then the
+    chunk's keys and values written (`_write_chunk`)."""
+    head = cfg.head_dim
+    tokens = x.shape[1]
+    max_seq_len = st["k_cache"].shape[2]
+    query, key, value, gate = _attention_project(cfg, w, x, cos, sin)
+    groups = cfg.num_key_value_groups
+    grouped = (query[0] * head**-0.5).reshape(cfg.num_key_value_heads, groups * tokens, head)
+    cache_keys = st["k_cache"].index_select(0, slot.long())[0]
+    cache_values = st["v_cache"].index_select(0, slot.long())[0]
+    index = torch.arange(groups * tokens) % tokens
+    visible = torch.cat(
+        ((torch.arange(max_seq_len) < start).expand(groups * tokens, -1), torch.arange(tokens).unsqueeze(0) <= index.unsqueeze(-1)),
+        dim=-1,
+    )
+    out = blocked_attention(grouped, torch.cat((cache_keys, key[0]), dim=1), torch.cat((cache_values, value[0]), dim=1), visible,
+                            ATTENTION_BLOCK)
+    out = out.to(x.dtype).reshape(cfg.num_attention_heads, tokens, head).transpose(0, 1).reshape(1, tokens, -1)
+    _write_chunk(st, key, value, slot, start)
+    return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
+
+
+def attention_cache_chunk(cfg, w: dict, st: dict, x, cos, sin, slot, start):
+    """`FullAttentionStep.cache_chunk` (model.py:784-790): only the chunk's keys and values, written as prefill does."""
+    _, key, value, _ = _attention_project(cfg, w, x, cos, sin)
+    _write_chunk(st, key, value, slot, start)
 
 
 # ----------------------------------------------------------------------------------------------- head and acceptance

@@ -1,7 +1,7 @@
 """Host side of the verify path, mirroring the reference's generate.py: RoPE tables, the verify/MTP input dicts,
 embedding gathers and the head that turns hidden states into token ids.
 
-The input builders keep the reference's names, arguments, dtypes and errors exactly (generate.py:25-107), so a
+The input builders keep the reference's names, arguments, dtypes and errors exactly (generate.py:25-116), so a
 caller written for the reference builds the same dicts. `ChipHead` keeps its signature (generate.py:162-208); its
 `run_graph` is this package's `steps.HeadGraph`, so the group max *and* the exact top-group recheck run on the GPU and
 only token ids come back to the host.
@@ -79,6 +79,38 @@ def mtp_step_inputs(
     cos, sin = rotary(cfg, at, dtype)
     inputs["cos"], inputs["sin"] = cos.reshape(len(indices), tokens, -1), sin.reshape(len(indices), tokens, -1)
     return inputs
+
+
+def prefill_inputs(cfg: TextConfig, slot: int, start: int, n_valid: int, chunk: int, dtype: torch.dtype) -> dict[str, torch.Tensor]:
+    """Prefill inputs for `n_valid` tokens of one row from position `start`, padded to a full chunk (reference
+    generate.py:58-69)."""
+    if start < 0 or not 0 < n_valid <= chunk:
+        raise ValueError(f"a chunk must start at a position and hold 1 to {chunk} tokens")
+    cos, sin = rotary(cfg, start + torch.arange(chunk), dtype)
+    return {
+        "cos": cos.unsqueeze(0),
+        "sin": sin.unsqueeze(0),
+        "slot": torch.tensor([slot], dtype=torch.int32),
+        "start": torch.tensor([start], dtype=torch.int32),
+        "n_valid": torch.tensor([n_valid], dtype=torch.int32),
+    }
+
+
+def mtp_prefill_inputs(cfg: TextConfig, slot: int, start: int, n_valid: int, chunk: int, dtype: torch.dtype) -> dict[str, torch.Tensor]:
+    """Inputs for an MTP prefill chunk of one row from MTP index `start`, at positions one on (reference
+    generate.py:102-107)."""
+    inputs = prefill_inputs(cfg, slot, start, n_valid, chunk, dtype)
+    cos, sin = rotary(cfg, start + 1 + torch.arange(chunk), dtype)
+    inputs["cos"], inputs["sin"] = cos.unsqueeze(0), sin.unsqueeze(0)
+    return inputs
+
+
+def state_copy_inputs(cfg: TextConfig, slot: int, save: bool, dtype: torch.dtype) -> dict[str, torch.Tensor]:
+    """Inputs that save one row's recurrent states, or restore them (reference generate.py:110-116)."""
+    return {
+        "inputs_embeds": torch.zeros(1, 1, cfg.hidden_size, dtype=dtype),
+        ("save_slot" if save else "restore_slot"): torch.tensor([slot], dtype=torch.int32),
+    }
 
 
 class BlockChain:

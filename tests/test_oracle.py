@@ -4,17 +4,20 @@ forms that a plausible mistake (a dropped term, a wrong index or sign, a transpo
 from __future__ import annotations
 
 import hashlib
+import json
 import math
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import model as om
 from qwen38_amd import synth
 from qwen38_amd.config import tiny_config, with_layers
-from qwen38_amd.generate import mtp_step_inputs, verify_inputs, batch_step_inputs
+from qwen38_amd.generate import batch_step_inputs, mtp_prefill_inputs, mtp_step_inputs, prefill_inputs, verify_inputs
 from qwen38_amd.quant import dequantize_e4m3, quantize_e4m3
-from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states
+from safetensors.torch import load_file
+from scenario import GOLDEN, clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states
 
 
 def _digest(t):
@@ -290,3 +293,139 @@ def test_e5m2_rounding_of_every_bf16_value_is_round_to_nearest_even():
     want = torch.where(want.abs() > 57344, torch.sign(x) * math.inf, want)
     sel = finite & (mag < 2.0**17)
     assert torch.equal(got[sel].double(), want[sel])
+
+
+def test_oracle_prefill_matches_the_reference_bit_for_bit(tiny):
+    """tests/golden/prefill_tiny.*: two prefill chunks of row 1 (a full one from position 0, then 40 real tokens of
+    the next from position 64) and the MTP layer's prefill form, from the reference's own CPU path."""
+    cfg, meta, values = tiny
+    gold = load_file(GOLDEN / "prefill_tiny.safetensors")
+    pmeta = json.loads((GOLDEN / "prefill_tiny.json").read_text())
+    layers, mtp_w, _ = oracle_weights(values, cfg)
+    states = tiny_states(cfg, meta, meta["seed"])
+    s, chunk, slot = pmeta["max_seq_len"], pmeta["chunk"], pmeta["slot"]
+    embed = values["embed_tokens"]
+    ids = gold["ids"].long()
+    for n, (start, n_valid) in enumerate(pmeta["chunks"]):
+        chunk_ids = ids[start : start + chunk].clone()
+        chunk_ids[n_valid:] = 0
+        pi = prefill_inputs(cfg, slot, start, n_valid, chunk, torch.bfloat16)
+        h = om.step_prefill(cfg, layers, states, embed[chunk_ids].reshape(1, chunk, -1), pi["cos"], pi["sin"], pi["slot"],
+                            pi["start"], pi["n_valid"])
+        assert torch.equal(h, gold[f"hidden_p{n + 1}"]), n
+    for i, (kind, st) in enumerate(zip(cfg.layer_types, states)):
+        owner = "linear_attn" if kind == "linear_attention" else "self_attn"
+        for key in ("recurrent_state", "conv_state", "k_cache", "v_cache"):
+            if key in st:
+                assert _digest(st[key]) == pmeta["state_sha256"][f"layers.{i}.{owner}.{key}"], (i, key)
+
+    mst = synth.kv_states(cfg, meta["batch"], s, meta["context"], meta["seed"], "mtp")
+    mi = mtp_prefill_inputs(cfg, slot, 0, chunk, chunk, torch.bfloat16)
+    x = om.mtp_prefill(cfg, mtp_w, mst, gold["hidden_p1"], embed[ids[1 : chunk + 1]].reshape(1, chunk, -1), mi["cos"], mi["sin"],
+                       mi["slot"], mi["start"], mi["n_valid"])
+    assert torch.equal(x, gold["mtp_x"])
+    for key, value in mst.items():
+        assert _digest(value) == pmeta["mtp_state_sha256"][f"layer.self_attn.{key}"], key
+
+
+def test_unit_lower_inverse_is_the_inverse_and_the_chunked_rule_is_the_recurrence():
+    """`unit_lower_inverse` against a dense inverse; `chunked_gated_delta` against the rule one token at a time in
+    float64, with pieces of 64 and 128, strongly correlated keys, and padding tokens (no decay, no write) that leave
+    the state alone (reference tests/test_prefill.py:18-71)."""
+    g = torch.Generator().manual_seed(0)
+    lower = torch.tril(torch.randn(3, 128, 128, generator=g, dtype=torch.float64) * 0.2, -1)
+    dense = torch.linalg.inv(torch.eye(128, dtype=torch.float64) - lower)
+    assert (om.unit_lower_inverse(lower) - dense).abs().max() < 1e-10
+
+    def recurrent(query, key, value, log_decay, beta, state):
+        outs = []
+        for t in range(key.shape[1]):
+            state = state * log_decay[:, t].exp().reshape(-1, 1, 1)
+            delta = (value[:, t] - (state * key[:, t].unsqueeze(-1)).sum(-2)) * beta[:, t].unsqueeze(-1)
+            state = state + key[:, t].unsqueeze(-1) * delta.unsqueeze(-2)
+            outs.append((state * query[:, t].unsqueeze(-1)).sum(-2))
+        return torch.stack(outs, dim=1), state
+
+    heads, tokens, dim = 2, 256, 64
+    shared = torch.randn(heads, 1, dim, generator=g)
+    for mix in (1.0, 0.01):  # independent keys, then keys within 1% of a shared direction
+        key = F.normalize((1 - mix) * shared + mix * torch.randn(heads, tokens, dim, generator=g), dim=-1)
+        query = F.normalize(torch.randn(heads, tokens, dim, generator=g), dim=-1) / dim**0.5
+        value = torch.randn(heads, tokens, dim, generator=g)
+        log_decay, beta = -torch.rand(heads, tokens, generator=g) * 0.3, torch.rand(heads, tokens, generator=g)
+        state = torch.randn(heads, dim, dim, generator=g) * 0.1
+        want_out, want_state = recurrent(*(t.double() for t in (query, key, value, log_decay, beta, state)))
+        for chunk in (64, 128):
+            out, got_state = om.chunked_gated_delta(query, key, value, log_decay, beta, state, chunk)
+            assert (out - want_out).abs().max() < 1e-4, (mix, chunk)
+            assert (got_state - want_state).abs().max() < 1e-4, (mix, chunk)
+        real = 200
+        log_decay[:, real:], beta[:, real:] = 0, 0
+        _, want_state = recurrent(*(t[:, :real].double() for t in (query, key, value, log_decay, beta)), state.double())
+        _, got_state = om.chunked_gated_delta(query, key, value, log_decay, beta, state, 128)
+        assert (got_state - want_state).abs().max() < 1e-4, mix
+
+
+def test_blocked_attention_equals_full_softmax():
+    """`blocked_attention` with blocks smaller than the positions against one softmax over every visible position."""
+    g = torch.Generator().manual_seed(1)
+    q = (torch.randn(2, 24, 32, generator=g) / 32**0.5).to(torch.bfloat16)
+    k = torch.randn(2, 100, 32, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 100, 32, generator=g).to(torch.bfloat16)
+    visible = torch.rand(24, 100, generator=g) < 0.6
+    visible[:, 0] = True
+    scores = (q.float() @ k.float().transpose(-1, -2)).masked_fill(~visible, float("-inf"))
+    want = torch.softmax(scores, dim=-1) @ v.float()
+    got = om.blocked_attention(q, k, v, visible, 32)
+    assert (got - want).abs().max() < 3e-2 * want.abs().max()
+
+
+def test_prefill_then_decode_equals_decoding_every_token(monkeypatch):
+    """A row prefilled in two chunks (the second part padding) and then decoded gives, in float32 without the e5m2
+    rounding, what feeding every token through decode gives: outputs at every real position and the final states
+    (reference tests/test_prefill.py:143-166)."""
+    monkeypatch.setattr(om, "ROUND_E5M2", False)
+    cfg, layers = _float32_tiny(("linear_attention", "full_attention"))
+    batch, s, chunk, slot = 2, 64, 16, 1
+    g = torch.Generator().manual_seed(9)
+    tokens = torch.randn(24, cfg.hidden_size, generator=g)
+
+    def fresh():
+        out = []
+        for i, kind in enumerate(cfg.layer_types):
+            if kind == "linear_attention":
+                st = synth.gdn_states(cfg, batch, 1, 7, f"x{i}")
+                out.append({"recurrent_state": st["recurrent_state"].float(), "conv_state": st["conv_state"].float()})
+            else:
+                st = synth.kv_states(cfg, batch, s, [0, 0], 7, f"x{i}")
+                out.append({key: v.float() for key, v in st.items()})
+        return out
+
+    plain = fresh()
+    want = []
+    for t in range(24):
+        inputs = batch_step_inputs(cfg, [0, t], s, torch.float32, [False, True])
+        x = torch.stack([torch.zeros(cfg.hidden_size), tokens[t]]).reshape(2, 1, -1)
+        want.append(om.step_decode(cfg, layers, plain, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"])[1, 0])
+
+    pre = fresh()
+    got = []
+    for start, n_valid in ((0, 16), (16, 4)):
+        x = torch.zeros(1, chunk, cfg.hidden_size)
+        x[0, :n_valid] = tokens[start : start + n_valid]
+        pi = prefill_inputs(cfg, slot, start, n_valid, chunk, torch.float32)
+        h = om.step_prefill(cfg, layers, pre, x, pi["cos"], pi["sin"], pi["slot"], pi["start"], pi["n_valid"])
+        got += list(h[0, :n_valid])
+    for t in range(20, 24):
+        inputs = batch_step_inputs(cfg, [0, t], s, torch.float32, [False, True])
+        x = torch.stack([torch.zeros(cfg.hidden_size), tokens[t]]).reshape(2, 1, -1)
+        got.append(om.step_decode(cfg, layers, pre, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"])[1, 0])
+    for t in range(24):
+        assert torch.allclose(got[t], want[t], atol=2e-4, rtol=2e-4), (t, (got[t] - want[t]).abs().max())
+    for i, kind in enumerate(cfg.layer_types):
+        keys = ("recurrent_state", "conv_state") if kind == "linear_attention" else ("k_cache", "v_cache")
+        for key in keys:
+            a, b = pre[i][key][slot], plain[i][key][slot]
+            if key.endswith("cache"):
+                a, b = a[:, :24], b[:, :24]
+            assert torch.allclose(a, b, atol=2e-4, rtol=2e-4), (i, key)
