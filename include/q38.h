@@ -6,6 +6,11 @@
  *                       (reference qwen38_inf2/model.py:933-995; call site scheduler.py:288; inputs generate.py:72-87)
  *   q38_decode       <- `step(**batch_step_inputs(...))`, the one-token graph: Qwen38Step.forward's decode form
  *                       (model.py:983-995; call sites generate.py:251,258,290; inputs generate.py:34-60)
+ *   q38_prefill      <- `prefill(**prefill_inputs(...))`, the step graph's prefill form (model.py:983-995 with
+ *                       GatedDeltaNetStep.prefill model.py:476-521 and FullAttentionStep.prefill model.py:704-783;
+ *                       call site scheduler.py:125; inputs generate.py:58-69)
+ *   q38_mtp_prefill  <- `mtp(hidden=..., inputs_embeds=..., **mtp_prefill_inputs(...))`, MTPStep.forward's prefill form
+ *                       (model.py:843-855; call site scheduler.py:157; inputs generate.py:102-107)
  *   q38_copy_states  <- the same graph with save_slot / restore_slot (model.py:988-992, GatedDeltaNetStep.copy_states
  *                       model.py:456-464; call sites scheduler.py:119,133; inputs generate.py:110-116)
  *   q38_mtp_step     <- `mtp(hidden=..., inputs_embeds=..., **mtp_step_inputs(...))`, MTPStep.forward
@@ -51,6 +56,7 @@ typedef struct q38_config {
     float rms_norm_eps;
     int batch_size, verify_tokens, max_seq_len, mtp;
     int saved_states; /* a saved recurrent and conv state per row, for q38_copy_states (reference saved_states) */
+    int prefill_chunk; /* most tokens of one q38_prefill call (a multiple of 32; 0: no prefill workspace) */
 } q38_config;
 
 const char* q38_last_error(void);
@@ -130,6 +136,21 @@ int q38_verify(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const
  * accepted = 0, as in the reference. */
 int q38_decode(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* position,
                const float* active, uint16_t* out_hidden, void* stream);
+
+/* One prefill chunk of one row: embeds bf16 [tokens][H]; cos, sin bf16 [tokens][rotary_dim] for positions start ..;
+ * slot, start, n_valid int32 [1] on the device (start 0 restarts the row's gated-delta states; tokens from n_valid on
+ * are padding, which leaves the states alone). tokens is a multiple of 32 up to the config's prefill_chunk, and
+ * start + tokens <= max_seq_len. Writes the last layer's hidden states bf16 [tokens][H] and updates row slot's
+ * gated-delta states (the current half) and its KV caches at start .. start + tokens - 1 in place; the other rows are
+ * untouched (the reference also writes junk at their cache's last positions, which nothing reads). */
+int q38_prefill(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* slot,
+                const int32_t* start, const int32_t* n_valid, int tokens, uint16_t* out_hidden, void* stream);
+
+/* The MTP layer's prefill form: hidden, embeds bf16 [tokens][H]; cos, sin for positions start + 1 ..; slot, start int32
+ * [1] on the device. Writes only the MTP layer's KV cache for row slot at start .. start + tokens - 1, and, when out_x
+ * is not null, the fc output's first row bf16 [H] (the reference returns x[:, :1]). */
+int q38_mtp_prefill(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin,
+                    const int32_t* slot, const int32_t* start, int tokens, uint16_t* out_x, void* stream);
 
 /* Save (to_saved != 0) or restore one row's gated-delta recurrent and conv states in every gated-delta layer; slot is
  * int32 [1] on the device (a slot outside [0, B) copies nothing). Needs saved_states in the config and the saved

@@ -8,6 +8,7 @@
 //   MLP:          gate/up GEMM with SwiGLU epilogue -> down GEMM (split-K) -> residual + next layer's input norm
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -91,6 +92,9 @@ struct q38_handle {
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
         off_scores, off_astats, off_aown, off_akv, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos,
         off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
+    // prefill scratch (with a prefill chunk in the config)
+    size_t off_pqn = 0, off_pkn = 0, off_pv = 0, off_po = 0, off_pbeta = 0, off_pg = 0, off_pqs = 0;
+    size_t part_floats;  // capacity of the split-K partial buffer
     int gate_groups;  // K ranges of the gated-delta gate projections
     int attn_nchunks;  // chunks of ATTN_CHUNK cached positions over S
     // Kernel timer (q38_kernel_timer): event pairs around the gate/up GEMM launches while on.
@@ -186,7 +190,10 @@ int gemm(q38_handle* h, const uint8_t* tiles, const uint8_t* scales, const uint8
     a.n0 = n0;
     a.out1 = out1;
     a.ld1 = ld1;
-    if (epi == EPI_PARTIAL) a.part = (float*)h->ws(h->off_part);
+    if (epi == EPI_PARTIAL) {
+        a.part = (float*)h->ws(h->off_part);
+        a.splits_max = (int)std::max<size_t>(1, h->part_floats / ((size_t)h->Tpad * N));
+    }
     gemm_scratch(a, h->ws(h->off_gemm), h->cus);
     int splits = 1;
     HIP_TRY(q38_gemm(a, epi, &splits, stream));
@@ -223,15 +230,18 @@ struct StepIO {
     const float* active;
     const int32_t* accepted;
     bool decode = false;  // one token per row, the gated-delta layers' recurrent form
+    const int32_t* slot = nullptr;  // prefill: one chunk of row *slot from position *start, *n_valid real tokens
+    const int32_t* start = nullptr;
+    const int32_t* n_valid = nullptr;
 };
 
 // Tokens per row of the call in progress: the verify width by default, 1 for a decode step (restored on exit).
 struct TokensScope {
     q38_handle* h;
     int K, T, Tpad;
-    TokensScope(q38_handle* h_, int k) : h(h_), K(h_->K), T(h_->T), Tpad(h_->Tpad) {
+    TokensScope(q38_handle* h_, int k, int t = 0) : h(h_), K(h_->K), T(h_->T), Tpad(h_->Tpad) {
         h->K = k;
-        h->T = h->B * k;
+        h->T = t ? t : h->B * k;
         h->Tpad = pad_tokens(h->T);
     }
     ~TokensScope() {
@@ -271,8 +281,9 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         if (!ok) return 1;
         const size_t BKC = (size_t)h->B * h->K * h->C;
         uint16_t* z = (uint16_t*)h->ws(h->off_z);
-        // A verify step's qkv output is also its pending input snapshot; a decode step's goes to scratch.
-        uint16_t* qkv_out = io.decode ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
+        // A verify step's qkv output is also its pending input snapshot; a decode step's or a prefill chunk's goes to
+        // scratch.
+        uint16_t* qkv_out = io.decode || io.slot ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
         if (gemm(h, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
             return 1;
         GatesArgs ga{};
@@ -285,6 +296,39 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         ga.groups = h->gate_groups;
         ga.part = (float*)h->ws(h->off_gates);
         HIP_TRY(q38_gdn_gates(ga, stream));
+        if (io.slot) {
+            PrefillGdnArgs p{};
+            p.L = h->T;
+            p.rows = h->B;
+            p.Hk = h->Hk;
+            p.Hv = h->Hv;
+            p.C = h->C;
+            p.slot = io.slot;
+            p.start = io.start;
+            p.n_valid = io.n_valid;
+            p.qkv = qkv_out;
+            p.z = z;
+            p.gate_part = ga.part;
+            p.gate_groups = ga.groups;
+            p.a_log = alog;
+            p.dt_bias = dtb;
+            p.conv_w = convw;
+            p.norm_w = normw;
+            p.state = state;
+            p.conv = conv + (size_t)rd * h->B * h->C * 3;  // the current half, in place
+            p.qn = (float*)h->ws(h->off_pqn);
+            p.kn = (float*)h->ws(h->off_pkn);
+            p.v = (float*)h->ws(h->off_pv);
+            p.beta = (float*)h->ws(h->off_pbeta);
+            p.g = (float*)h->ws(h->off_pg);
+            p.o = (float*)h->ws(h->off_po);
+            p.act = act_mid;
+            p.eps = h->cfg.rms_norm_eps;
+            HIP_TRY(q38_gdn_prefill(p, stream));
+            kmid = h->Hv * h->dk;
+            goto out_proj;
+        }
+        {
         GdnArgs g{};
         g.B = h->B;
         g.K = h->K;
@@ -318,6 +362,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         g.eps = h->cfg.rms_norm_eps;
         HIP_TRY(io.decode ? q38_gdn_decode(g, stream) : q38_gdn_verify(g, stream));
         kmid = h->Hv * h->dk;
+        }
     } else {
         auto qkv_t = get<uint8_t>(h, "self_attn.qkv.tiles", li, &ok);
         auto qkv_s = get<uint8_t>(h, "self_attn.qkv.scales", li, &ok);
@@ -331,6 +376,31 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         const int nqkv = h->Hq * h->hd * 2 + 2 * h->Hkv * h->hd;
         uint16_t* qkv = (uint16_t*)h->ws(h->off_qkv);
         if (gemm(h, qkv_t, qkv_s, act_h, H, nqkv, EPI_BF16, qkv, nqkv, nqkv, nullptr, 0, stream)) return 1;
+        if (io.slot) {
+            PrefillAttnArgs p{};
+            p.L = h->T;
+            p.rows = h->B;
+            p.Hq = h->Hq;
+            p.Hkv = h->Hkv;
+            p.S = h->S;
+            p.slot = io.slot;
+            p.start = io.start;
+            p.qkv = qkv;
+            p.ld = nqkv;
+            p.kv_col = h->Hq * h->hd * 2;
+            p.q_norm = qn;
+            p.k_norm = kn;
+            p.cos = io.cos;
+            p.sin = io.sin;
+            p.k_cache = kc;
+            p.v_cache = vc;
+            p.qs = (uint16_t*)h->ws(h->off_pqs);
+            p.act = act_mid;
+            p.eps = h->cfg.rms_norm_eps;
+            HIP_TRY(q38_attn_prefill(p, stream));
+            kmid = h->Hq * h->hd;
+            goto out_proj;
+        }
         AttnArgs a{};
         a.B = h->B;
         a.K = h->K;
@@ -357,6 +427,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         HIP_TRY(q38_attn_verify(a, stream));
         kmid = h->Hq * h->hd;
     }
+out_proj:
     // x += o_proj(mixer): split-K partials, then residual add and the post-mixer norm in one row kernel.
     if (gemm(h, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     auto post = get<uint16_t>(h, "post_attention_layernorm", li, &ok);
@@ -422,6 +493,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     if (c.num_attention_heads / c.num_key_value_heads * c.verify_tokens > 64) bad += "query rows per KV head above 64; ";
     if (c.batch_size < 1) bad += "batch_size must be positive; ";
     if (c.max_seq_len % 32 || c.max_seq_len < 64) bad += "max_seq_len must be a multiple of 32; ";
+    if (c.prefill_chunk < 0 || c.prefill_chunk % 32 || c.prefill_chunk > c.max_seq_len) bad += "prefill_chunk must be a multiple of 32 up to max_seq_len; ";
     for (int i = 0; i < c.num_layers && i < Q38_MAX_LAYERS; ++i)
         if (c.layer_types[i] != Q38_LINEAR && c.layer_types[i] != Q38_FULL) bad += "unknown layer type; ";
     if (!bad.empty()) return fail(bad);
@@ -447,7 +519,9 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->layer.resize(c.num_layers + 1);
     h->act_h_k = c.mtp ? 2 * h->H : h->H;
 
-    const size_t Tp = h->Tpad, H = h->H;
+    // Per-token buffers of the layer chain hold a verify step or a prefill chunk; the head and the speculative step's
+    // buffers hold a verify step.
+    const size_t Tv = h->Tpad, Tc = c.prefill_chunk ? pad_tokens(c.prefill_chunk) : 0, Tp = std::max(Tv, Tc), H = h->H;
     const size_t mid = std::max((size_t)h->Hv * h->dk, (size_t)h->Hq * h->hd);
     const size_t nqkv = (size_t)h->Hq * h->hd * 2 + 2 * (size_t)h->Hkv * h->hd;
     size_t o = 0;
@@ -473,20 +547,32 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_astats = take(heads * h->attn_nchunks * ATTN_QMAX * 2 * 4);
     h->off_aown = take(heads * ATTN_QMAX * ATTN_KMAX * 4);
     h->off_akv = take(heads * 2 * ATTN_KMAX * 256 * 4);
-    h->off_htiles = take(Tp * H * 2);
-    h->off_x32 = take(Tp * H * 4);
-    h->off_maxima = take(Tp * (h->V / 32) * 4);
-    h->off_sp_embeds = take(Tp * H * 2);
-    h->off_sp_cos = take(Tp * 64 * 2);
-    h->off_sp_sin = take(Tp * 64 * 2);
-    h->off_sp_states = take(Tp * H * 2);
-    h->off_sp_out = take(Tp * H * 2);
-    h->off_sp_current = take(Tp * H * 2);
-    h->off_sp_ids = take(Tp * 4);
-    h->off_sp_at = take(Tp * 4);
-    h->off_sp_draft = take(Tp * 4);
+    h->off_htiles = take(Tv * H * 2);
+    h->off_x32 = take(Tv * H * 4);
+    h->off_maxima = take(Tv * (h->V / 32) * 4);
+    h->off_sp_embeds = take(Tv * H * 2);
+    h->off_sp_cos = take(Tv * 64 * 2);
+    h->off_sp_sin = take(Tv * 64 * 2);
+    h->off_sp_states = take(Tv * H * 2);
+    h->off_sp_out = take(Tv * H * 2);
+    h->off_sp_current = take(Tv * H * 2);
+    h->off_sp_ids = take(Tv * 4);
+    h->off_sp_at = take(Tv * 4);
+    h->off_sp_draft = take(Tv * 4);
     h->off_gemm = take(gemm_scratch_bytes(h->cus));
-    h->off_part = take((size_t)GEMM_SPLIT_MAX * Tp * H * 4);
+    // Split-K partials: up to GEMM_SPLIT_MAX splits at the verify width, 2 at a prefill chunk's (whose tiles alone
+    // fill the CUs); gemm() caps the splits at what fits.
+    h->part_floats = std::max((size_t)GEMM_SPLIT_MAX * Tv, 2 * Tc) * H;
+    h->off_part = take(h->part_floats * 4);
+    if (Tc) {
+        h->off_pqn = take(Tc * h->Hk * h->dk * 4);
+        h->off_pkn = take(Tc * h->Hk * h->dk * 4);
+        h->off_pv = take(Tc * h->Hv * h->dk * 4);
+        h->off_po = take(Tc * h->Hv * h->dk * 4);
+        h->off_pbeta = take(Tc * h->Hv * 4);
+        h->off_pg = take(Tc * h->Hv * 4);
+        h->off_pqs = take((size_t)h->Hq * Tc * 256 * 2);
+    }
     h->workspace_bytes = o;
     *out = h;
     return 0;
@@ -663,6 +749,96 @@ int q38_decode(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const
         if (run_mlp(h, li, li + 1 < L ? li + 1 : -1, out_hidden, false, stream)) return 1;
     }
     h->parity = wr;  // the conv states were written to the other half
+    return 0;
+}
+
+int q38_prefill(q38_handle* h, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin, const int32_t* slot,
+                const int32_t* start, const int32_t* n_valid, int tokens, uint16_t* out_hidden, void* stream_) {
+    if (!h || !embeds || !cos || !sin || !slot || !start || !n_valid || !out_hidden) return fail("null argument");
+    if (!h->cfg.prefill_chunk) return fail("the handle was created without a prefill chunk (config prefill_chunk is 0)");
+    if (tokens < 32 || tokens % 32 || tokens > h->cfg.prefill_chunk)
+        return fail("prefill tokens must be a multiple of 32 up to the config's prefill_chunk");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto in0 = get<uint16_t>(h, "input_layernorm", 0, &ok);
+    if (!ok) return 1;
+    TokensScope chunk(h, 1, tokens);
+    const int L = h->cfg.num_layers, rd = h->parity;
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    uint16_t* hbf = is_linear(h, 0) ? (uint16_t*)h->ws(h->off_hbf) : nullptr;
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, x, in0, h->ws(h->off_act_h), h->H, 0, hbf, nullptr, stream)) return 1;
+    StepIO io{cos, sin, nullptr, nullptr, nullptr, false, slot, start, n_valid};
+    for (int li = 0; li < L; ++li) {
+        if (run_mixer(h, li, io, rd, rd, stream)) return 1;
+        if (run_mlp(h, li, li + 1 < L ? li + 1 : -1, out_hidden, false, stream)) return 1;
+    }
+    return 0;  // the row's states and cache were updated in place; the parity stays
+}
+
+int q38_mtp_prefill(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, const uint16_t* cos, const uint16_t* sin,
+                    const int32_t* slot, const int32_t* start, int tokens, uint16_t* out_x, void* stream_) {
+    if (!h || !hidden || !embeds || !cos || !sin || !slot || !start) return fail("null argument");
+    if (!h->cfg.mtp) return fail("the handle was created without the MTP layer");
+    if (!h->cfg.prefill_chunk) return fail("the handle was created without a prefill chunk (config prefill_chunk is 0)");
+    if (tokens < 32 || tokens % 32 || tokens > h->cfg.prefill_chunk)
+        return fail("prefill tokens must be a multiple of 32 up to the config's prefill_chunk");
+    hipStream_t stream = (hipStream_t)stream_;
+    const int M = h->cfg.num_layers, H = h->H;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto en = get<uint16_t>(h, "mtp.embedding_norm", M, &ok);
+    auto hn = get<uint16_t>(h, "mtp.hidden_norm", M, &ok);
+    auto fin = get<uint16_t>(h, "head.norm", -1, &ok);
+    auto fc_t = get<uint8_t>(h, "mtp.fc.tiles", M, &ok);
+    auto fc_s = get<uint8_t>(h, "mtp.fc.scales", M, &ok);
+    auto in0 = get<uint16_t>(h, "input_layernorm", M, &ok);
+    auto qkv_t = get<uint8_t>(h, "self_attn.qkv.tiles", M, &ok);
+    auto qkv_s = get<uint8_t>(h, "self_attn.qkv.scales", M, &ok);
+    auto kn = get<uint16_t>(h, "self_attn.k_norm", M, &ok);
+    auto kc = get<uint16_t>(h, "self_attn.k_cache", M, &ok);
+    auto vc = get<uint16_t>(h, "self_attn.v_cache", M, &ok);
+    if (!ok) return 1;
+    TokensScope chunk(h, 1, tokens);
+    uint8_t* act_h = h->ws(h->off_act_h);
+    uint16_t* tmp = (uint16_t*)h->ws(h->off_tmp);
+    uint16_t* x = (uint16_t*)h->ws(h->off_x);
+    // [rms(embeds) | rms(rms(hidden, final norm), hidden norm)] -> fc -> x; rms(x, input norm) as e5m2 tiles
+    // (model.py:845-855, the prefill form).
+    if (norm_rows(h, nullptr, 0, embeds, nullptr, nullptr, en, act_h, 2 * H, 0, nullptr, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, hidden, nullptr, nullptr, fin, nullptr, 0, 0, tmp, nullptr, stream)) return 1;
+    if (norm_rows(h, nullptr, 0, tmp, nullptr, nullptr, hn, act_h, 2 * H, H, nullptr, nullptr, stream)) return 1;
+    int splits = 0;
+    if (gemm(h, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, nullptr, x, in0, act_h, H, 0, nullptr, nullptr, stream))
+        return 1;
+    // Keys and values only (cache_chunk, model.py:784-790): the k and v rows of the qkv weight, after the q rows.
+    const size_t q_rows = (size_t)h->Hq * h->hd * 2, kt = (size_t)H / 64;
+    const int nkv = 2 * h->Hkv * h->hd;
+    uint16_t* kv = (uint16_t*)h->ws(h->off_qkv);
+    if (gemm(h, qkv_t + q_rows / 32 * kt * 2048, qkv_s + q_rows / 32 * kt * 64, act_h, H, nkv, EPI_BF16, kv, nkv, nkv, nullptr, 0,
+             stream))
+        return 1;
+    PrefillAttnArgs p{};
+    p.L = h->T;
+    p.rows = h->B;
+    p.Hq = h->Hq;
+    p.Hkv = h->Hkv;
+    p.S = h->S;
+    p.slot = slot;
+    p.start = start;
+    p.qkv = kv;
+    p.ld = nkv;
+    p.kv_col = 0;
+    p.k_norm = kn;
+    p.cos = cos;
+    p.sin = sin;
+    p.k_cache = kc;
+    p.v_cache = vc;
+    p.eps = h->cfg.rms_norm_eps;
+    p.keys_only = 1;
+    HIP_TRY(q38_attn_prefill(p, stream));
+    if (out_x) HIP_TRY(hipMemcpyAsync(out_x, x, (size_t)H * 2, hipMemcpyDeviceToDevice, stream));
     return 0;
 }
 

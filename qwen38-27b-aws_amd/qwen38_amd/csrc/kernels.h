@@ -80,6 +80,54 @@ struct GdnArgs {
     float eps;
 };
 
+// Gated delta net over one prefill chunk of one row (prefill.hip).
+struct PrefillGdnArgs {
+    int L, Hk, Hv, C;
+    int rows;                // rows of the state buffers: a slot outside [0, rows) makes every kernel return
+    const int* slot;         // int32 [1] on the device: the row
+    const int* start;        // int32 [1]: the chunk's first position (0 restarts the row's states)
+    const int* n_valid;      // int32 [1]: real tokens; the rest are padding
+    const bf16_t* qkv;       // [L][C]: the chunk's in_proj_qkv output
+    const bf16_t* z;         // [L][Hv*128]
+    const float* gate_part;  // [gate_groups][L][2 Hv] (gates kernel)
+    int gate_groups;
+    const bf16_t* a_log;
+    const bf16_t* dt_bias;
+    const bf16_t* conv_w;    // [C][4]
+    const bf16_t* norm_w;    // [128]
+    bf16_t* state;           // [B][Hv][128][128]: row slot read and replaced
+    bf16_t* conv;            // [B][C][3], the current half: row slot read and replaced
+    float* qn;               // scratch [L][Hk][128]: normed q times d^-1/2
+    float* kn;               // scratch [L][Hk][128]
+    float* v;                // scratch [L][Hv][128]
+    float* beta;             // scratch [L][Hv]
+    float* g;                // scratch [L][Hv]
+    float* o;                // scratch [L][Hv][128]
+    uint8_t* act;            // e5m2 activation tiles of width Hv*128 for out_proj
+    float eps;
+};
+
+// Attention over one prefill chunk of one row (prefill.hip); with keys_only, only the keys and values are written
+// (the MTP layer's cache_chunk).
+struct PrefillAttnArgs {
+    int L, Hq, Hkv, S;
+    int rows;                // rows of the caches: a slot outside [0, rows) makes every kernel return
+    const int* slot;
+    const int* start;
+    const bf16_t* qkv;       // [L][ld]: per query head [q 256 | gate 256], keys and values from column kv_col
+    int ld, kv_col;
+    const bf16_t* q_norm;
+    const bf16_t* k_norm;
+    const bf16_t* cos;       // [L][64]
+    const bf16_t* sin;
+    bf16_t* k_cache;         // [B][Hkv][S][256]
+    bf16_t* v_cache;         // [B][Hkv][S/32][256][32]
+    bf16_t* qs;              // scratch [Hq][L][256]: normed, rotated queries times 1/16
+    uint8_t* act;            // e5m2 activation tiles of width Hq*256 for o_proj
+    float eps;
+    int keys_only;
+};
+
 #define ATTN_KMAX 8   // verify tokens
 #define ATTN_QMAX 64  // query rows per KV head
 #define ATTN_CHUNK 512  // cached positions per attn_scores workgroup (32 per wave)
@@ -142,6 +190,8 @@ struct CopyStatesArgs {
     int to_saved;
 };
 hipError_t q38_copy_states(const CopyStatesArgs& a, hipStream_t stream);
+hipError_t q38_gdn_prefill(const PrefillGdnArgs& a, hipStream_t stream);
+hipError_t q38_attn_prefill(const PrefillAttnArgs& a, hipStream_t stream);
 hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream);
 hipError_t q38_head_pick(const PickArgs& a, hipStream_t stream);
 hipError_t q38_accept(const int* picks, const int* drafts, const float* active, int B, int K, int* match, int* accepted,

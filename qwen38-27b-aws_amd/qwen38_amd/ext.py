@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
     "q38_kernel_timer",
 )
 
@@ -33,7 +33,7 @@ class Q38Config(ctypes.Structure):
         ("linear_key_head_dim", ctypes.c_int), ("linear_value_head_dim", ctypes.c_int),
         ("linear_conv_kernel_dim", ctypes.c_int), ("rms_norm_eps", ctypes.c_float),
         ("batch_size", ctypes.c_int), ("verify_tokens", ctypes.c_int), ("max_seq_len", ctypes.c_int), ("mtp", ctypes.c_int),
-        ("saved_states", ctypes.c_int),
+        ("saved_states", ctypes.c_int), ("prefill_chunk", ctypes.c_int),
     ]
 
 
@@ -68,6 +68,8 @@ def library() -> ctypes.CDLL:
     lib.q38_verify.argtypes = [p] * 8 + [p]
     lib.q38_decode.argtypes = [p] * 8
     lib.q38_copy_states.argtypes = [p, p, i, p]
+    lib.q38_prefill.argtypes = [p, p, p, p, p, p, p, i, p, p]
+    lib.q38_mtp_prefill.argtypes = [p, p, p, p, p, p, p, i, p, p]
     lib.q38_mtp_step.argtypes = [p] * 8 + [p]
     lib.q38_head_groupmax.argtypes = [p, p, i, p, p]
     lib.q38_head_pick.argtypes = [p, p, i, i, p, p]
@@ -100,7 +102,8 @@ def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False) -> Q38Config:
+def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
+                prefill_chunk: int = 0) -> Q38Config:
     c = Q38Config()
     c.hidden_size, c.intermediate_size, c.vocab_size = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     if cfg.num_hidden_layers > MAX_LAYERS:
@@ -116,15 +119,17 @@ def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp:
     c.rms_norm_eps = cfg.rms_norm_eps
     c.batch_size, c.verify_tokens, c.max_seq_len, c.mtp = batch, tokens, max_seq_len, int(mtp)
     c.saved_states = int(saved_states)
+    c.prefill_chunk = prefill_chunk
     return c
 
 
 class Handle:
     """One q38_handle: shapes fixed at creation, every buffer bound by the owner."""
 
-    def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False):
+    def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
+                 prefill_chunk: int = 0):
         self.lib = library()
-        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states)
+        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk)
         h = ctypes.c_void_p()
         check(self.lib.q38_create(ctypes.byref(self.c), ctypes.byref(h)))
         self.h = h
@@ -157,6 +162,12 @@ class Handle:
 
     def decode(self, embeds, cos, sin, position, active, out) -> None:
         check(self.lib.q38_decode(self.h, *map(ptr, (embeds, cos, sin, position, active, out)), stream()))
+
+    def prefill(self, embeds, cos, sin, slot, start, n_valid, tokens: int, out) -> None:
+        check(self.lib.q38_prefill(self.h, *map(ptr, (embeds, cos, sin, slot, start, n_valid)), tokens, ptr(out), stream()))
+
+    def mtp_prefill(self, hidden, embeds, cos, sin, slot, start, tokens: int, out) -> None:
+        check(self.lib.q38_mtp_prefill(self.h, *map(ptr, (hidden, embeds, cos, sin, slot, start)), tokens, ptr(out), stream()))
 
     def copy_states(self, slot, to_saved: bool) -> None:
         check(self.lib.q38_copy_states(self.h, ptr(slot), int(to_saved), stream()))

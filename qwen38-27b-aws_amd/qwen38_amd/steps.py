@@ -42,13 +42,13 @@ class Engine:
     """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
 
     def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda",
-                 saved_states: bool = False):
+                 saved_states: bool = False, prefill_chunk: int = 0):
         if not torch.cuda.is_available():
             raise RuntimeError("the verify path runs on the GPU only")
         self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
-        self.saved_states = saved_states
+        self.saved_states, self.prefill_chunk = saved_states, prefill_chunk
         self.device = torch.device(device)
-        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states)
+        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk)
         self.buffers: dict[tuple[str, int], torch.Tensor] = {}
         self.mtp_layer = cfg.num_hidden_layers
         self._bind_zeros("workspace", -1, torch.uint8)
@@ -255,7 +255,7 @@ class StepGraph:
             e.handle.copy_states(_dev(torch.as_tensor(which).reshape(1), torch.int32, e.device), save_slot is not None)
             return inputs_embeds
         if slot is not None:
-            raise NotImplementedError("the prefill form is not part of this build")
+            return self._prefill(inputs_embeds, cos, sin, slot, start, n_valid)
         if accepted is not None:
             return self.verify(inputs_embeds, cos=cos, sin=sin, position=position, active=active, accepted=accepted)
         b, h = e.batch_size, e.cfg.hidden_size
@@ -270,6 +270,35 @@ class StepGraph:
         return out
 
 
+    def _prefill(self, inputs_embeds, cos, sin, slot, start, n_valid) -> torch.Tensor:
+        """One chunk ``[1, L, H]`` of row ``slot`` from ``start`` (model.py:476-521, 704-783); returns ``[1, L, H]``."""
+        e = self.engine
+        chunk = _check_chunk(e, inputs_embeds, slot, start, n_valid)
+        dev, h = e.device, e.cfg.hidden_size
+        out = torch.empty(1, chunk, h, dtype=DTYPE, device=dev)
+        e.handle.prefill(
+            _dev(inputs_embeds.reshape(chunk, h), DTYPE, dev), _dev(cos.reshape(chunk, -1), DTYPE, dev),
+            _dev(sin.reshape(chunk, -1), DTYPE, dev), _dev(slot.reshape(1), torch.int32, dev),
+            _dev(start.reshape(1), torch.int32, dev), _dev(n_valid.reshape(1), torch.int32, dev), chunk, out,
+        )
+        return out
+
+
+def _check_chunk(e, inputs_embeds, slot, start, n_valid) -> int:
+    """The host-side checks of a prefill chunk's inputs (the device reads slot, start and n_valid itself)."""
+    if not e.prefill_chunk:
+        raise ValueError("the engine was built without a prefill chunk (prefill_chunk=0)")
+    if inputs_embeds.dim() != 3 or inputs_embeds.shape[0] != 1 or inputs_embeds.shape[2] != e.cfg.hidden_size:
+        raise ValueError(f"inputs_embeds must be [1, chunk, {e.cfg.hidden_size}], got {list(inputs_embeds.shape)}")
+    chunk = inputs_embeds.shape[1]
+    if chunk % 32 or chunk > e.prefill_chunk:
+        raise ValueError(f"a chunk holds a multiple of 32 tokens up to {e.prefill_chunk}, got {chunk}")
+    s, st, n = int(torch.as_tensor(slot).reshape(-1)[0]), int(torch.as_tensor(start).reshape(-1)[0]), int(torch.as_tensor(n_valid).reshape(-1)[0])
+    if not 0 <= s < e.batch_size or st < 0 or st + chunk > e.max_seq_len or not 0 < n <= chunk:
+        raise ValueError(f"slot {s}, start {st}, n_valid {n} do not fit a chunk of {chunk} in {e.batch_size} rows of {e.max_seq_len}")
+    return chunk
+
+
 class MTPStep:
     """The MTP drafter's step form over [B, K] rows and tokens."""
 
@@ -280,8 +309,8 @@ class MTPStep:
 
     def __call__(self, hidden: torch.Tensor, inputs_embeds: torch.Tensor, **inputs: torch.Tensor) -> torch.Tensor:
         e = self.engine
-        if "slot" in inputs:
-            raise NotImplementedError("the MTP prefill form is not part of the verify path")
+        if inputs.get("slot") is not None:
+            return self._prefill(hidden, inputs_embeds, **inputs)
         b, k, h = e.batch_size, e.verify_tokens, e.cfg.hidden_size
         for name, t in (("hidden", hidden), ("inputs_embeds", inputs_embeds)):
             if tuple(t.shape) != (b, k, h):
@@ -292,6 +321,23 @@ class MTPStep:
             _dev(hidden, DTYPE, dev), _dev(inputs_embeds, DTYPE, dev), _dev(inputs["cos"], DTYPE, dev),
             _dev(inputs["sin"], DTYPE, dev), _dev(inputs["position"], torch.int32, dev),
             _dev(inputs["active"], torch.float32, dev), out,
+        )
+        return out
+
+
+    def _prefill(self, hidden, inputs_embeds, cos, sin, slot, start, n_valid, **_) -> torch.Tensor:
+        """The prefill form (model.py:843-855): only the layer's cache for the chunk; returns the fc output's first
+        row ``[1, 1, H]`` as the reference does."""
+        e = self.engine
+        chunk = _check_chunk(e, inputs_embeds, slot, start, n_valid)
+        if tuple(hidden.shape) != tuple(inputs_embeds.shape):
+            raise ValueError(f"hidden must be {list(inputs_embeds.shape)}, got {list(hidden.shape)}")
+        dev, h = e.device, e.cfg.hidden_size
+        out = torch.empty(1, 1, h, dtype=DTYPE, device=dev)
+        e.handle.mtp_prefill(
+            _dev(hidden.reshape(chunk, h), DTYPE, dev), _dev(inputs_embeds.reshape(chunk, h), DTYPE, dev),
+            _dev(cos.reshape(chunk, -1), DTYPE, dev), _dev(sin.reshape(chunk, -1), DTYPE, dev),
+            _dev(slot.reshape(1), torch.int32, dev), _dev(start.reshape(1), torch.int32, dev), chunk, out,
         )
         return out
 

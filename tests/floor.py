@@ -14,6 +14,7 @@ and the decode scenario's hidden states and states) computed by the oracle in th
 
 from __future__ import annotations
 
+import json
 import os
 import subprocess
 import sys
@@ -27,11 +28,12 @@ for p in (ROOT, ROOT / "qwen38-27b-aws_amd", HERE):
         sys.path.insert(0, str(p))
 
 import torch  # noqa: E402
+from safetensors.torch import load_file  # noqa: E402
 
 from oracle import model as om  # noqa: E402
 from qwen38_amd import synth  # noqa: E402
 from qwen38_amd.config import tiny_config  # noqa: E402
-from qwen38_amd.generate import batch_step_inputs, mtp_step_inputs, verify_inputs  # noqa: E402
+from qwen38_amd.generate import batch_step_inputs, mtp_prefill_inputs, mtp_step_inputs, prefill_inputs, verify_inputs  # noqa: E402
 from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states  # noqa: E402
 
 DECODE_STEPS = 3
@@ -80,6 +82,29 @@ def run_scenario() -> dict:
     vi = verify_inputs(cfg, pos, k, s, torch.bfloat16, meta["active"], [0] * b)
     out["decode.verify"] = om.step_verify(cfg, layers, dst, embed[ids[1]], vi["cos"], vi["sin"], vi["position"], vi["active"],
                                           vi["accepted"])
+
+    # Prefill: the two chunks of tests/golden/prefill_tiny.json on row 1 from the scenario's starting states, then the
+    # MTP layer's prefill form on the first chunk's hidden states.
+    pmeta = json.loads((HERE / "golden" / "prefill_tiny.json").read_text())
+    pids = load_file(HERE / "golden" / "prefill_tiny.safetensors")["ids"].long()
+    pst = tiny_states(cfg, meta, meta["seed"])
+    chunk, slot = pmeta["chunk"], pmeta["slot"]
+    for n, (start, n_valid) in enumerate(pmeta["chunks"]):
+        chunk_ids = pids[start : start + chunk].clone()
+        chunk_ids[n_valid:] = 0
+        pi = prefill_inputs(cfg, slot, start, n_valid, chunk, torch.bfloat16)
+        out[f"prefill.hidden_p{n + 1}"] = om.step_prefill(cfg, layers, pst, embed[chunk_ids].reshape(1, chunk, -1), pi["cos"],
+                                                          pi["sin"], pi["slot"], pi["start"], pi["n_valid"])[0]
+    for i, st in enumerate(pst):
+        for key in ("recurrent_state", "conv_state", "k_cache", "v_cache"):
+            if key in st:
+                out[f"prefill.state.{i}.{key}"] = st[key][slot]
+    mst = synth.kv_states(cfg, b, s, meta["context"], meta["seed"], "mtp")
+    mi = mtp_prefill_inputs(cfg, slot, 0, chunk, chunk, torch.bfloat16)
+    out["prefill.mtp_x"] = om.mtp_prefill(cfg, mtp_w, mst, out["prefill.hidden_p1"].unsqueeze(0),
+                                          embed[pids[1 : chunk + 1]].reshape(1, chunk, -1), mi["cos"], mi["sin"], mi["slot"],
+                                          mi["start"], mi["n_valid"])[0]
+    out["prefill.mtp.k_cache"], out["prefill.mtp.v_cache"] = mst["k_cache"][slot], mst["v_cache"][slot]
     return out
 
 
