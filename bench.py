@@ -8,7 +8,7 @@ the state advance. It runs as one library call, `q38_spec_step`, on torch's curr
 resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill]
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
@@ -24,6 +24,12 @@ model.py:983-995 with GatedDeltaNetStep.forward and FullAttentionStep.forward) o
 contexts, one token per row per step: `value` is tokens per second, `roofline` the step's algorithmic HBM bytes
 (weights, scales, gated-delta and conv state read + written, KV read over the context, inputs and outputs) over its
 time, and `cpu_baseline` the CPU oracle's decode of one block, x16.
+
+`--prefill` measures the prefill form (`q38_prefill`, model.py:476-521 and 704-783): one row's prompt of 4096 tokens in
+two chunks of 2048 (the second one attending to the first's 2048 cached positions) plus the MTP layer's cache-only
+prefill of each chunk: `value` is prompt tokens per second, `roofline` the projections' bf16 MFMA work (2 x tokens x
+every projection weight; attention's own products left out) over the time against the dense bf16 peak, and `cpu_baseline` the CPU oracle's prefill of one block
+on a 512-token chunk, x16.
 """
 
 from __future__ import annotations
@@ -289,6 +295,123 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
     }
 
 
+def cpu_prefill_baseline(cfg_block, max_seq_len: int, chunk: int, seed: int, n_blocks: int) -> dict:
+    """The CPU oracle's prefill of one chunk on one block (bf16, all host threads), timed once after one warm-up."""
+    import torch
+
+    from oracle import model as om
+    from qwen38_amd import synth
+    from qwen38_amd.generate import prefill_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    layers = []
+    for i in range(cfg_block.num_hidden_layers):
+        prefix = f"layers.{i}."
+        w = {}
+        for spec in synth.layer_specs(cfg_block, i):
+            v = synth.make(spec, seed, "cuda")
+            w[spec.name[len(prefix):]] = om.FP8Weight(*(x.cpu() for x in v)) if isinstance(v, tuple) else v.cpu()
+        layers.append(w)
+    x = synth.hidden_states((1, chunk, cfg_block.hidden_size), seed, "cpu.prefill.x")
+    pi = prefill_inputs(cfg_block, 0, 0, chunk, chunk, torch.bfloat16)
+    times = []
+    for _ in range(2):
+        states = []
+        for i, kind in enumerate(cfg_block.layer_types):
+            if kind == "linear_attention":
+                st = synth.gdn_states(cfg_block, 1, 1, seed, f"cpu.{i}", "cuda")
+                states.append({k: st[k].cpu() for k in ("recurrent_state", "conv_state")})
+            else:
+                states.append({k: v.cpu() for k, v in synth.kv_states(cfg_block, 1, max_seq_len, [0], seed, f"cpu.{i}", "cuda").items()})
+        started = time.perf_counter()
+        om.step_prefill(cfg_block, layers, states, x, pi["cos"], pi["sin"], pi["slot"], pi["start"], pi["n_valid"])
+        times.append(time.perf_counter() - started)
+        log(f"cpu prefill block {times[-1]:.2f}s")
+    return {
+        "value": chunk / (times[-1] * n_blocks),
+        "unit": "prompt tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one block (3 gated-delta + 1 attention layer) prefilling a {chunk}-token chunk from position 0 on the "
+        f"CPU oracle in bf16 ({times[-1]:.2f} s after one warm-up), x{n_blocks} for 64 layers; no MTP layer",
+    }
+
+
+def prefill_main(args) -> dict:
+    """Prompt prefill of one row: chunks of 2048 tokens from position 0, each also through the MTP layer's cache-only
+    prefill, as the reference's scheduler runs a prompt (scheduler.py:110-158)."""
+    import torch
+
+    from qwen38_amd import synth
+    from qwen38_amd.config import qwen38_27b_config
+    from qwen38_amd.generate import mtp_prefill_inputs, prefill_inputs
+    from qwen38_amd.steps import Engine, MTPStep, StepGraph
+
+    cfg = qwen38_27b_config(16)
+    batch, chunk, n_chunks, max_seq_len = 64, 2048, 2, 4096 + 64
+    engine = Engine(cfg, batch, 4, max_seq_len, mtp=True, prefill_chunk=chunk)
+    started = time.time()
+    specs = synth.model_specs(cfg, mtp=True, head=True)
+    engine.load((spec.name, synth.make(spec, args.seed, "cuda")) for spec in specs)
+    log(f"model ready in {time.time() - started:.0f}s")
+    step, mtp = StepGraph(engine), MTPStep(engine)
+    embeds = synth.hidden_states((1, chunk, cfg.hidden_size), args.seed, "bench.prefill", "cuda")
+    inputs = []
+    for c in range(n_chunks):
+        pi = {k: v.cuda() for k, v in prefill_inputs(cfg, 0, c * chunk, chunk, chunk, torch.bfloat16).items()}
+        mi = {k: v.cuda() for k, v in mtp_prefill_inputs(cfg, 0, c * chunk, chunk, chunk, torch.bfloat16).items()}
+        inputs.append((pi, mi))
+
+    def prompt():
+        for pi, mi in inputs:
+            hidden = step(inputs_embeds=embeds, **pi)
+            mtp(hidden=hidden, inputs_embeds=embeds, **mi)
+
+    for _ in range(args.warmup):
+        prompt()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        prompt()
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    tokens = chunk * n_chunks
+    log(f"prefill: {ms:.2f} ms per {tokens}-token prompt")
+    h, inter = cfg.hidden_size, cfg.intermediate_size
+    hv, d, c = cfg.linear_num_value_heads, cfg.linear_key_head_dim, cfg.linear_conv_dim
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    n_gdn = sum(1 for k in cfg.layer_types if k == "linear_attention")
+    n_attn = cfg.num_hidden_layers - n_gdn
+    mlp = 3 * inter * h
+    per_gdn = (c + hv * d) * h + h * hv * d + mlp + 2 * hv * h  # projections, MLP, the bf16 gate projections
+    per_attn = (hq * hd * 2 + 2 * hkv * hd) * h + h * hq * hd + mlp
+    mtp_w = 2 * h * h + 2 * hkv * hd * h  # fc and the k/v rows (cache_chunk)
+    flops = 2.0 * tokens * (n_gdn * per_gdn + n_attn * per_attn + mtp_w)
+    achieved = flops / (ms / 1000.0) / 1e12
+    return {
+        "metric": "prefill prompt tokens/s/GPU, 64 layers + MTP cache, 4096-token prompt in 2048-token chunks",
+        "value": round(tokens / (ms / 1000.0), 1),
+        "unit": "prompt tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "data": "synthetic: seeded random-init weights of the 27B shapes, a synthetic prompt",
+        "config": {"workload": "27b-64L-prefill-4096-chunk2048", "global_batch": 1, "tokens_per_row": tokens, "context": 0,
+                   "parallelism": "none (one GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "flops_per_step": flops},
+        "_engine": engine,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -297,6 +420,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode", action="store_true", help="time the one-token decode graph instead of the speculative step")
+    ap.add_argument("--prefill", action="store_true", help="time the prefill form (one 4096-token prompt) instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -320,6 +444,15 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy probe: {args.copy_probe} MiB read and written by one bitwise_not kernel")
         del src, dst
+    if args.prefill:
+        result = prefill_main(args)
+        engine = result.pop("_engine")
+        if not args.no_cpu_baseline:
+            del engine
+            torch.cuda.empty_cache()
+            result["cpu_baseline"] = cpu_prefill_baseline(qwen38_27b_config(1), 1024, 512, seed, 16)
+        print(json.dumps(result), flush=True)
+        return 0
     engine, st = build(cfg, batch, tokens, max_seq_len, context, seed)
     if args.decode:
         result = decode_main(args, cfg, engine, batch, context, max_seq_len)
