@@ -1,4 +1,5 @@
-"""FP8 weight format of this build: e4m3 bytes with one E8M0 power-of-two scale per 32 input elements.
+"""Weight formats of this build: FP8 e4m3 bytes with one E8M0 power-of-two scale per 32 input elements, and the
+checkpoint's MXFP4 (E2M1 nibbles with the same E8M0 scales), which the GEMMs also read directly.
 
 The reference stores FP8 e5m2 weights ``[in, out]`` with the FP4 checkpoint's scale folded in
 (qwen38_inf2/fp4.py:118-140, checkpoint.py:177-182). BASELINE's weights are FP8 e4m3 with per-32 power-of-two
@@ -49,6 +50,54 @@ def dequantize_e4m3(coded: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     n, k = coded.shape
     values = coded.view(torch.float8_e4m3fn).float().reshape(n, k // GROUP, GROUP)
     return (values * pow2(scales.to(torch.int32) - E8M0_BIAS).unsqueeze(-1)).reshape(n, k)
+
+
+E2M1_MAGNITUDES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def quantize_mxfp4(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize a float ``[N, K]`` matrix to the checkpoint's MXFP4 (OCP microscaling E2M1 + E8M0, the format the
+    reference loads, fp4.py:1-13): (packed bytes ``[N, K/2]``, the even element in the low nibble, a nibble being sign
+    (bit 3) and a magnitude index into 0, 0.5, 1, 1.5, 2, 3, 4, 6; E8M0 bytes ``[N, K/32]``). A group's scale is
+    ``2**(floor(log2(amax)) - 2)``, 2 being E2M1's largest exponent; values round to the nearest magnitude (ties to
+    the even index) and saturate at 6."""
+    n, k = weight.shape
+    if k % GROUP:
+        raise ValueError(f"K={k} is not a multiple of {GROUP}")
+    groups = weight.float().reshape(n, k // GROUP, GROUP)
+    amax = groups.abs().amax(dim=-1)
+    _, exponent = torch.frexp(amax)
+    scale_exp = torch.where(amax > 0, exponent - 1 - 2, torch.zeros_like(exponent)).clamp(-126, 126)
+    scaled = groups * pow2(-scale_exp).unsqueeze(-1)
+    mags = torch.tensor(E2M1_MAGNITUDES, device=weight.device)
+    # Nearest magnitude; at a midpoint the even index (a zero mantissa bit) wins, as round-to-nearest-even does.
+    dist = (scaled.abs().clamp(max=6.0).unsqueeze(-1) - mags).abs()
+    best = dist.min(dim=-1, keepdim=True).values
+    cand = (dist == best) & (torch.arange(8, device=weight.device) % 2 == 0)
+    index = torch.where(cand.any(dim=-1), cand.int().argmax(dim=-1), dist.argmin(dim=-1))
+    nibble = (index | torch.where(scaled < 0, 8, 0)).to(torch.uint8).reshape(n, k)
+    packed = nibble[:, 0::2] | (nibble[:, 1::2] << 4)
+    return packed, (scale_exp + E8M0_BIAS).to(torch.uint8)
+
+
+def dequantize_mxfp4(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """float32 ``[N, K]`` from MXFP4 bytes and E8M0 scale bytes (the reference's `fp4.decode_host`, fp4.py:36-42)."""
+    n, half = packed.shape
+    lut = torch.tensor(E2M1_MAGNITUDES, device=packed.device)
+    lut = torch.cat((lut, -lut))
+    nibbles = torch.stack((packed & 0x0F, packed >> 4), dim=-1).reshape(n, 2 * half)
+    values = lut[nibbles.long()].reshape(n, half * 2 // GROUP, GROUP)
+    return (values * pow2(scales.to(torch.int32) - E8M0_BIAS).unsqueeze(-1)).reshape(n, 2 * half)
+
+
+def mxfp4_to_e4m3(packed: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The same weights in this build's FP8 format, exactly: every E2M1 magnitude is an e4m3 value, so the e4m3 bytes
+    keep the group's E8M0 scale."""
+    n, half = packed.shape
+    lut = torch.tensor(E2M1_MAGNITUDES, device=packed.device)
+    lut = torch.cat((lut, -lut)).to(torch.float8_e4m3fn).view(torch.uint8)
+    nibbles = torch.stack((packed & 0x0F, packed >> 4), dim=-1).reshape(n, 2 * half)
+    return lut[nibbles.long()], scales.clone()
 
 
 def round_e5m2(x: torch.Tensor) -> torch.Tensor:

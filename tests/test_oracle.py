@@ -429,3 +429,26 @@ def test_prefill_then_decode_equals_decoding_every_token(monkeypatch):
             if key.endswith("cache"):
                 a, b = a[:, :24], b[:, :24]
             assert torch.allclose(a, b, atol=2e-4, rtol=2e-4), (i, key)
+
+
+def test_mxfp4_codec_matches_the_references_decode_kat_and_converts_exactly_to_e4m3():
+    """The checkpoint's MXFP4 decode against the reference's own known-answer file (tests/golden/fp4_decode_kat,
+    the reference's tests/golden/decode.safetensors: every byte value, scales as bf16 powers of two); quantization
+    round trips every E2M1 value; the e4m3 form of the same weights dequantizes to the same values."""
+    from safetensors.torch import load_file as load
+
+    from qwen38_amd.quant import dequantize_e4m3, dequantize_mxfp4, mxfp4_to_e4m3, quantize_mxfp4
+
+    kat = load(GOLDEN / "fp4_decode_kat.safetensors")
+    mant, exp = torch.frexp(kat["weight_scale"].float())
+    assert bool((mant == 0.5).all())
+    scale_bytes = (exp - 1 + 127).to(torch.uint8)
+    assert torch.equal(dequantize_mxfp4(kat["weight_packed"], scale_bytes).to(torch.bfloat16), kat["expected"])
+
+    codes = torch.arange(256, dtype=torch.uint8).reshape(8, 32)  # every byte: both nibbles of every code
+    scales = torch.tensor([[100 + r] for r in range(8)], dtype=torch.uint8)
+    values = dequantize_mxfp4(codes, scales)
+    packed, back = quantize_mxfp4(values)
+    assert torch.equal(dequantize_mxfp4(packed, back), values)
+    coded, s8 = mxfp4_to_e4m3(codes, scales)
+    assert torch.equal(dequantize_e4m3(coded, s8), values)
