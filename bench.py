@@ -8,7 +8,7 @@ the state advance. It runs as one library call, `q38_spec_step`, on torch's curr
 resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill] [--mxfp4]
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
@@ -30,6 +30,10 @@ two chunks of 2048 (the second one attending to the first's 2048 cached position
 prefill of each chunk: `value` is prompt tokens per second, `roofline` the projections' bf16 MFMA work (2 x tokens x
 every projection weight; attention's own products left out) over the time against the dense bf16 peak, and `cpu_baseline` the CPU oracle's prefill of one block
 on a 512-token chunk, x16.
+
+`--mxfp4` binds the 64 decoder layers' projections as MXFP4 (the checkpoint's E2M1 nibbles + E8M0 scales, read by the
+GEMMs directly: half the weight bytes of e4m3), the seeded e4m3 weights requantized; the MTP layer and the head stay
+e4m3, as an MXFP4 checkpoint holds them in bf16. The algorithmic bytes count the decoder weights at 4.25 bits.
 """
 
 from __future__ import annotations
@@ -58,7 +62,11 @@ def fp8_bytes(n: int, k: int) -> int:
     return n * k + n * k // 32
 
 
-def algorithmic_bytes(cfg, batch: int, tokens: int, context: int) -> dict:
+def fp4_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * k // 32
+
+
+def algorithmic_bytes(cfg, batch: int, tokens: int, context: int, mxfp4: bool = False) -> dict:
     """Compulsory HBM bytes of one step, each counted once: FP8 weights + E8M0 scales of every projection streamed,
     bf16 small weights, gated-delta state and conv state read + written, KV read over each row's context plus the
     step's own K/V written, the head read once per pass plus the recheck rows, the MTP layer per call, inputs/outputs."""
@@ -66,9 +74,11 @@ def algorithmic_bytes(cfg, batch: int, tokens: int, context: int) -> dict:
     hv, hk, d, c = cfg.linear_num_value_heads, cfg.linear_num_key_heads, cfg.linear_key_head_dim, cfg.linear_conv_dim
     hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     t = batch * tokens
-    mlp = fp8_bytes(2 * inter, h) + fp8_bytes(h, inter)
-    gdn_w = fp8_bytes(c + hv * d, h) + fp8_bytes(h, hv * d) + mlp + 2 * hv * h * 2 + c * 4 * 2
-    attn_w = fp8_bytes(hq * hd * 2 + 2 * hkv * hd, h) + fp8_bytes(h, hq * hd) + mlp
+    wb = fp4_bytes if mxfp4 else fp8_bytes  # the decoder layers' projections
+    mlp = wb(2 * inter, h) + wb(h, inter)
+    gdn_w = wb(c + hv * d, h) + wb(h, hv * d) + mlp + 2 * hv * h * 2 + c * 4 * 2
+    attn_w = wb(hq * hd * 2 + 2 * hkv * hd, h) + wb(h, hq * hd) + mlp
+    attn_w8 = fp8_bytes(hq * hd * 2 + 2 * hkv * hd, h) + fp8_bytes(h, hq * hd) + fp8_bytes(2 * inter, h) + fp8_bytes(h, inter)
     n_gdn = sum(1 for k in cfg.layer_types if k == "linear_attention")
     n_attn = cfg.num_hidden_layers - n_gdn
     weights = n_gdn * gdn_w + n_attn * attn_w
@@ -78,19 +88,19 @@ def algorithmic_bytes(cfg, batch: int, tokens: int, context: int) -> dict:
     io = t * h * 2 * 2
     head_pass = fp8_bytes(v, h)
     head = 4 * head_pass + (t * 4 + 3 * batch) * 32 * (h + h // 32)
-    mtp_w = fp8_bytes(h, 2 * h) + attn_w
+    mtp_w = fp8_bytes(h, 2 * h) + attn_w8
     mtp = 3 * (mtp_w + kv_read + t * hkv * hd * 2 * 2 + 3 * t * h * 2)
     total = weights + state + kv + io + head + mtp
     return {"total": total, "weights": weights, "state": state, "kv": kv, "head": head, "mtp": mtp, "io": io}
 
 
-def decode_bytes(cfg, batch: int, context: int) -> int:
+def decode_bytes(cfg, batch: int, context: int, mxfp4: bool = False) -> int:
     """Compulsory HBM bytes of one decode step (no head, no MTP): as `algorithmic_bytes` with one token per row."""
-    b = algorithmic_bytes(cfg, batch, 1, context)
+    b = algorithmic_bytes(cfg, batch, 1, context, mxfp4)
     return b["weights"] + b["state"] + b["kv"] + b["io"]
 
 
-def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int):
+def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, mxfp4: bool = False):
     import torch
 
     from qwen38_amd import synth
@@ -98,7 +108,7 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
     from qwen38_amd.steps import Engine
 
     dev = "cuda"
-    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev)
+    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev, weight_format="mxfp4" if mxfp4 else "e4m3")
     started = time.time()
     specs = synth.model_specs(cfg, mtp=True, head=True)
 
@@ -108,7 +118,7 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
                 log(f"weights {n}/{len(specs)} ({time.time() - started:.0f}s)")
             yield spec.name, synth.make(spec, seed, dev)
 
-    engine.load(weights())
+    engine.load(synth.to_mxfp4(weights()) if mxfp4 else weights())
     ctx = [context] * batch
     for i, kind in enumerate(cfg.layer_types):
         if kind == "linear_attention":
@@ -273,7 +283,7 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
     end.synchronize()
     ms = start.elapsed_time(end) / args.steps
     log(f"decode: {ms:.3f} ms/step")
-    alg = decode_bytes(cfg, batch, context + args.warmup + args.steps // 2)
+    alg = decode_bytes(cfg, batch, context + args.warmup + args.steps // 2, args.mxfp4)
     gbs = alg / (ms / 1000.0) / 1e9
     return {
         "metric": "decode tokens/s/GPU, 64-layer one-token step, batch 64",
@@ -286,9 +296,9 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
-        "config": {"workload": "27b-64L-b64-decode-ctx512", "global_batch": batch, "tokens_per_row": 1, "context": context,
+        "config": {"workload": "27b-64L-b64-decode-ctx512" + ("-mxfp4" if args.mxfp4 else ""), "global_batch": batch, "tokens_per_row": 1, "context": context,
                    "parallelism": "none (one GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": alg},
@@ -350,10 +360,11 @@ def prefill_main(args) -> dict:
 
     cfg = qwen38_27b_config(16)
     batch, chunk, n_chunks, max_seq_len = 64, 2048, 2, 4096 + 64
-    engine = Engine(cfg, batch, 4, max_seq_len, mtp=True, prefill_chunk=chunk)
+    engine = Engine(cfg, batch, 4, max_seq_len, mtp=True, prefill_chunk=chunk, weight_format="mxfp4" if args.mxfp4 else "e4m3")
     started = time.time()
     specs = synth.model_specs(cfg, mtp=True, head=True)
-    engine.load((spec.name, synth.make(spec, args.seed, "cuda")) for spec in specs)
+    weights = ((spec.name, synth.make(spec, args.seed, "cuda")) for spec in specs)
+    engine.load(synth.to_mxfp4(weights) if args.mxfp4 else weights)
     log(f"model ready in {time.time() - started:.0f}s")
     step, mtp = StepGraph(engine), MTPStep(engine)
     embeds = synth.hidden_states((1, chunk, cfg.hidden_size), args.seed, "bench.prefill", "cuda")
@@ -402,14 +413,20 @@ def prefill_main(args) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, a synthetic prompt",
-        "config": {"workload": "27b-64L-prefill-4096-chunk2048", "global_batch": 1, "tokens_per_row": tokens, "context": 0,
+        "config": {"workload": "27b-64L-prefill-4096-chunk2048" + ("-mxfp4" if args.mxfp4 else ""), "global_batch": 1, "tokens_per_row": tokens, "context": 0,
                    "parallelism": "none (one GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "flops_per_step": flops},
         "_engine": engine,
     }
+
+
+def weight_dtype(args) -> str:
+    if args.mxfp4:
+        return "mxfp4 (e2m1 + e8m0) decoder weights, fp8 e4m3 mtp/head weights, bf16 MFMA (fp32 accumulate)"
+    return "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)"
 
 
 def main() -> int:
@@ -421,6 +438,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode", action="store_true", help="time the one-token decode graph instead of the speculative step")
     ap.add_argument("--prefill", action="store_true", help="time the prefill form (one 4096-token prompt) instead")
+    ap.add_argument("--mxfp4", action="store_true", help="decoder-layer projections as MXFP4 (half the weight bytes)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -453,7 +471,7 @@ def main() -> int:
             result["cpu_baseline"] = cpu_prefill_baseline(qwen38_27b_config(1), 1024, 512, seed, 16)
         print(json.dumps(result), flush=True)
         return 0
-    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed)
+    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4)
     if args.decode:
         result = decode_main(args, cfg, engine, batch, context, max_seq_len)
         if not args.no_cpu_baseline:
@@ -496,7 +514,7 @@ def main() -> int:
     log(f"gate/up GEMM inside the steps: {launches} launches, {kernel_ms * 1000:.1f} us each")
     flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
     achieved = flops / (kernel_ms / 1000.0) / 1e12
-    alg = algorithmic_bytes(cfg, batch, tokens, context)
+    alg = algorithmic_bytes(cfg, batch, tokens, context, args.mxfp4)
     step_gbs = alg["total"] / (ms / 1000.0) / 1e9
     result = {
         "metric": "accepted tokens/s/GPU, 64-layer verify step, batch 64, 4 tokens; HBM GB/s %peak",
@@ -509,10 +527,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)",
+        "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
         "config": {
-            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)",
+            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)" + (" with MXFP4 decoder weights" if args.mxfp4 else ""),
             "global_batch": batch,
             "tokens_per_row": tokens,
             "context": context,
@@ -520,7 +538,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_kernel<2,4,2,2,e5m2,5,SWIGLU> (MLP gate/up, 256 x 34816 x 5120)",
+            "kernel": f"gemm_kernel<2,4,2,2,e5m2,5,SWIGLU,{'e2m1' if args.mxfp4 else 'e4m3'}> (MLP gate/up, 256 x 34816 x 5120)",
             "achieved": round(achieved, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -42,6 +42,8 @@ typedef struct q38_handle q38_handle;
 #define Q38_MAX_LAYERS 128
 #define Q38_LINEAR 0
 #define Q38_FULL 1
+#define Q38_WEIGHTS_E4M3 0  /* projections bound as q38_pack_weight tiles */
+#define Q38_WEIGHTS_MXFP4 1 /* decoder-layer projections bound as q38_pack_weight_fp4 tiles (MTP layer, head: e4m3) */
 
 /* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
  * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
@@ -57,6 +59,7 @@ typedef struct q38_config {
     int batch_size, verify_tokens, max_seq_len, mtp;
     int saved_states; /* a saved recurrent and conv state per row, for q38_copy_states (reference saved_states) */
     int prefill_chunk; /* most tokens of one q38_prefill call (a multiple of 32; 0: no prefill workspace) */
+    int weight_format; /* Q38_WEIGHTS_E4M3 or Q38_WEIGHTS_MXFP4 (the reference's weight_format, config.py:28-30) */
 } q38_config;
 
 const char* q38_last_error(void);
@@ -66,7 +69,8 @@ int q38_create(const q38_config* cfg, q38_handle** out);
 void q38_destroy(q38_handle* h);
 
 /* Buffers, by name and layer (layer -1 for model-wide buffers; layer num_layers is the MTP layer). Sizes in bytes.
- * Weights (FP8 projections bound as packed tiles + tile scales from q38_pack_weight):
+ * Weights (projections bound as packed tiles + tile scales from q38_pack_weight; with weight_format MXFP4 the decoder
+ * layers' projections from q38_pack_weight_fp4, half the tile bytes):
  *   per layer: input_layernorm, post_attention_layernorm (bf16 [H]), mlp.gate_up.{tiles,scales} (gate and up rows
  *     interleaved by 32), mlp.down.{tiles,scales}
  *   gated-delta layers: linear_attn.in_proj_qkvz.{tiles,scales} (in_proj_qkv rows then in_proj_z rows),
@@ -99,6 +103,14 @@ int q38_set_parity(q38_handle* h, int parity);
 int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, uint8_t* tiles, uint8_t* tile_scales,
                     void* stream);
 
+/* Pack an MXFP4 projection as the checkpoint stores it (weight_packed uint8 [N][K/2], the even input in the low
+ * nibble; weight_scale E8M0 bytes [N][K/32]; reference fp4.py:1-13, checkpoint.py:177-182) into tiles
+ * [N/32][K/64][4][64][4] (N * K / 2 bytes: the same element order as q38_pack_weight's, two inputs per byte) and the
+ * same tile scales. N % 32 == 0, K % 256 == 0. The checkpoint's bytes are read as they are: no e5m2 re-encoding
+ * (fp4.to_fp8, fp4.py:118-140) and so none of its rounding of groups with tiny scales. */
+int q38_pack_weight_fp4(const uint8_t* packed, const uint8_t* scales, int n, int k, uint8_t* tiles, uint8_t* tile_scales,
+                        void* stream);
+
 /* A standalone FP8 projection, `FP8Linear.forward` (reference model.py:211-229): x bf16 [rows][k] rounded to e5m2,
  * times the packed weight ([n][k] e4m3 + E8M0), float32 sums, bf16 out [rows][n]. n % 256 == 0, k % 256 == 0.
  * scratch holds q38_fp8_linear_scratch(rows, k) bytes: the e5m2 input tiles (q38_tiles_size(rows, k) bytes), then the
@@ -108,6 +120,11 @@ int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, u
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                    uint8_t* scratch, uint16_t* out, void* stream);
 size_t q38_fp8_linear_scratch(int rows, int k);
+/* q38_fp8_linear with an MXFP4 weight from q38_pack_weight_fp4: e5m2(x) times the exact E2M1 x E8M0 values, which is
+ * `FP8Linear.forward` on the weights `fp4.to_fp8` makes from the checkpoint (model.py:211-229) wherever that conversion
+ * is exact. Same scratch. */
+int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                     uint8_t* scratch, uint16_t* out, void* stream);
 /* The same with float32 output [rows][n] (no bf16 rounding); rows in {32, 64, 128} or a multiple of 256. */
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                        uint8_t* scratch, float* out, void* stream);

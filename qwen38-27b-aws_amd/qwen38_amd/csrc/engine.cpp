@@ -110,12 +110,18 @@ namespace {
 
 bool is_linear(const q38_handle* h, int layer) { return layer < h->cfg.num_layers && h->cfg.layer_types[layer] == Q38_LINEAR; }
 
+// Whether a layer's projections are bound as MXFP4 tiles: the decoder layers of an MXFP4 checkpoint. The MTP layer and
+// the head come as bf16 in that checkpoint and are always e4m3.
+bool fp4_layer(const q38_handle* h, int layer) {
+    return h->cfg.weight_format == Q38_WEIGHTS_MXFP4 && layer >= 0 && layer < h->cfg.num_layers;
+}
+
 // Expected size of a named buffer, or 0 if the name does not exist for that layer.
 size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     const size_t H = h->H, I = h->I, V = h->V, B = h->B, K = h->K, S = h->S;
     const size_t Hq = h->Hq, Hkv = h->Hkv, hd = h->hd, Hk = h->Hk, Hv = h->Hv, dk = h->dk, C = h->C;
     auto fp8 = [&](const std::string& base, size_t n, size_t k) -> size_t {
-        if (name == base + ".tiles") return n * k;
+        if (name == base + ".tiles") return fp4_layer(h, layer) ? n * k / 2 : n * k;
         if (name == base + ".scales") return n * k / 32;
         return 0;
     };
@@ -174,11 +180,13 @@ T* get(q38_handle* h, const std::string& name, int layer, bool* ok) {
     return (T*)it->second.p;
 }
 
-int gemm(q38_handle* h, const uint8_t* tiles, const uint8_t* scales, const uint8_t* act, int K, int N, int epi,
+// A projection of layer li (its weight format decides the GEMM variant).
+int gemm(q38_handle* h, int li, const uint8_t* tiles, const uint8_t* scales, const uint8_t* act, int K, int N, int epi,
          void* out0, int ld0, int n0, void* out1, int ld1, hipStream_t stream, int* splits_out = nullptr) {
     if (N % 256 || K % 256) return fail("GEMM shape N=" + std::to_string(N) + " K=" + std::to_string(K) + " not tileable");
     GemmArgs a{};
     a.w = tiles;
+    a.w4 = fp4_layer(h, li);
     a.ws = scales;
     a.act = act;
     a.K = K;
@@ -284,7 +292,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         // A verify step's qkv output is also its pending input snapshot; a decode step's or a prefill chunk's goes to
         // scratch.
         uint16_t* qkv_out = io.decode || io.slot ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
-        if (gemm(h, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
+        if (gemm(h, li, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
             return 1;
         GatesArgs ga{};
         ga.x = (const bf16_t*)h->ws(h->off_hbf);
@@ -375,7 +383,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         if (!ok) return 1;
         const int nqkv = h->Hq * h->hd * 2 + 2 * h->Hkv * h->hd;
         uint16_t* qkv = (uint16_t*)h->ws(h->off_qkv);
-        if (gemm(h, qkv_t, qkv_s, act_h, H, nqkv, EPI_BF16, qkv, nqkv, nqkv, nullptr, 0, stream)) return 1;
+        if (gemm(h, li, qkv_t, qkv_s, act_h, H, nqkv, EPI_BF16, qkv, nqkv, nqkv, nullptr, 0, stream)) return 1;
         if (io.slot) {
             PrefillAttnArgs p{};
             p.L = h->T;
@@ -429,7 +437,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
     }
 out_proj:
     // x += o_proj(mixer): split-K partials, then residual add and the post-mixer norm in one row kernel.
-    if (gemm(h, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (gemm(h, li, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     auto post = get<uint16_t>(h, "post_attention_layernorm", li, &ok);
     if (!ok) return 1;
     return norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, x, x, post, act_h, H, 0, nullptr, nullptr, stream);
@@ -450,10 +458,10 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     hipEvent_t* timed = h->timer_on && h->timer_used < TIMER_PAIRS ? &h->timer_events[2 * h->timer_used++] : nullptr;
     if (timed) HIP_TRY(hipEventRecord(timed[0], stream));
-    if (gemm(h, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
+    if (gemm(h, li, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
     if (timed) HIP_TRY(hipEventRecord(timed[1], stream));
     int splits = 0;
-    if (gemm(h, dn_t, dn_s, act_ffn, I, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (gemm(h, li, dn_t, dn_s, act_ffn, I, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     const float* part = (const float*)h->ws(h->off_part);
     if (mtp_tail) {
         auto nw = get<uint16_t>(h, "mtp.norm", li, &ok);
@@ -494,6 +502,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     if (c.batch_size < 1) bad += "batch_size must be positive; ";
     if (c.max_seq_len % 32 || c.max_seq_len < 64) bad += "max_seq_len must be a multiple of 32; ";
     if (c.prefill_chunk < 0 || c.prefill_chunk % 32 || c.prefill_chunk > c.max_seq_len) bad += "prefill_chunk must be a multiple of 32 up to max_seq_len; ";
+    if (c.weight_format != Q38_WEIGHTS_E4M3 && c.weight_format != Q38_WEIGHTS_MXFP4) bad += "unknown weight_format; ";
     for (int i = 0; i < c.num_layers && i < Q38_MAX_LAYERS; ++i)
         if (c.layer_types[i] != Q38_LINEAR && c.layer_types[i] != Q38_FULL) bad += "unknown layer type; ";
     if (!bad.empty()) return fail(bad);
@@ -657,6 +666,14 @@ int q38_pack_weight(const uint8_t* coded, const uint8_t* scales, int n, int k, u
     return 0;
 }
 
+int q38_pack_weight_fp4(const uint8_t* packed, const uint8_t* scales, int n, int k, uint8_t* tiles, uint8_t* tile_scales,
+                        void* stream) {
+    if (!packed || !scales || !tiles || !tile_scales) return fail("null argument");
+    if (n <= 0 || k <= 0 || n % 32 || k % 256) return fail("pack needs N % 32 == 0 and K % 256 == 0");
+    HIP_TRY(q38_pack_fp4(packed, scales, n, k, tiles, tile_scales, (hipStream_t)stream));
+    return 0;
+}
+
 size_t q38_tiles_size(int rows, int k) { return align256((size_t)pad_tokens(rows) * k); }
 
 size_t q38_fp8_linear_scratch(int rows, int k) { return q38_tiles_size(rows, k) + gemm_scratch_bytes(device_cus()); }
@@ -665,7 +682,7 @@ namespace {
 
 // One projection outside a handle: e5m2 tiles of x (unless x is null: the scratch already holds them), then the GEMM.
 int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
-               uint8_t* scratch, void* out, int splits_max, hipStream_t stream) {
+               uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0) {
     if (!tiles || !tile_scales || !scratch || !out) return fail("null argument");
     if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
     if (x) HIP_TRY(q38_act_tiles(x, rows, k, scratch, stream));
@@ -678,6 +695,7 @@ int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const u
     a.T = rows;
     a.Tpad = pad_tokens(rows);
     a.splits_max = splits_max;
+    a.w4 = w4;
     if (epi == EPI_PARTIAL)
         a.part = (float*)out;
     else {
@@ -695,6 +713,11 @@ int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const u
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                    uint8_t* scratch, uint16_t* out, void* stream) {
     return standalone(x, rows, k, tiles, tile_scales, n, EPI_BF16, scratch, out, 0, (hipStream_t)stream);
+}
+
+int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                     uint8_t* scratch, uint16_t* out, void* stream) {
+    return standalone(x, rows, k, tiles, tile_scales, n, EPI_BF16, scratch, out, 0, (hipStream_t)stream, 1);
 }
 
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
@@ -809,14 +832,14 @@ int q38_mtp_prefill(q38_handle* h, const uint16_t* hidden, const uint16_t* embed
     if (norm_rows(h, nullptr, 0, hidden, nullptr, nullptr, fin, nullptr, 0, 0, tmp, nullptr, stream)) return 1;
     if (norm_rows(h, nullptr, 0, tmp, nullptr, nullptr, hn, act_h, 2 * H, H, nullptr, nullptr, stream)) return 1;
     int splits = 0;
-    if (gemm(h, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (gemm(h, M, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     if (norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, nullptr, x, in0, act_h, H, 0, nullptr, nullptr, stream))
         return 1;
     // Keys and values only (cache_chunk, model.py:784-790): the k and v rows of the qkv weight, after the q rows.
     const size_t q_rows = (size_t)h->Hq * h->hd * 2, kt = (size_t)H / 64;
     const int nkv = 2 * h->Hkv * h->hd;
     uint16_t* kv = (uint16_t*)h->ws(h->off_qkv);
-    if (gemm(h, qkv_t + q_rows / 32 * kt * 2048, qkv_s + q_rows / 32 * kt * 64, act_h, H, nkv, EPI_BF16, kv, nkv, nkv, nullptr, 0,
+    if (gemm(h, M, qkv_t + q_rows / 32 * kt * 2048, qkv_s + q_rows / 32 * kt * 64, act_h, H, nkv, EPI_BF16, kv, nkv, nkv, nullptr, 0,
              stream))
         return 1;
     PrefillAttnArgs p{};
@@ -898,7 +921,7 @@ int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, 
     if (norm_rows(h, nullptr, 0, hidden, nullptr, nullptr, fin, nullptr, 0, 0, tmp, nullptr, stream)) return 1;
     if (norm_rows(h, nullptr, 0, tmp, nullptr, nullptr, hn, act_h, 2 * H, H, nullptr, nullptr, stream)) return 1;
     int splits = 0;
-    if (gemm(h, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
+    if (gemm(h, M, fc_t, fc_s, act_h, 2 * H, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     if (norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, nullptr, x, in0, act_h, H, 0, nullptr, nullptr, stream))
         return 1;
     StepIO io{cos, sin, position, active, nullptr};

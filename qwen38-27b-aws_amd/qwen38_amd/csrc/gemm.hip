@@ -2,8 +2,9 @@
 // 32 inputs (the reference's `FP8Linear`, qwen38_inf2/model.py:211-229; its MLP, model.py:250-259; its head,
 // model.py:890-900).
 //
-// Numerics. Weights stream from HBM as FP8 and are widened in registers to bf16 by v_cvt_scalef32_pk_bf16_fp8, exactly
-// (4 significant bits times a power of two); projection activations are e5m2 bytes (the reference rounds every
+// Numerics. Weights stream from HBM as FP8 e4m3 and are widened in registers to bf16 by v_cvt_scalef32_pk_bf16_fp8,
+// exactly (4 significant bits times a power of two); or, for the checkpoint's MXFP4 projections (W4), as E2M1 nibbles
+// widened by v_cvt_scalef32_pk_bf16_fp4 with the same E8M0 scales, also exactly (half the weight bytes); projection activations are e5m2 bytes (the reference rounds every
 // projection input to e5m2) widened exactly by v_cvt_scalef32_pk_bf16_bf8; the head's activations are bf16. Products
 // run on the bf16 MFMA, v_mfma_f32_32x32x16_bf16, whose float32 accumulation is as precise as a float32 dot product
 // (measured: about 1e-8 of sum |x w|). The FP8 MFMA accumulates internally to only about 2^-14 of that sum, and the
@@ -11,7 +12,7 @@
 // within a layer, so it is not used.
 //
 // Data movement. A workgroup owns a (WF*FR*32 features) x (WT*TR*32 tokens) output tile; every K-step of 64 inputs, its
-// weight tiles, their scales and its activation tiles go straight from global memory into one stage of an S-deep LDS
+// weight tiles (2 KiB of e4m3, or 1 KiB of E2M1 in the same element order), their scales and its activation tiles go straight from global memory into one stage of an S-deep LDS
 // ring (global_load_lds, no VGPR staging), S-1 K-steps ahead of the MFMAs. One barrier per K-step: the stage a wave
 // loads into is the one every wave finished reading before that barrier. Weight and activation tiles are both
 // MFMA-step-major (common.h), so every operand read is 8 (or 16) contiguous bytes per lane, free of bank conflicts.
@@ -79,18 +80,30 @@ __device__ __forceinline__ v8bf widen_e5m2(uint32_t x0, uint32_t x1) {
     return __builtin_bit_cast(v8bf, r);
 }
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI>
+// 8 E2M1 weights (one word, the first input in the lowest nibble) times 2^(scale byte - 127) as one bf16 MFMA operand.
+__device__ __forceinline__ v8bf widen_e2m1(uint32_t w, float scale) {
+    u4 r = {bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2)),
+            bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3))};
+    return __builtin_bit_cast(v8bf, r);
+}
+
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4>
 __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a) {
     constexpr int NW = WF * WT, NTH = NW * 64;
     constexpr int TT = WT * TR, FT = WF * FR;  // 32-token and 32-feature tiles per workgroup
     constexpr int AT = A8 ? 2048 : 4096;       // bytes of one activation tile (32 tokens x 64 inputs)
-    constexpr int ACT_B = TT * AT, W_B = FT * 2048, SC_B = FT * 64;
+    constexpr int WTB = W4 ? 1024 : 2048;      // bytes of one weight tile (32 features x 64 inputs)
+    constexpr int ACT_B = TT * AT, W_B = FT * WTB, SC_B = FT * 64;
     constexpr int STAGE = ACT_B + W_B + SC_B;
     constexpr int ACT_DMA = ACT_B >= NW * 1024 ? 16 : 4;  // bytes per lane of one activation load
-    constexpr int N_ACT = ACT_B / (NW * 64 * ACT_DMA), N_W = W_B / (NW * 1024), SC_CHUNKS = SC_B / 256;
+    constexpr int W_DMA = W_B >= NW * 1024 ? 16 : 4;      // bytes per lane of one weight load
+    constexpr int N_ACT = ACT_B / (NW * 64 * ACT_DMA), N_W = W_B / (NW * 64 * W_DMA), SC_CHUNKS = SC_B / 256;
     constexpr int OPS = N_ACT + N_W + 1;  // loads per wave per stage
     static_assert(N_ACT >= 1 && N_ACT * NW * 64 * ACT_DMA == ACT_B, "activation stage splits evenly over the waves");
-    static_assert(N_W >= 1 && N_W * NW * 1024 == W_B, "weight stage splits evenly over the waves");
+    static_assert(N_W >= 1 && N_W * NW * 64 * W_DMA == W_B && WTB % (64 * W_DMA) == 0,
+                  "weight stage splits evenly over the waves, each load inside one tile");
     static_assert(SC_CHUNKS >= 1 && NW % SC_CHUNKS == 0, "scale stage splits evenly over the waves");
     static_assert(OPS * (S - 2) <= 63 && S >= 2, "vmcnt range");
     static_assert(EPI != EPI_SWIGLU || FR == 2, "gate and up tiles pair up");
@@ -137,8 +150,8 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     const int n = u1 - u0;
     if (n <= 0) return;
 
-    // Loads of one stage. Each wave moves N_ACT activation chunks, N_W weight chunks of 1 KiB and one scale chunk of
-    // 256 bytes (waves with the same chunk index load identical bytes to the same place).
+    // Loads of one stage. Each wave moves N_ACT activation chunks, N_W weight chunks of 64 * W_DMA bytes and one scale
+    // chunk of 256 bytes (waves with the same chunk index load identical bytes to the same place).
     const uint8_t* act_base = (const uint8_t*)a.act + (size_t)tb * TT * KS * AT;
     const int sc_c = wave % SC_CHUNKS;
     const uint32_t sc_lane = (uint32_t)((lane >> 4) * KS * 64 + (lane & 15) * 4);
@@ -153,9 +166,9 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
         }
 #pragma unroll
         for (int j = 0; j < N_W; ++j) {
-            const int off = (j * NW + wave) * 1024;
-            const uint8_t* g = a.w + ((size_t)(fb * FT + off / 2048) * KS + k) * 2048 + off % 2048;
-            lds_load<16>(g + lane * 16, sb + ACT_B + off);
+            const int off = (j * NW + wave) * (64 * W_DMA);
+            const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS + k) * WTB + off % WTB;
+            lds_load<W_DMA>(g + lane * W_DMA, sb + ACT_B + off);
         }
         const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS + k) * 64;
         lds_load<4>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
@@ -171,11 +184,11 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                 for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.0f;
     };
 
-    // One K-step: per MFMA step m, each weight fragment and activation fragment is 8 contiguous bytes (16 for bf16
-    // activations) per lane.
+    // One K-step: per MFMA step m, each weight fragment is 8 contiguous bytes (4 for E2M1) per lane, each activation
+    // fragment 8 (16 for bf16 activations).
     auto compute = [&](int st) {
         const uint8_t* sb = lds + st * STAGE;
-        const uint8_t* wl = sb + ACT_B + (wf * FR) * 2048 + lane * 8;
+        const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * (WTB / 256);
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
         float scl[FR][2];  // 2^(scale byte - 127) of the K-step's two MX blocks (inputs 0-31, 32-63)
 #pragma unroll
@@ -191,8 +204,12 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             for (int f = 0; f < FR; ++f) {
                 // Steps 0-1 are inputs of the K-step's first MX block, steps 2-3 of its second.
                 const float scale = scl[f][m >> 1];
-                const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
-                wb[f] = widen_e4m3(r[0], r[1], scale);
+                if constexpr (W4) {
+                    wb[f] = widen_e2m1(*(const uint32_t*)(wl + f * 1024 + m * 256), scale);
+                } else {
+                    const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
+                    wb[f] = widen_e4m3(r[0], r[1], scale);
+                }
             }
 #pragma unroll
             for (int t = 0; t < TR; ++t) {
@@ -368,7 +385,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
 constexpr int MIN_UNITS = 8;  // smallest K range worth a stream-K group
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI>
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4>
 hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
     GemmArgs a = a0;
     constexpr int BF = WF * FR * 32, BT = WT * TR * 32, NTH = WF * WT * 64;
@@ -396,40 +413,40 @@ hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
         a.splits = 1;
     }
     if (splits_out) *splits_out = a.splits;
-    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI>), dim3(grid), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI, W4>), dim3(grid), dim3(NTH), 0, stream, a);
     return hipGetLastError();
 }
 
 // Tile shape: 256 tokens per workgroup from 256 tokens up (128 for bf16 outputs), Tpad tokens below. Features per workgroup: with e5m2
 // activations 128 when N / 128 is a multiple of 8 (an equal share of tiles per XCD; as fast per tile as 256 and twice
 // the tiles), else 256; with bf16 activations (the head) 256, and 512 below 256 tokens when N allows.
-template <bool A8, int EPI>
+template <bool A8, int EPI, bool W4>
 hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
     auto balanced = [&](int bf) { return a.N % bf == 0 && (a.N / bf) % 8 == 0; };
     if (a.Tpad % 256 == 0) {
         if constexpr (A8) {
             // bf16 outputs: 128 x 128 tiles, two token blocks per weight tile on one XCD (their stream-K ranges split
             // fewer tiles; measured 4-8 % faster on the 16384- and 14336-wide projections than 128 x 256).
-            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 5, EPI>(a, splits_out, stream);
-            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 5, EPI>(a, splits_out, stream);
-            return launch<4, 2, 2, 4, true, 4, EPI>(a, splits_out, stream);
+            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
+            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 5, EPI, W4>(a, splits_out, stream);
+            return launch<4, 2, 2, 4, true, 4, EPI, W4>(a, splits_out, stream);
         } else {
-            return launch<4, 2, 2, 4, false, 3, EPI>(a, splits_out, stream);
+            return launch<4, 2, 2, 4, false, 3, EPI, W4>(a, splits_out, stream);
         }
     }
     const bool wide = a.N % 512 == 0 && (balanced(512) || !balanced(256));
     switch (a.Tpad) {
         case 128:
-            return wide ? launch<8, 1, 2, 4, A8, 3, EPI>(a, splits_out, stream)
-                        : launch<4, 2, 2, 2, A8, 3, EPI>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 4, A8, 3, EPI, W4>(a, splits_out, stream)
+                        : launch<4, 2, 2, 2, A8, 3, EPI, W4>(a, splits_out, stream);
         case 64:
             if constexpr (A8)
-                if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI>(a, splits_out, stream);
-            return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI>(a, splits_out, stream)
-                        : launch<4, 2, 2, 1, A8, 4, EPI>(a, splits_out, stream);
+                if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4>(a, splits_out, stream)
+                        : launch<4, 2, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
         case 32:
-            return wide ? launch<8, 1, 2, 1, A8, 4, EPI>(a, splits_out, stream)
-                        : launch<4, 1, 2, 1, A8, 4, EPI>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream)
+                        : launch<4, 1, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
         default:
             return hipErrorInvalidValue;
     }
@@ -469,11 +486,19 @@ int q38_gemm_l2_local() {
 }
 
 hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream) {
+    if (a.w4) {
+        switch (epi) {
+            case EPI_BF16: return dispatch<true, EPI_BF16, true>(a, splits_out, stream);
+            case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, true>(a, splits_out, stream);
+            case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, true>(a, splits_out, stream);
+            default: return hipErrorInvalidValue;  // the head's weights are e4m3
+        }
+    }
     switch (epi) {
-        case EPI_BF16: return dispatch<true, EPI_BF16>(a, splits_out, stream);
-        case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU>(a, splits_out, stream);
-        case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL>(a, splits_out, stream);
-        case EPI_GROUPMAX: return dispatch<false, EPI_GROUPMAX>(a, splits_out, stream);
+        case EPI_BF16: return dispatch<true, EPI_BF16, false>(a, splits_out, stream);
+        case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, false>(a, splits_out, stream);
+        case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, false>(a, splits_out, stream);
+        case EPI_GROUPMAX: return dispatch<false, EPI_GROUPMAX, false>(a, splits_out, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -10,7 +10,7 @@ constexpr int GEMM_COUNTERS = 65536;   // stream-K arrival counters
 constexpr int GEMM_SLOT_FLOATS = 65536;  // floats of one stream-K partial (largest workgroup tile)
 
 struct GemmArgs {
-    const uint8_t* w;    // weight tiles [N/32][K/64][64][32] (e4m3)
+    const uint8_t* w;    // weight tiles [N/32][K/64][64][32] (e4m3), or with w4 [N/32][K/64][4][64][4] (E2M1 pairs)
     const uint8_t* ws;   // scales [N/32][K/64][32][2] (E8M0): row r's bytes for the K-step's two MX blocks
     const void* act;     // activation tiles [Tpad/32][K/64][4][64][8]: e5m2 bytes, or bf16 for EPI_GROUPMAX
     int K, N, T, Tpad;
@@ -27,6 +27,7 @@ struct GemmArgs {
     int splits_max;      // EPI_PARTIAL: at most this many splits (0: as many as fill the CUs)
     int l2_local;        // workgroup i runs on XCD i % 8 (q38_gemm_l2_local()): stream-K partials stay in L2
     int splits;          // EPI_PARTIAL split count (set by the launcher)
+    int w4;              // weight tiles hold MXFP4 (q38_pack_fp4) rather than e4m3
 };
 
 struct NormArgs {
@@ -198,6 +199,8 @@ hipError_t q38_accept(const int* picks, const int* drafts, const float* active, 
                       hipStream_t stream);
 hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, uint8_t* tiles, uint8_t* tile_scales,
                     hipStream_t stream);
+hipError_t q38_pack_fp4(const uint8_t* packed, const uint8_t* scales, int N, int K, uint8_t* tiles, uint8_t* tile_scales,
+                        hipStream_t stream);
 hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);
 hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
                            hipStream_t s);

@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
     "q38_kernel_timer",
 )
 
@@ -33,11 +33,14 @@ class Q38Config(ctypes.Structure):
         ("linear_key_head_dim", ctypes.c_int), ("linear_value_head_dim", ctypes.c_int),
         ("linear_conv_kernel_dim", ctypes.c_int), ("rms_norm_eps", ctypes.c_float),
         ("batch_size", ctypes.c_int), ("verify_tokens", ctypes.c_int), ("max_seq_len", ctypes.c_int), ("mtp", ctypes.c_int),
-        ("saved_states", ctypes.c_int), ("prefill_chunk", ctypes.c_int),
+        ("saved_states", ctypes.c_int), ("prefill_chunk", ctypes.c_int), ("weight_format", ctypes.c_int),
     ]
 
 
 _lib = None
+
+
+WEIGHT_FORMATS = {"e4m3": 0, "mxfp4": 1}
 
 
 def library() -> ctypes.CDLL:
@@ -59,7 +62,9 @@ def library() -> ctypes.CDLL:
     lib.q38_parity.argtypes = [p, ctypes.POINTER(i)]
     lib.q38_set_parity.argtypes = [p, i]
     lib.q38_pack_weight.argtypes = [p, p, i, i, p, p, p]
+    lib.q38_pack_weight_fp4.argtypes = [p, p, i, i, p, p, p]
     lib.q38_fp8_linear.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_mxfp4_linear.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_fp8_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_mlp_up.argtypes = [p, i, i, p, p, i, p, p, p]
@@ -103,7 +108,7 @@ def stream() -> int:
 
 
 def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                prefill_chunk: int = 0) -> Q38Config:
+                prefill_chunk: int = 0, weight_format: str = "e4m3") -> Q38Config:
     c = Q38Config()
     c.hidden_size, c.intermediate_size, c.vocab_size = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     if cfg.num_hidden_layers > MAX_LAYERS:
@@ -120,6 +125,7 @@ def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp:
     c.batch_size, c.verify_tokens, c.max_seq_len, c.mtp = batch, tokens, max_seq_len, int(mtp)
     c.saved_states = int(saved_states)
     c.prefill_chunk = prefill_chunk
+    c.weight_format = WEIGHT_FORMATS[weight_format]
     return c
 
 
@@ -127,9 +133,9 @@ class Handle:
     """One q38_handle: shapes fixed at creation, every buffer bound by the owner."""
 
     def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                 prefill_chunk: int = 0):
+                 prefill_chunk: int = 0, weight_format: str = "e4m3"):
         self.lib = library()
-        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk)
+        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format)
         h = ctypes.c_void_p()
         check(self.lib.q38_create(ctypes.byref(self.c), ctypes.byref(h)))
         self.h = h
@@ -207,6 +213,17 @@ def pack_weight(coded: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor
     return tiles, tile_scales
 
 
+def pack_weight_fp4(packed: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The checkpoint's MXFP4 (packed bytes [N, K/2], E8M0 bytes [N, K/32]) on the GPU -> (tiles, tile scales)."""
+    n, half = packed.shape
+    k = 2 * half
+    tiles = torch.empty(n * half, dtype=torch.uint8, device=packed.device)
+    tile_scales = torch.empty(n * k // 32, dtype=torch.uint8, device=packed.device)
+    check(library().q38_pack_weight_fp4(ptr(packed.contiguous()), ptr(scales.contiguous()), n, k, ptr(tiles), ptr(tile_scales),
+                                        stream()))
+    return tiles, tile_scales
+
+
 def linear_scratch(rows: int, k: int, device="cuda") -> torch.Tensor:
     """Zero-filled scratch for the standalone projections (input tiles, then the GEMM's counters and partials)."""
     return torch.zeros(library().q38_fp8_linear_scratch(rows, k), dtype=torch.uint8, device=device)
@@ -218,6 +235,15 @@ def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: in
     scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
     check(library().q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def mxfp4_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, scratch=None) -> torch.Tensor:
+    """The projection through a packed MXFP4 weight (`pack_weight_fp4`): bf16 x [rows, k] -> bf16 [rows, n]."""
+    rows, k = x.shape
+    scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
+    check(library().q38_mxfp4_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
     return out
 
 

@@ -42,13 +42,13 @@ class Engine:
     """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
 
     def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda",
-                 saved_states: bool = False, prefill_chunk: int = 0):
+                 saved_states: bool = False, prefill_chunk: int = 0, weight_format: str = "e4m3"):
         if not torch.cuda.is_available():
             raise RuntimeError("the verify path runs on the GPU only")
         self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
-        self.saved_states, self.prefill_chunk = saved_states, prefill_chunk
+        self.saved_states, self.prefill_chunk, self.weight_format = saved_states, prefill_chunk, weight_format
         self.device = torch.device(device)
-        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk)
+        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format)
         self.buffers: dict[tuple[str, int], torch.Tensor] = {}
         self.mtp_layer = cfg.num_hidden_layers
         self._bind_zeros("workspace", -1, torch.uint8)
@@ -90,7 +90,14 @@ class Engine:
     # ------------------------------------------------------------------------------------------------ weights
 
     def _fp8(self, name: str, layer: int, coded: torch.Tensor, scales: torch.Tensor) -> None:
-        tiles, scales_t = ext.pack_weight(coded.to(self.device), scales.to(self.device))
+        """A projection: (e4m3 bytes [N, K], E8M0 [N, K/32]); for a decoder layer of an "mxfp4" engine the checkpoint's
+        (packed E2M1 [N, K/2], E8M0 [N, K/32]) instead."""
+        if self.weight_format == "mxfp4" and 0 <= layer < self.cfg.num_hidden_layers:
+            if coded.shape[1] * 2 != scales.shape[1] * 32:
+                raise ValueError(f"{name} of layer {layer}: an mxfp4 engine takes packed E2M1 weights [N, K/2]")
+            tiles, scales_t = ext.pack_weight_fp4(coded.to(self.device), scales.to(self.device))
+        else:
+            tiles, scales_t = ext.pack_weight(coded.to(self.device), scales.to(self.device))
         self.bind(name + ".tiles", layer, tiles)
         self.bind(name + ".scales", layer, scales_t)
 

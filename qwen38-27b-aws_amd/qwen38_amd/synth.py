@@ -20,13 +20,13 @@ Distributions (plus the builder's choices where it says nothing, 
 from __future__ import annotations
 
 import zlib
-from collections.abc import Iterator
+from collections.abc import Iterable, Iterator
 from dataclasses import dataclass
 
 import torch
 
 from .config import FULL, LINEAR, TextConfig
-from .quant import quantize_e4m3
+from .quant import dequantize_e4m3, mxfp4_to_e4m3, quantize_e4m3, quantize_mxfp4
 
 
 @dataclass(frozen=True)
@@ -157,6 +157,31 @@ def make(spec: Spec, seed: int, device="cpu"):
 def make_all(specs: list[Spec], seed: int, device="cpu") -> Iterator[tuple[Spec, object]]:
     for spec in specs:
         yield spec, make(spec, seed, device)
+
+
+def to_mxfp4(weights: Iterable[tuple[str, object]]) -> Iterator[tuple[str, object]]:
+    """The same model as an MXFP4 checkpoint holds it: each decoder layer's projection requantized from its e4m3 values
+    to (packed E2M1 [N, K/2], E8M0 [N, K/32]); the MTP layer and the head, bf16 in such a checkpoint, stay e4m3."""
+    for name, value in weights:
+        if name.startswith("layers.") and isinstance(value, tuple):
+            coded, scales = value
+            n, k = coded.shape
+            packed = torch.empty(n, k // 2, dtype=torch.uint8, device=coded.device)
+            e8m0 = torch.empty_like(scales)
+            step = max(32, (1 << 24) // k)  # rows per slice: bounds the quantizer's [rows, K, 8] temporary
+            for first in range(0, n, step):
+                rows = slice(first, min(n, first + step))
+                packed[rows], e8m0[rows] = quantize_mxfp4(dequantize_e4m3(coded[rows], scales[rows]))
+            value = (packed, e8m0)
+        yield name, value
+
+
+def mxfp4_as_e4m3(weights: Iterable[tuple[str, object]]) -> Iterator[tuple[str, object]]:
+    """`to_mxfp4`'s model with its decoder-layer projections written back as e4m3 + E8M0, value for value (exact)."""
+    for name, value in weights:
+        if name.startswith("layers.") and isinstance(value, tuple):
+            value = mxfp4_to_e4m3(*value)
+        yield name, value
 
 
 # ----------------------------------------------------------------------------------------------- states
