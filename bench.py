@@ -8,7 +8,7 @@ the state advance. It runs as one library call, `q38_spec_step`, on torch's curr
 resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill] [--mxfp4]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill] [--mxfp4] [--kv-fp8]
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
@@ -34,6 +34,9 @@ on a 512-token chunk, x16.
 `--mxfp4` binds the 64 decoder layers' projections as MXFP4 (the checkpoint's E2M1 nibbles + E8M0 scales, read by the
 GEMMs directly: half the weight bytes of e4m3), the seeded e4m3 weights requantized; the MTP layer and the head stay
 e4m3, as an MXFP4 checkpoint holds them in bf16. The algorithmic bytes count the decoder weights at 4.25 bits.
+
+`--kv-fp8` keeps every attention layer's KV cache (the MTP layer's too) as e4m3 bytes with per-layer bf16 scales (the
+reference's kv_cache_format "fp8"): half the KV bytes; the synthetic caches are encoded with seeded scales.
 """
 
 from __future__ import annotations
@@ -66,7 +69,7 @@ def fp4_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * k // 32
 
 
-def algorithmic_bytes(cfg, batch: int, tokens: int, context: int, mxfp4: bool = False) -> dict:
+def algorithmic_bytes(cfg, batch: int, tokens: int, context: int, mxfp4: bool = False, kv8: bool = False) -> dict:
     """Compulsory HBM bytes of one step, each counted once: FP8 weights + E8M0 scales of every projection streamed,
     bf16 small weights, gated-delta state and conv state read + written, KV read over each row's context plus the
     step's own K/V written, the head read once per pass plus the recheck rows, the MTP layer per call, inputs/outputs."""
@@ -83,32 +86,44 @@ def algorithmic_bytes(cfg, batch: int, tokens: int, context: int, mxfp4: bool = 
     n_attn = cfg.num_hidden_layers - n_gdn
     weights = n_gdn * gdn_w + n_attn * attn_w
     state = n_gdn * batch * (hv * d * d * 2 * 2 + c * 3 * 2 * 2)
-    kv_read = batch * hkv * context * hd * 2 * 2
-    kv = n_attn * (kv_read + t * hkv * hd * 2 * 2)
+    kv_elem = 1 if kv8 else 2  # bytes per cached element
+    kv_read = batch * hkv * context * hd * 2 * kv_elem
+    kv = n_attn * (kv_read + t * hkv * hd * 2 * kv_elem)
     io = t * h * 2 * 2
     head_pass = fp8_bytes(v, h)
     head = 4 * head_pass + (t * 4 + 3 * batch) * 32 * (h + h // 32)
     mtp_w = fp8_bytes(h, 2 * h) + attn_w8
-    mtp = 3 * (mtp_w + kv_read + t * hkv * hd * 2 * 2 + 3 * t * h * 2)
+    mtp = 3 * (mtp_w + kv_read + t * hkv * hd * 2 * kv_elem + 3 * t * h * 2)
     total = weights + state + kv + io + head + mtp
     return {"total": total, "weights": weights, "state": state, "kv": kv, "head": head, "mtp": mtp, "io": io}
 
 
-def decode_bytes(cfg, batch: int, context: int, mxfp4: bool = False) -> int:
+def decode_bytes(cfg, batch: int, context: int, mxfp4: bool = False, kv8: bool = False) -> int:
     """Compulsory HBM bytes of one decode step (no head, no MTP): as `algorithmic_bytes` with one token per row."""
-    b = algorithmic_bytes(cfg, batch, 1, context, mxfp4)
+    b = algorithmic_bytes(cfg, batch, 1, context, mxfp4, kv8)
     return b["weights"] + b["state"] + b["kv"] + b["io"]
 
 
-def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, mxfp4: bool = False):
+def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, mxfp4: bool = False, kv8: bool = False):
     import torch
 
     from qwen38_amd import synth
     from qwen38_amd.generate import rope_table
+    from qwen38_amd.quant import encode_kv
     from qwen38_amd.steps import Engine
 
     dev = "cuda"
-    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev, weight_format="mxfp4" if mxfp4 else "e4m3")
+    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev, weight_format="mxfp4" if mxfp4 else "e4m3",
+                    kv_cache_format="fp8" if kv8 else "bf16")
+
+    def set_kv(layer, name):
+        kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, name, dev)
+        if kv8:
+            ks, vs = synth.kv_scales(cfg, seed, name, dev)
+            engine.set_kv_scales(layer, ks, vs)
+            kv = {"k_cache": encode_kv(kv["k_cache"], ks), "v_cache": encode_kv(kv["v_cache"], vs)}
+        engine.set_kv(layer, kv["k_cache"], kv["v_cache"])
+
     started = time.time()
     specs = synth.model_specs(cfg, mtp=True, head=True)
 
@@ -124,10 +139,8 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
         if kind == "linear_attention":
             engine.set_gdn(i, synth.gdn_states(cfg, batch, tokens, seed, f"state.{i}", dev))
         else:
-            kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, f"kv.{i}", dev)
-            engine.set_kv(i, kv["k_cache"], kv["v_cache"])
-    kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, "kv.mtp", dev)
-    engine.set_kv(engine.mtp_layer, kv["k_cache"], kv["v_cache"])
+            set_kv(i, f"kv.{i}")
+    set_kv(engine.mtp_layer, "kv.mtp")
     engine.bind("rope_table", -1, rope_table(cfg, max_seq_len))
     torch.cuda.synchronize()
     log(f"model and state ready in {time.time() - started:.0f}s")
@@ -283,7 +296,7 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
     end.synchronize()
     ms = start.elapsed_time(end) / args.steps
     log(f"decode: {ms:.3f} ms/step")
-    alg = decode_bytes(cfg, batch, context + args.warmup + args.steps // 2, args.mxfp4)
+    alg = decode_bytes(cfg, batch, context + args.warmup + args.steps // 2, args.mxfp4, args.kv_fp8)
     gbs = alg / (ms / 1000.0) / 1e9
     return {
         "metric": "decode tokens/s/GPU, 64-layer one-token step, batch 64",
@@ -298,7 +311,7 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
         "vs_baseline": None,
         "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
-        "config": {"workload": "27b-64L-b64-decode-ctx512" + ("-mxfp4" if args.mxfp4 else ""), "global_batch": batch, "tokens_per_row": 1, "context": context,
+        "config": {"workload": "27b-64L-b64-decode-ctx512" + variant(args), "global_batch": batch, "tokens_per_row": 1, "context": context,
                    "parallelism": "none (one GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": alg},
@@ -360,7 +373,11 @@ def prefill_main(args) -> dict:
 
     cfg = qwen38_27b_config(16)
     batch, chunk, n_chunks, max_seq_len = 64, 2048, 2, 4096 + 64
-    engine = Engine(cfg, batch, 4, max_seq_len, mtp=True, prefill_chunk=chunk, weight_format="mxfp4" if args.mxfp4 else "e4m3")
+    engine = Engine(cfg, batch, 4, max_seq_len, mtp=True, prefill_chunk=chunk, weight_format="mxfp4" if args.mxfp4 else "e4m3",
+                    kv_cache_format="fp8" if args.kv_fp8 else "bf16")
+    if args.kv_fp8:
+        for i in [i for i, kind in enumerate(cfg.layer_types) if kind == "full_attention"] + [engine.mtp_layer]:
+            engine.set_kv_scales(i, *synth.kv_scales(cfg, args.seed, f"kv.{i}", "cuda"))
     started = time.time()
     specs = synth.model_specs(cfg, mtp=True, head=True)
     weights = ((spec.name, synth.make(spec, args.seed, "cuda")) for spec in specs)
@@ -415,7 +432,7 @@ def prefill_main(args) -> dict:
         "vs_baseline": None,
         "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, a synthetic prompt",
-        "config": {"workload": "27b-64L-prefill-4096-chunk2048" + ("-mxfp4" if args.mxfp4 else ""), "global_batch": 1, "tokens_per_row": tokens, "context": 0,
+        "config": {"workload": "27b-64L-prefill-4096-chunk2048" + variant(args), "global_batch": 1, "tokens_per_row": tokens, "context": 0,
                    "parallelism": "none (one GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "flops_per_step": flops},
@@ -424,9 +441,14 @@ def prefill_main(args) -> dict:
 
 
 def weight_dtype(args) -> str:
+    kv = ", fp8 e4m3 KV cache" if args.kv_fp8 else ""
     if args.mxfp4:
-        return "mxfp4 (e2m1 + e8m0) decoder weights, fp8 e4m3 mtp/head weights, bf16 MFMA (fp32 accumulate)"
-    return "fp8 e4m3 weights, bf16 MFMA (fp32 accumulate)"
+        return "mxfp4 (e2m1 + e8m0) decoder weights, fp8 e4m3 mtp/head weights" + kv + ", bf16 MFMA (fp32 accumulate)"
+    return "fp8 e4m3 weights" + kv + ", bf16 MFMA (fp32 accumulate)"
+
+
+def variant(args) -> str:
+    return ("-mxfp4" if args.mxfp4 else "") + ("-kvfp8" if args.kv_fp8 else "")
 
 
 def main() -> int:
@@ -439,6 +461,7 @@ def main() -> int:
     ap.add_argument("--decode", action="store_true", help="time the one-token decode graph instead of the speculative step")
     ap.add_argument("--prefill", action="store_true", help="time the prefill form (one 4096-token prompt) instead")
     ap.add_argument("--mxfp4", action="store_true", help="decoder-layer projections as MXFP4 (half the weight bytes)")
+    ap.add_argument("--kv-fp8", action="store_true", help="KV caches as e4m3 bytes with per-layer scales")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -471,7 +494,7 @@ def main() -> int:
             result["cpu_baseline"] = cpu_prefill_baseline(qwen38_27b_config(1), 1024, 512, seed, 16)
         print(json.dumps(result), flush=True)
         return 0
-    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4)
+    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4, args.kv_fp8)
     if args.decode:
         result = decode_main(args, cfg, engine, batch, context, max_seq_len)
         if not args.no_cpu_baseline:
@@ -514,7 +537,7 @@ def main() -> int:
     log(f"gate/up GEMM inside the steps: {launches} launches, {kernel_ms * 1000:.1f} us each")
     flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
     achieved = flops / (kernel_ms / 1000.0) / 1e12
-    alg = algorithmic_bytes(cfg, batch, tokens, context, args.mxfp4)
+    alg = algorithmic_bytes(cfg, batch, tokens, context, args.mxfp4, args.kv_fp8)
     step_gbs = alg["total"] / (ms / 1000.0) / 1e9
     result = {
         "metric": "accepted tokens/s/GPU, 64-layer verify step, batch 64, 4 tokens; HBM GB/s %peak",
@@ -530,7 +553,7 @@ def main() -> int:
         "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
         "config": {
-            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)" + (" with MXFP4 decoder weights" if args.mxfp4 else ""),
+            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)" + variant(args),
             "global_batch": batch,
             "tokens_per_row": tokens,
             "context": context,

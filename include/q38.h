@@ -44,6 +44,8 @@ typedef struct q38_handle q38_handle;
 #define Q38_FULL 1
 #define Q38_WEIGHTS_E4M3 0  /* projections bound as q38_pack_weight tiles */
 #define Q38_WEIGHTS_MXFP4 1 /* decoder-layer projections bound as q38_pack_weight_fp4 tiles (MTP layer, head: e4m3) */
+#define Q38_KV_BF16 0
+#define Q38_KV_FP8 1 /* KV caches of e4m3 bytes of value / scale, clamped to +-240, with bf16 scales per layer */
 
 /* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
  * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
@@ -60,6 +62,7 @@ typedef struct q38_config {
     int saved_states; /* a saved recurrent and conv state per row, for q38_copy_states (reference saved_states) */
     int prefill_chunk; /* most tokens of one q38_prefill call (a multiple of 32; 0: no prefill workspace) */
     int weight_format; /* Q38_WEIGHTS_E4M3 or Q38_WEIGHTS_MXFP4 (the reference's weight_format, config.py:28-30) */
+    int kv_cache_format; /* Q38_KV_BF16 or Q38_KV_FP8 (the reference's kv_cache_format, config.py:33-34, model.py:557-601) */
 } q38_config;
 
 const char* q38_last_error(void);
@@ -87,7 +90,9 @@ void q38_destroy(q38_handle* h);
  *   linear_attn.conv_state bf16 [2][B][C][3], linear_attn.pending_key f32 [2][B][K][Hk][128],
  *   linear_attn.pending_delta f32 [2][B][K][Hv][128], linear_attn.pending_decay f32 [2][B][K][Hv],
  *   linear_attn.pending_input bf16 [2][B][K][C]: two halves, the current one given by q38_parity
- *   self_attn.k_cache bf16 [B][Hkv][S][hd]; self_attn.v_cache bf16 [B][Hkv][S/32][hd][32] (transposed per 32 positions)
+ *   self_attn.k_cache bf16 [B][Hkv][S][hd]; self_attn.v_cache bf16 [B][Hkv][S/32][hd][32] (transposed per 32 positions);
+ *   with kv_cache_format FP8 the same layouts of e4m3 bytes, and self_attn.k_scale, self_attn.v_scale (bf16 [1], the
+ *   checkpoint's static scales, reference checkpoint.py:227-233) among the layer's weights
  *   with saved_states: linear_attn.saved_state bf16 [B][Hv][128][128], linear_attn.saved_conv bf16 [B][C][3]
  * Scratch: workspace (model-wide; its GEMM counters are zeroed when it is bound). */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);

@@ -14,6 +14,11 @@ Pinning of each function (what fixes it besides this text):
   pins `gdn_prefill`, `chunked_gated_delta`, `unit_lower_inverse`, `attention_prefill`, `blocked_attention`,
   `_write_chunk`, `attention_cache_chunk`, `step_prefill` and `mtp_prefill` bit for bit (two chunks of one row, the
   second padded, and the MTP layer's prefill form).
+* tests/golden/kv8_tiny.safetensors, written by tests/golden/make_golden_kv8.py from the reference's CPU path with
+  kv_cache_format "fp8": pins `kv_store`, `kv_load`, `kv_round_trip` and the FP8-cache branches of
+  `attention_verify`, `attention_decode` and `attention_prefill` bit for bit (hidden states and cache bytes after two
+  verify steps, a decode step and a prefill chunk of one attention layer); tests/test_oracle.py also holds the e4m3
+  codec against its bit fields over every bf16 value.
 * invariants in tests/test_oracle.py: prefill then decode equals decoding every token (float32, reference
   tests/test_prefill.py:143-166); the chunked rule equals the recurrence in float64 with correlated keys and padding;
   `unit_lower_inverse` equals a dense inverse; blocked attention equals one softmax;
@@ -36,6 +41,9 @@ MASKED_SCORE = -1e4
 # (model.py:36).
 DELTA_CHUNK = 128
 ATTENTION_BLOCK = 2048
+# The FP8 KV cache's largest value: the reference clamps to NeuronCore-v2's finite e4m3 range before the cast to
+# e4m3fn (model.py:41, 581-585).
+FP8_KV_MAX = 240.0
 # The reference rounds every FP8 projection's input to e5m2 (model.py:85-87, 222-225). Tests that compare two float32
 # forms of the same computation switch it off, as reference tests/test_model_parity.py:255-260 does.
 ROUND_E5M2 = True
@@ -296,8 +304,33 @@ def _attention_project(cfg, w: dict, x, cos, sin):
     return query, key, value, gate.reshape(rows, tokens, cfg.num_attention_heads * head)
 
 
+def kv_store(t: torch.Tensor, scale) -> torch.Tensor:
+    """`FullAttentionStep._store` (model.py:579-585), CPU branch: what the cache holds for ``t``: itself (a bf16 cache,
+    ``scale`` None), or the e4m3 bytes of ``float32(t) / float32(scale)`` clamped to +-240."""
+    if scale is None:
+        return t
+    return (t.float() / scale.float()).clamp(-FP8_KV_MAX, FP8_KV_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def kv_load(t: torch.Tensor, scale, dtype: torch.dtype) -> torch.Tensor:
+    """`FullAttentionStep._load` (model.py:587-589): cached values back, ``dtype(e4m3 value * scale)`` for bytes."""
+    if scale is None:
+        return t
+    return (t.view(torch.float8_e4m3fn).to(dtype) * scale).to(dtype)
+
+
+def kv_round_trip(t: torch.Tensor, scale, dtype: torch.dtype) -> torch.Tensor:
+    """`FullAttentionStep._round_trip` (model.py:591-593): a step's own key or value as later steps will read it."""
+    return kv_load(kv_store(t, scale), scale, dtype)
+
+
+def kv_scales(st: dict):
+    """The layer's (k_scale, v_scale) for an FP8 cache (``st`` holding them), else (None, None)."""
+    return st.get("k_scale"), st.get("v_scale")
+
+
 def _write_both(st: dict, key, value, positions):
-    """`FullAttentionStep._write_both` (model.py:603-608) for a bf16 cache."""
+    """`FullAttentionStep._write_both` (model.py:603-608): ``key``/``value`` already in the cache's format."""
     rows, kv_heads, n, head = key.shape
     at = positions.reshape(rows, 1, n, 1).expand(-1, kv_heads, -1, head)
     st["k_cache"] = st["k_cache"].scatter(2, at, key)
@@ -305,8 +338,8 @@ def _write_both(st: dict, key, value, positions):
 
 
 def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active):
-    """`FullAttentionStep.verify` bf16-cache branch (model.py:641-672), tp 1. ``st`` holds ``k_cache``/``v_cache``
-    ``[B, Hkv, S, hd]``, replaced by the written caches."""
+    """`FullAttentionStep.verify` CPU branch (model.py:641-672), tp 1. ``st`` holds ``k_cache``/``v_cache``
+    ``[B, Hkv, S, hd]`` (bf16, or e4m3 bytes with ``k_scale``/``v_scale``), replaced by the written caches."""
     head = cfg.head_dim
     batch, tokens = x.shape[:2]
     max_seq_len = st["k_cache"].shape[2]
@@ -315,37 +348,39 @@ def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active):
     steps = torch.arange(tokens)
     where = torch.where(active.unsqueeze(-1) > 0.5, position.long().unsqueeze(-1) + steps, max_seq_len - tokens + steps)
     grouped = query.reshape(batch, cfg.num_key_value_heads, groups, tokens, head)
-    keys = st["k_cache"].unsqueeze(2)
-    values = st["v_cache"].unsqueeze(2)
+    ks, vs = kv_scales(st)
+    keys = kv_load(st["k_cache"], ks, x.dtype).unsqueeze(2)
+    values = kv_load(st["v_cache"], vs, x.dtype).unsqueeze(2)
     earlier = torch.arange(max_seq_len) < position.unsqueeze(-1)
     cached = torch.matmul(grouped, keys.transpose(-1, -2)).float() + torch.where(earlier, 0.0, MASKED_SCORE).reshape(batch, 1, 1, 1, -1)
-    own_key = key.unsqueeze(2)
-    own_value = value.unsqueeze(2)
+    own_key = kv_round_trip(key, ks, x.dtype).unsqueeze(2)
+    own_value = kv_round_trip(value, vs, x.dtype).unsqueeze(2)
     causal = steps.unsqueeze(0) <= steps.unsqueeze(-1)
     own = torch.matmul(grouped, own_key.transpose(-1, -2)).float() + torch.where(causal, 0.0, MASKED_SCORE)
     weights = torch.softmax(torch.cat((cached, own), dim=-1) * head**-0.5, dim=-1).to(x.dtype)
     out = torch.matmul(weights[..., :max_seq_len], values) + torch.matmul(weights[..., max_seq_len:], own_value)
     out = out.permute(0, 3, 1, 2, 4).reshape(batch, tokens, cfg.num_attention_heads * head)
-    _write_both(st, key, value, where)
+    _write_both(st, kv_store(key, ks), kv_store(value, vs), where)
     return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
 
 
 def attention_decode(cfg, w: dict, st: dict, x, cos, sin, position, active):
-    """`FullAttentionStep.forward` bf16-cache branch (model.py:610-639): one token per row."""
+    """`FullAttentionStep.forward` CPU branch (model.py:610-639): one token per row."""
     head = cfg.head_dim
     batch = x.shape[0]
     max_seq_len = st["k_cache"].shape[2]
     query, key, value, gate = _attention_project(cfg, w, x, cos, sin)
     grouped = query.reshape(batch, cfg.num_key_value_heads, cfg.num_key_value_groups, head)
     where = torch.where(active > 0.5, position.long(), max_seq_len - 1).unsqueeze(-1)
-    keys, values = st["k_cache"], st["v_cache"]
+    ks, vs = kv_scales(st)
+    keys, values = kv_load(st["k_cache"], ks, x.dtype), kv_load(st["v_cache"], vs, x.dtype)
     earlier = torch.arange(max_seq_len) < position.unsqueeze(-1)
     cached = torch.matmul(grouped, keys.transpose(2, 3)).float() + torch.where(earlier, 0.0, MASKED_SCORE).reshape(batch, 1, 1, -1)
-    own = torch.matmul(grouped, key.transpose(2, 3)).float()
+    own = torch.matmul(grouped, kv_round_trip(key, ks, x.dtype).transpose(2, 3)).float()
     weights = torch.softmax(torch.cat((cached, own), dim=-1) * head**-0.5, dim=-1).to(x.dtype)
-    out = torch.matmul(weights[..., :-1], values) + weights[..., -1:] * value
+    out = torch.matmul(weights[..., :-1], values) + weights[..., -1:] * kv_round_trip(value, vs, x.dtype)
     out = out.reshape(batch, 1, cfg.num_attention_heads * head)
-    _write_both(st, key, value, where)
+    _write_both(st, kv_store(key, ks), kv_store(value, vs), where)
     return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
 
 
@@ -537,8 +572,8 @@ def blocked_attention(query, keys, values, visible, block: int):
 
 
 def _write_chunk(st: dict, key, value, slot, start):
-    """`FullAttentionStep._write_chunk` (model.py:791-799) for a bf16 cache: row ``slot`` at ``start`` onward, every
-    other row at the cache's last ``L`` positions (junk, never read before overwritten)."""
+    """`FullAttentionStep._write_chunk` (model.py:791-799), ``key``/``value`` in the cache's format: row ``slot`` at
+    ``start`` onward, every other row at the cache's last ``L`` positions (junk, never read before overwritten)."""
     rows, max_seq_len = st["k_cache"].shape[0], st["k_cache"].shape[2]
     tokens = key.shape[2]
     positions = start.long() + torch.arange(tokens)
@@ -549,7 +584,7 @@ def _write_chunk(st: dict, key, value, slot, start):
 
 
 def attention_prefill(cfg, w: dict, st: dict, x, cos, sin, slot, start, n_valid):
-    """`FullAttentionStep.prefill` CPU branch with a bf16 cache (model.py:704-783): the chunk's queries against row
+    """`FullAttentionStep.prefill` CPU branch (model.py:704-783): the chunk's queries against row
     ``slot``'s cached positions before ``start`` and the chunk's own tokens causally, by `blocked_attention`; then the
     chunk's keys and values written (`_write_chunk`)."""
     head = cfg.head_dim
@@ -558,24 +593,27 @@ def attention_prefill(cfg, w: dict, st: dict, x, cos, sin, slot, start, n_valid)
     query, key, value, gate = _attention_project(cfg, w, x, cos, sin)
     groups = cfg.num_key_value_groups
     grouped = (query[0] * head**-0.5).reshape(cfg.num_key_value_heads, groups * tokens, head)
-    cache_keys = st["k_cache"].index_select(0, slot.long())[0]
-    cache_values = st["v_cache"].index_select(0, slot.long())[0]
+    ks, vs = kv_scales(st)
+    cache_keys = kv_load(st["k_cache"].index_select(0, slot.long())[0], ks, x.dtype)
+    cache_values = kv_load(st["v_cache"].index_select(0, slot.long())[0], vs, x.dtype)
     index = torch.arange(groups * tokens) % tokens
     visible = torch.cat(
         ((torch.arange(max_seq_len) < start).expand(groups * tokens, -1), torch.arange(tokens).unsqueeze(0) <= index.unsqueeze(-1)),
         dim=-1,
     )
-    out = blocked_attention(grouped, torch.cat((cache_keys, key[0]), dim=1), torch.cat((cache_values, value[0]), dim=1), visible,
-                            ATTENTION_BLOCK)
+    own_keys, own_values = kv_round_trip(key[0], ks, x.dtype), kv_round_trip(value[0], vs, x.dtype)
+    out = blocked_attention(grouped, torch.cat((cache_keys, own_keys), dim=1), torch.cat((cache_values, own_values), dim=1),
+                            visible, ATTENTION_BLOCK)
     out = out.to(x.dtype).reshape(cfg.num_attention_heads, tokens, head).transpose(0, 1).reshape(1, tokens, -1)
-    _write_chunk(st, key, value, slot, start)
+    _write_chunk(st, kv_store(key, ks), kv_store(value, vs), slot, start)
     return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
 
 
 def attention_cache_chunk(cfg, w: dict, st: dict, x, cos, sin, slot, start):
     """`FullAttentionStep.cache_chunk` (model.py:784-790): only the chunk's keys and values, written as prefill does."""
     _, key, value, _ = _attention_project(cfg, w, x, cos, sin)
-    _write_chunk(st, key, value, slot, start)
+    ks, vs = kv_scales(st)
+    _write_chunk(st, kv_store(key, ks), kv_store(value, vs), slot, start)
 
 
 # ----------------------------------------------------------------------------------------------- head and acceptance

@@ -22,8 +22,13 @@
 //       o_proj; then the step's keys and values into the cache. The weights differ from the reference's
 //       bf16(e^(s - M) / S) by a few float32 ulps before the bf16 rounding (the product of two exponentials).
 //
+// FP8 KV cache (KV8; the reference's kv_cache_format "fp8", model.py:557-601 with its CPU path's _store / _load /
+// _round_trip): the same layouts with one e4m3 byte of value / scale per element. Cached keys and values widen to
+// bf16(e4m3 x scale) in registers as they load; the step's own keys and values are used as they read back
+// (kv_round_trip) and written as bytes.
+//
 // Cache layout (this build's): K row-major [B][Hkv][S][256]; V transposed per block of 32 positions,
-// [B][Hkv][S/32][256][32], so both MFMA operands read 16 contiguous bytes per lane:
+// [B][Hkv][S/32][256][32], so both MFMA operands read 16 contiguous bytes per lane (8 with KV8):
 //   scores  v_mfma_f32_32x32x16_bf16, A = 32 keys x 16 dims, B = 16 dims x 32 query rows
 //   output  v_mfma_f32_32x32x16_bf16, A = 32 query rows x 16 positions (weights), B = 16 positions x 32 dims (V)
 // The cache loads of a workgroup are issued first, so their latency overlaps the row-statistics work; loads are issued
@@ -59,16 +64,28 @@ constexpr int SW = ATTN_CHUNK / 32;  // waves of the 1024-thread kernels: one bl
 
 // This wave's 32 keys of the cache, positions p0 .. p0 + 31: lane l holds key l % 32, dims 128 (l / 32) + 8m .. + 7
 // in kf[m].
+template <bool KV8>
 __device__ __forceinline__ void load_keys(const AttnArgs& a, size_t head, int p0, int lane, v8bf (&kf)[16]) {
-    const bf16_t* kp = a.k_cache + (head * a.S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
+    const size_t off = (head * a.S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
+    if constexpr (KV8) {
+        const uint8_t* kp = (const uint8_t*)a.k_cache + off;
+        uint2 r[16];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) kf[m] = load8(kp + m * 8);
+        for (int m = 0; m < 16; ++m) r[m] = *(const uint2*)(kp + m * 8);
+        const float sc = bf2f(*a.k_scale);
+#pragma unroll
+        for (int m = 0; m < 16; ++m) kf[m] = __builtin_bit_cast(v8bf, kv_widen8(r[m].x, r[m].y, sc));
+    } else {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) kf[m] = load8(a.k_cache + off + m * 8);
+    }
 }
 
 // q rows normed and rotated (bf16, qb; rows NQ .. QT*32 - 1 zero) and, with `own`, the step's keys normed and rotated
-// (bf16, kb) and values: to kv_own (float32, global) and/or vown (float32, LDS), where given. NWV waves; wave w takes
-// rows w, w + NWV, ...; lane l holds dims 4l .. 4l + 3. Loads are issued before any store.
-template <int QT, int NWV>
+// (bf16, kb) and values: to kv_own (float32, global) and/or vown (float32, LDS), where given; with KV8 the own keys
+// and values as they read back from the cache. NWV waves; wave w takes rows w, w + NWV, ...; lane l holds dims
+// 4l .. 4l + 3. Loads are issued before any store.
+template <int QT, int NWV, bool KV8>
 __device__ __forceinline__ void project_rows(const AttnArgs& a, int b, int kvh, int wave, int lane, bool own,
                                              bf16_t* qb, bf16_t* kb, float* kv_own, float (*vown)[256]) {
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K;
@@ -98,7 +115,8 @@ __device__ __forceinline__ void project_rows(const AttnArgs& a, int b, int kvh, 
             rs_[i] = *(const uint2*)(a.sin + ((size_t)b * K + t) * 64 + d0);
         }
     }
-    float qn_w[4], kn_w[4];
+    float qn_w[4], kn_w[4], ksc = 0.0f, vsc = 0.0f;
+    if (KV8 && own) ksc = bf2f(*a.k_scale), vsc = bf2f(*a.v_scale);
     unpack4(*(const uint2*)(a.q_norm + d0), qn_w);
     unpack4(*(const uint2*)(a.k_norm + d0), kn_w);
 
@@ -137,10 +155,16 @@ __device__ __forceinline__ void project_rows(const AttnArgs& a, int b, int kvh, 
             // rows of own keys and values exist only with `own`
         } else if (r < QT * 32 + K) {
             const int t = r - QT * 32;
+            if constexpr (KV8)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) out[e] = kv_round_trip(out[e], ksc);
             *(uint2*)(kb + t * QPITCH + d0) = pack4(out);
             if (kv_own) *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
         } else {
             const int t = r - QT * 32 - K;
+            if constexpr (KV8)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = kv_round_trip(v[i][e], vsc);
             if (kv_own) *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
             if (vown) *(v4f*)&vown[t][d0] = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
         }
@@ -201,7 +225,7 @@ __device__ __forceinline__ void own_scores(const bf16_t* qb, const bf16_t* kb, i
 // output. The softmax is complete inside the workgroup, so the weights are the reference's bf16(e^(s - M) / S) exactly;
 // they go through LDS to the weights x V product (v_mfma_f32_16x16x32_bf16: A = 16 query rows x 32 positions, B = 32
 // positions x 16 dims), one pass of 16 position blocks per nb.
-template <int QT, int NB>
+template <int QT, int NB, bool KV8>
 __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     constexpr int RT = QT * 2;                   // 16-row tiles of query rows
     constexpr int WPITCH = NB * ATTN_CHUNK + 8;  // bf16 per weight row in LDS (rows start 4 banks apart)
@@ -221,7 +245,7 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     const int dcol = wave * 16 + (lane & 15);  // output dim of this lane
 
     v8bf kf[16];
-    if (scored(0)) load_keys(a, head, wave * 32, lane, kf);
+    if (scored(0)) load_keys<KV8>(a, head, wave * 32, lane, kf);
     uint32_t gate[RT][4];  // gates of this lane's output rows rt*16 + 4 (l / 16) + i, dim dcol
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -230,7 +254,7 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
             const int q = min(rt * 16 + 4 * (lane >> 4) + i, NQ - 1);
             gate[rt][i] = a.qkv[(size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + dcol];
         }
-    project_rows<QT, SW>(a, b, kvh, wave, lane, true, qb, kb, nullptr, vown);
+    project_rows<QT, SW, KV8>(a, b, kvh, wave, lane, true, qb, kb, nullptr, vown);
     __syncthreads();
 
     v16f sacc[NB][QT];
@@ -241,7 +265,7 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
 #pragma unroll
     for (int nb = 1; nb < NB; ++nb)
         if (scored(nb)) {
-            load_keys(a, head, (nb * SW + wave) * 32, lane, kf);
+            load_keys<KV8>(a, head, (nb * SW + wave) * 32, lane, kf);
             score_block<QT>(kf, qb, lane, (nb * SW + wave) * 32, npos, sacc[nb], lmax);
         }
     if (wave == SW - 1) own_scores<QT>(qb, kb, lane, K, NQ, [&](int q, int tp, float v) { sown[q][tp] = v; });
@@ -251,10 +275,18 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     asm volatile("" ::: "memory");
     const int nblk = (npos + 31) >> 5;
     v8bf vf[SW];
-    const bf16_t* vp = a.v_cache + head * S * 256 + dcol * 32 + 8 * (lane >> 4);
+    uint2 vr[SW];  // KV8: the raw bytes, widened at their MFMA
+    const size_t voff = head * S * 256 + dcol * 32 + 8 * (lane >> 4);
+    const float vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
     auto load_v = [&](int nb) {
 #pragma unroll
-        for (int j = 0; j < SW; ++j) vf[j] = load8(vp + (size_t)max(min(nb * SW + j, nblk - 1), 0) * 8192);  // past nblk: unused
+        for (int j = 0; j < SW; ++j) {
+            const size_t off = voff + (size_t)max(min(nb * SW + j, nblk - 1), 0) * 8192;  // past nblk: unused
+            if constexpr (KV8)
+                vr[j] = *(const uint2*)((const uint8_t*)a.v_cache + off);
+            else
+                vf[j] = load8(a.v_cache + off);
+        }
     };
     load_v(0);
 
@@ -338,11 +370,17 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < SW; ++j)
-            if (nb * SW + j < nblk)
+            if (nb * SW + j < nblk) {
+                v8bf vj;
+                if constexpr (KV8)
+                    vj = __builtin_bit_cast(v8bf, kv_widen8(vr[j].x, vr[j].y, vsc));
+                else
+                    vj = vf[j];
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
                     acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        load8(wts + (rt * 16 + (lane & 15)) * WPITCH + (nb * SW + j) * 32 + 8 * (lane >> 4)), vf[j], acc[rt], 0, 0, 0);
+                        load8(wts + (rt * 16 + (lane & 15)) * WPITCH + (nb * SW + j) * 32 + 8 * (lane >> 4)), vj, acc[rt], 0, 0, 0);
+            }
     }
     const int act_k = a.Hq * 256;
 #pragma unroll
@@ -362,15 +400,22 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     // inactive rows write the tail.
     __syncthreads();
     const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
+    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f;
     for (int i = tid; i < K * 256; i += SW * 64) {
         const int t = i >> 8, d = i & 255, p = base + t;
         if (p < 0 || p >= S) continue;
-        a.k_cache[(head * S + p) * 256 + d] = kb[t * QPITCH + d];
-        a.v_cache[head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31)] = f2bf(vown[t][d]);
+        const size_t ko = (head * S + p) * 256 + d, vo = head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31);
+        if constexpr (KV8) {
+            ((uint8_t*)a.k_cache)[ko] = (uint8_t)kv_code(bf2f(kb[t * QPITCH + d]), ksc);
+            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vown[t][d], vsc);
+        } else {
+            a.k_cache[ko] = kb[t * QPITCH + d];
+            a.v_cache[vo] = f2bf(vown[t][d]);
+        }
     }
 }
 
-template <int QT>
+template <int QT, bool KV8>
 __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) {
     __shared__ __attribute__((aligned(16))) bf16_t qb[QT * 32 * QPITCH];
     __shared__ __attribute__((aligned(16))) bf16_t kb[ATTN_KMAX * QPITCH];  // own keys (chunk 0)
@@ -388,8 +433,8 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     const bool scored = blk * 32 < p_hi;
 
     v8bf kf[16];
-    if (scored) load_keys(a, head, blk * 32, lane, kf);
-    project_rows<QT, SW>(a, b, kvh, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
+    if (scored) load_keys<KV8>(a, head, blk * 32, lane, kf);
+    project_rows<QT, SW, KV8>(a, b, kvh, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
     __syncthreads();
 
     // The wave's block of scores, kept in registers; chunk 0's last wave also scores the own keys.
@@ -449,7 +494,7 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     }
 }
 
-template <int QT>
+template <int QT, bool KV8>
 __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
     constexpr int PF = QT == 1 ? 4 : 2;  // blocks of 32 positions whose loads one wave keeps in flight
     __shared__ float mx[QT * 32], inv[QT * 32];
@@ -477,12 +522,14 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
     const int dq = quarter * 64;
     const float* pr = a.probs + head * ATTN_QMAX * S;
     const float* cmax = a.stats + head * a.nchunks * ATTN_QMAX * 2;
-    const bf16_t* vc = a.v_cache + head * S * 256;
+    const size_t vc = head * S * 256;
+    const float vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
 
     // V and probability loads of the wave's first blocks (w, w + 4, ...). Lane l: V dims dq + 32 dt + l % 32, positions
     // 16 (l / 32) .. + 15 of the block; probabilities of query row l % 32 of each tile at the same positions, and that
     // row's chunk max.
     v8bf vf[PF][2][2];
+    uint4 vr[PF][2];  // KV8: the raw bytes, widened at their MFMAs
     v4f ef[PF][QT][4];
     float mc[PF][QT];
     auto issue = [&](int blk0) {
@@ -492,9 +539,13 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
             if (blk >= nblk) break;
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-                const bf16_t* vp = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
-                vf[j][dt][0] = load8(vp);
-                vf[j][dt][1] = load8(vp + 8);
+                const size_t vo = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
+                if constexpr (KV8) {
+                    vr[j][dt] = *(const uint4*)((const uint8_t*)a.v_cache + vo);
+                } else {
+                    vf[j][dt][0] = load8(a.v_cache + vo);
+                    vf[j][dt][1] = load8(a.v_cache + vo + 8);
+                }
             }
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
@@ -584,6 +635,12 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
                 const v8bf w1 = __builtin_bit_cast(v8bf, (u4t){wbits[4], wbits[5], wbits[6], wbits[7]});
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
+                    if constexpr (KV8) {
+                        if (qt == 0) {
+                            vf[j][dt][0] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].x, vr[j][dt].y, vsc));
+                            vf[j][dt][1] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].z, vr[j][dt].w, vsc));
+                        }
+                    }
                     acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, vf[j][dt][0], acc[qt][dt], 0, 0, 0);
                     acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, vf[j][dt][1], acc[qt][dt], 0, 0, 0);
                 }
@@ -628,21 +685,28 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
 
     // The step's own keys and values into the cache (model.py:603-608, 653-654); inactive rows write the tail.
     const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
+    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f;
     for (int i = tid; i < K * 64; i += 256) {
         const int t = i >> 6, d = dq + (i & 63), p = base + t;
         if (p < 0 || p >= S) continue;
-        a.k_cache[(head * S + p) * 256 + d] = f2bf(kq[t][i & 63]);
-        a.v_cache[head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31)] = f2bf(vq[t][i & 63]);
+        const size_t ko = (head * S + p) * 256 + d, vo = head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31);
+        if constexpr (KV8) {
+            ((uint8_t*)a.k_cache)[ko] = (uint8_t)kv_code(kq[t][i & 63], ksc);
+            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vq[t][i & 63], vsc);
+        } else {
+            a.k_cache[ko] = f2bf(kq[t][i & 63]);
+            a.v_cache[vo] = f2bf(vq[t][i & 63]);
+        }
     }
 }
 
-template <int QT, int NB>
+template <int QT, int NB, bool KV8>
 hipError_t launch_attn(AttnArgs a, hipStream_t stream) {
     a.fused_max = NB * ATTN_CHUNK;
-    hipLaunchKernelGGL((attn_fused_kernel<QT, NB>), dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+    hipLaunchKernelGGL((attn_fused_kernel<QT, NB, KV8>), dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
     if (a.S > a.fused_max) {
-        hipLaunchKernelGGL(attn_scores_kernel<QT>, dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
-        hipLaunchKernelGGL(attn_out_kernel<QT>, dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((attn_scores_kernel<QT, KV8>), dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
+        hipLaunchKernelGGL((attn_out_kernel<QT, KV8>), dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -653,5 +717,9 @@ hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream) {
     const int NQ = a.Hq / a.Hkv * a.K;
     if (NQ > ATTN_QMAX || a.K > ATTN_KMAX || (long)a.nchunks * ATTN_CHUNK < a.S) return hipErrorInvalidValue;
     // Two position blocks per wave need 66 KB of bf16 weights in LDS at 32 query rows; 64 rows keep one.
-    return NQ <= 32 ? launch_attn<1, 2>(a, stream) : launch_attn<2, 1>(a, stream);
+    if (a.kv8) {
+        if (!a.k_scale || !a.v_scale) return hipErrorInvalidValue;
+        return NQ <= 32 ? launch_attn<1, 2, true>(a, stream) : launch_attn<2, 1, true>(a, stream);
+    }
+    return NQ <= 32 ? launch_attn<1, 2, false>(a, stream) : launch_attn<2, 1, false>(a, stream);
 }

@@ -77,6 +77,35 @@ __device__ __forceinline__ uint32_t pk_e5m2(float a, float b, float c, float d) 
     return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, lo, true);
 }
 
+// FP8 KV cache: e4m3 bytes of value / scale with one bf16 scale per layer and K or V (reference model.py:579-593).
+// The cache byte of x: e4m3 (round to nearest even) of float32(x) / float32(scale), clamped to +-240 first.
+__device__ __forceinline__ uint32_t kv_code(float x, float scale) {
+    const float q = fminf(fmaxf(__fdiv_rn(x, scale), -240.0f), 240.0f);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false) & 0xffu;
+}
+
+// Two cached bytes (the low or high half of `word`) read back as bf16 (e4m3 value x scale), packed: the e4m3 x bf16
+// product is exact in float32 (4 x 8 significant bits), then rounded once to bf16.
+template <bool HIGH>
+__device__ __forceinline__ uint32_t kv_pk2(uint32_t word, float scale) {
+    typedef float v2f_ __attribute__((ext_vector_type(2)));
+    const v2f_ f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, HIGH);
+    return pk_bf16(f[0] * scale, f[1] * scale);
+}
+
+// Eight cached bytes as one bf16 MFMA operand.
+__device__ __forceinline__ v8bf16 kv_widen8(uint32_t lo, uint32_t hi, float scale) {
+    typedef uint32_t u4_ __attribute__((ext_vector_type(4)));
+    const u4_ r = {kv_pk2<false>(lo, scale), kv_pk2<true>(lo, scale), kv_pk2<false>(hi, scale), kv_pk2<true>(hi, scale)};
+    return __builtin_bit_cast(v8bf16, r);
+}
+
+// x as a later step reads it back from the cache. Encoding the result again gives kv_code(x) (the bf16 rounding moves
+// a value by at most 2^-9 relative, e4m3's rounding boundaries lie at least 2^-5 away), so kernels keep only this.
+__device__ __forceinline__ float kv_round_trip(float x, float scale) {
+    return lo_bf(kv_pk2<false>(kv_code(x, scale), scale));
+}
+
 __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);

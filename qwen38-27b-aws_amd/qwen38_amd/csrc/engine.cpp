@@ -159,7 +159,9 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     if ((r = fp8("self_attn.qkv", Hq * hd * 2 + 2 * Hkv * hd, H))) return r;
     if ((r = fp8("self_attn.o_proj", H, Hq * hd))) return r;
     if (name == "self_attn.q_norm" || name == "self_attn.k_norm") return hd * 2;
-    if (name == "self_attn.k_cache" || name == "self_attn.v_cache") return B * Hkv * S * hd * 2;
+    const bool kv8 = h->cfg.kv_cache_format == Q38_KV_FP8;
+    if (name == "self_attn.k_cache" || name == "self_attn.v_cache") return B * Hkv * S * hd * (kv8 ? 1 : 2);
+    if (kv8 && (name == "self_attn.k_scale" || name == "self_attn.v_scale")) return 2;
     if (layer == h->cfg.num_layers) {
         if ((r = fp8("mtp.fc", H, 2 * H))) return r;
         if (name == "mtp.embedding_norm" || name == "mtp.hidden_norm" || name == "mtp.norm") return H * 2;
@@ -378,6 +380,9 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         auto kn = get<uint16_t>(h, "self_attn.k_norm", li, &ok);
         auto kc = get<uint16_t>(h, "self_attn.k_cache", li, &ok);
         auto vc = get<uint16_t>(h, "self_attn.v_cache", li, &ok);
+        const bool kv8 = h->cfg.kv_cache_format == Q38_KV_FP8;
+        const uint16_t* ks = kv8 ? get<uint16_t>(h, "self_attn.k_scale", li, &ok) : nullptr;
+        const uint16_t* vs = kv8 ? get<uint16_t>(h, "self_attn.v_scale", li, &ok) : nullptr;
         otiles = get<uint8_t>(h, "self_attn.o_proj.tiles", li, &ok);
         oscales = get<uint8_t>(h, "self_attn.o_proj.scales", li, &ok);
         if (!ok) return 1;
@@ -402,6 +407,9 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
             p.sin = io.sin;
             p.k_cache = kc;
             p.v_cache = vc;
+            p.kv8 = kv8;
+            p.k_scale = ks;
+            p.v_scale = vs;
             p.qs = (uint16_t*)h->ws(h->off_pqs);
             p.act = act_mid;
             p.eps = h->cfg.rms_norm_eps;
@@ -425,6 +433,9 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         a.active = io.active;
         a.k_cache = kc;
         a.v_cache = vc;
+        a.kv8 = kv8;
+        a.k_scale = ks;
+        a.v_scale = vs;
         a.nchunks = h->attn_nchunks;
         a.probs = (float*)h->ws(h->off_scores);
         a.stats = (float*)h->ws(h->off_astats);
@@ -503,6 +514,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     if (c.max_seq_len % 32 || c.max_seq_len < 64) bad += "max_seq_len must be a multiple of 32; ";
     if (c.prefill_chunk < 0 || c.prefill_chunk % 32 || c.prefill_chunk > c.max_seq_len) bad += "prefill_chunk must be a multiple of 32 up to max_seq_len; ";
     if (c.weight_format != Q38_WEIGHTS_E4M3 && c.weight_format != Q38_WEIGHTS_MXFP4) bad += "unknown weight_format; ";
+    if (c.kv_cache_format != Q38_KV_BF16 && c.kv_cache_format != Q38_KV_FP8) bad += "unknown kv_cache_format; ";
     for (int i = 0; i < c.num_layers && i < Q38_MAX_LAYERS; ++i)
         if (c.layer_types[i] != Q38_LINEAR && c.layer_types[i] != Q38_FULL) bad += "unknown layer type; ";
     if (!bad.empty()) return fail(bad);
@@ -821,6 +833,9 @@ int q38_mtp_prefill(q38_handle* h, const uint16_t* hidden, const uint16_t* embed
     auto kn = get<uint16_t>(h, "self_attn.k_norm", M, &ok);
     auto kc = get<uint16_t>(h, "self_attn.k_cache", M, &ok);
     auto vc = get<uint16_t>(h, "self_attn.v_cache", M, &ok);
+    const bool kv8 = h->cfg.kv_cache_format == Q38_KV_FP8;
+    const uint16_t* ks = kv8 ? get<uint16_t>(h, "self_attn.k_scale", M, &ok) : nullptr;
+    const uint16_t* vs = kv8 ? get<uint16_t>(h, "self_attn.v_scale", M, &ok) : nullptr;
     if (!ok) return 1;
     TokensScope chunk(h, 1, tokens);
     uint8_t* act_h = h->ws(h->off_act_h);
@@ -858,6 +873,9 @@ int q38_mtp_prefill(q38_handle* h, const uint16_t* hidden, const uint16_t* embed
     p.sin = sin;
     p.k_cache = kc;
     p.v_cache = vc;
+    p.kv8 = kv8;
+    p.k_scale = ks;
+    p.v_scale = vs;
     p.eps = h->cfg.rms_norm_eps;
     p.keys_only = 1;
     HIP_TRY(q38_attn_prefill(p, stream));

@@ -127,6 +127,9 @@ struct PrefillAttnArgs {
     uint8_t* act;            // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
     int keys_only;
+    int kv8;                 // e4m3 caches with the layer's scales, as AttnArgs
+    const bf16_t* k_scale;
+    const bf16_t* v_scale;
 };
 
 #define ATTN_KMAX 8   // verify tokens
@@ -153,6 +156,9 @@ struct AttnArgs {
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
     int fused_max;          // set by the launcher: rows with at most this many visible positions take attn_fused
+    int kv8;                // the caches hold e4m3 bytes of value / scale (same layouts, one byte per element)
+    const bf16_t* k_scale;  // kv8: the layer's scales, bf16 [1] each
+    const bf16_t* v_scale;
 };
 
 struct PickArgs {

@@ -197,13 +197,16 @@ __device__ __forceinline__ int drow(int i, int lane) { return 8 * (i >> 2) + 4 *
 }  // namespace
 
 // Grid (token): wave w normalises and rotates rows w, w + 4, ...: query heads (scaled by 1/16 into qs), then the KV
-// heads' keys (into the cache) and values (into the cache, transposed per 32 positions). Lane l holds dims 4l .. 4l+3.
+// heads' keys (into the cache) and values (into the cache, transposed per 32 positions), as e4m3 bytes of value / scale
+// with KV8. Lane l holds dims 4l .. 4l+3.
+template <bool KV8>
 __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAttnArgs a) {
     const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int Hq = a.Hq, Hkv = a.Hkv, S = a.S, d0 = lane * 4;
     const int slot = *a.slot, p = *a.start + t;
     if (slot < 0 || slot >= a.rows) return;
     const int rows = a.keys_only ? 2 * Hkv : Hq + 2 * Hkv;
+    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f, vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
     float cs[4], sn[4];
     {
         const uint2 rc = *(const uint2*)(a.cos + (size_t)t * 64 + (d0 & 63));
@@ -220,9 +223,14 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAtt
         if (r >= Hq + Hkv) {  // a value: stored as is
             const int kvh = r - Hq - Hkv;
             if (p < S) {
-                bf16_t* vc = a.v_cache + (((size_t)slot * Hkv + kvh) * S + (p & ~31)) * 256 + (p & 31);
+                const size_t vo = (((size_t)slot * Hkv + kvh) * S + (p & ~31)) * 256 + (p & 31);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) vc[(size_t)(d0 + e) * 32] = f2bf(v[e]);
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (KV8)
+                        ((uint8_t*)a.v_cache)[vo + (size_t)(d0 + e) * 32] = (uint8_t)kv_code(v[e], vsc);
+                    else
+                        a.v_cache[vo + (size_t)(d0 + e) * 32] = f2bf(v[e]);
+                }
             }
             continue;
         }
@@ -243,8 +251,12 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAtt
                 make_uint2(pk_bf16(out[0] * 0.0625f, out[1] * 0.0625f), pk_bf16(out[2] * 0.0625f, out[3] * 0.0625f));
         } else if (p < S) {
             const int kvh = r - Hq;
-            *(uint2*)(a.k_cache + (((size_t)slot * Hkv + kvh) * S + p) * 256 + d0) =
-                make_uint2(pk_bf16(out[0], out[1]), pk_bf16(out[2], out[3]));
+            const size_t ko = (((size_t)slot * Hkv + kvh) * S + p) * 256 + d0;
+            if constexpr (KV8)
+                *(uint32_t*)((uint8_t*)a.k_cache + ko) = kv_code(out[0], ksc) | kv_code(out[1], ksc) << 8 |
+                                                         kv_code(out[2], ksc) << 16 | kv_code(out[3], ksc) << 24;
+            else
+                *(uint2*)(a.k_cache + ko) = make_uint2(pk_bf16(out[0], out[1]), pk_bf16(out[2], out[3]));
         }
     }
 }
@@ -252,7 +264,9 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAtt
 // Grid (tiles of 32 tokens, query head), one wave. Scores by v_mfma_f32_32x32x16_bf16 with the keys as A (32 positions)
 // and the queries as B (32 tokens): lane l holds token t0 + l % 32 and positions drow(i, l). The weights go straight
 // from those registers into the A operand of weights x V (two MFMA steps of 16 positions: rows drow(0..7) and
-// drow(8..15) of the lane), with V's B operand loaded in the same position order from the transposed cache.
+// drow(8..15) of the lane), with V's B operand loaded in the same position order from the transposed cache. With KV8
+// the cached bytes (the chunk's own included, written by the prep kernel) widen to bf16(e4m3 x scale) as they load.
+template <bool KV8>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs a) {
     __shared__ float so[32][256 + 4];  // output so far, [token][dim]
     __shared__ float s_scale[32];
@@ -262,6 +276,7 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs 
     if (start < 0 || start + L > S || slot < 0 || slot >= a.rows) return;  // the host checks these too
     const int tq = t0 + (lane & 31);  // this lane's token (query)
     const size_t head = (size_t)slot * a.Hkv + kvh;
+    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f, vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
 
     v8bf16 qf[16];
     {
@@ -274,10 +289,18 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs 
 
     // Scores of the 32 cached positions from p0 against the 32 tokens; visible(pos_index) decides the mask.
     auto score = [&](int p0, v16f& acc) {
-        const bf16_t* kp = a.k_cache + (head * S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
+        const size_t ko = (head * S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
         v8bf16 kf[16];
+        if constexpr (KV8) {
+            uint2 r[16];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) kf[m] = load8p(kp + m * 8);
+            for (int m = 0; m < 16; ++m) r[m] = *(const uint2*)((const uint8_t*)a.k_cache + ko + m * 8);
+#pragma unroll
+            for (int m = 0; m < 16; ++m) kf[m] = kv_widen8(r[m].x, r[m].y, ksc);
+        } else {
+#pragma unroll
+            for (int m = 0; m < 16; ++m) kf[m] = load8p(a.k_cache + ko + m * 8);
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
@@ -336,13 +359,19 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs 
                 const v8bf16 pa = __builtin_bit_cast(v8bf16, pw);
                 // Positions of this step in this lane: 16 ks + 4 (l / 32) + [0, 4) and 16 ks + 8 + 4 (l / 32) + [0, 4).
                 const int q0 = p0 + 16 * ks + 4 * (lane >> 5);
-                const bf16_t* vb = a.v_cache + (head * S + (q0 & ~31)) * 256 + (q0 & 31);
+                const size_t vb = (head * S + (q0 & ~31)) * 256 + (q0 & 31);
 #pragma unroll
                 for (int db = 0; db < 8; ++db) {
-                    const bf16_t* vp = vb + (size_t)(db * 32 + (lane & 31)) * 32;
-                    const uint2 lo = *(const uint2*)vp, hi = *(const uint2*)(vp + 8);
-                    const u4_ vw = {lo.x, lo.y, hi.x, hi.y};
-                    pv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, __builtin_bit_cast(v8bf16, vw), pv[db], 0, 0, 0);
+                    const size_t vo = vb + (size_t)(db * 32 + (lane & 31)) * 32;
+                    v8bf16 vw;
+                    if constexpr (KV8) {
+                        const uint8_t* vp = (const uint8_t*)a.v_cache + vo;
+                        vw = kv_widen8(*(const uint32_t*)vp, *(const uint32_t*)(vp + 8), vsc);
+                    } else {
+                        const uint2 lo = *(const uint2*)(a.v_cache + vo), hi = *(const uint2*)(a.v_cache + vo + 8);
+                        vw = __builtin_bit_cast(v8bf16, (u4_){lo.x, lo.y, hi.x, hi.y});
+                    }
+                    pv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, vw, pv[db], 0, 0, 0);
                 }
             }
         }
@@ -374,8 +403,14 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs 
 
 hipError_t q38_attn_prefill(const PrefillAttnArgs& a, hipStream_t stream) {
     if (a.L < 1 || a.L % 32 || a.Hq % a.Hkv || a.S % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_prefill_prep_kernel, dim3(a.L), dim3(256), 0, stream, a);
-    if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.L / 32, a.Hq), dim3(64), 0, stream, a);
+    if (a.kv8) {
+        if (!a.k_scale || !a.v_scale) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(attn_prefill_prep_kernel<true>, dim3(a.L), dim3(256), 0, stream, a);
+        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(a.L / 32, a.Hq), dim3(64), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(attn_prefill_prep_kernel<false>, dim3(a.L), dim3(256), 0, stream, a);
+        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(a.L / 32, a.Hq), dim3(64), 0, stream, a);
+    }
     return hipGetLastError();
 }
 

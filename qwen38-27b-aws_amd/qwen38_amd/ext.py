@@ -34,6 +34,7 @@ class Q38Config(ctypes.Structure):
         ("linear_conv_kernel_dim", ctypes.c_int), ("rms_norm_eps", ctypes.c_float),
         ("batch_size", ctypes.c_int), ("verify_tokens", ctypes.c_int), ("max_seq_len", ctypes.c_int), ("mtp", ctypes.c_int),
         ("saved_states", ctypes.c_int), ("prefill_chunk", ctypes.c_int), ("weight_format", ctypes.c_int),
+        ("kv_cache_format", ctypes.c_int),
     ]
 
 
@@ -41,6 +42,7 @@ _lib = None
 
 
 WEIGHT_FORMATS = {"e4m3": 0, "mxfp4": 1}
+KV_CACHE_FORMATS = {"bf16": 0, "fp8": 1}
 
 
 def library() -> ctypes.CDLL:
@@ -108,7 +110,7 @@ def stream() -> int:
 
 
 def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                prefill_chunk: int = 0, weight_format: str = "e4m3") -> Q38Config:
+                prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16") -> Q38Config:
     c = Q38Config()
     c.hidden_size, c.intermediate_size, c.vocab_size = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     if cfg.num_hidden_layers > MAX_LAYERS:
@@ -126,6 +128,7 @@ def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp:
     c.saved_states = int(saved_states)
     c.prefill_chunk = prefill_chunk
     c.weight_format = WEIGHT_FORMATS[weight_format]
+    c.kv_cache_format = KV_CACHE_FORMATS[kv_cache_format]
     return c
 
 
@@ -133,9 +136,9 @@ class Handle:
     """One q38_handle: shapes fixed at creation, every buffer bound by the owner."""
 
     def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                 prefill_chunk: int = 0, weight_format: str = "e4m3"):
+                 prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16"):
         self.lib = library()
-        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format)
+        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format, kv_cache_format)
         h = ctypes.c_void_p()
         check(self.lib.q38_create(ctypes.byref(self.c), ctypes.byref(h)))
         self.h = h

@@ -100,6 +100,21 @@ def mxfp4_to_e4m3(packed: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Ten
     return lut[nibbles.long()], scales.clone()
 
 
+# The FP8 KV cache's largest value (the reference clamps to NeuronCore-v2's finite e4m3 range, model.py:41).
+FP8_KV_MAX = 240.0
+
+
+def encode_kv(t: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """KV-cache bytes of ``t`` with the layer's bf16 scale: e4m3 of ``float32(t) / float32(scale)`` clamped to +-240
+    (the reference's `FullAttentionStep._store`, model.py:579-585), for preparing synthetic caches on the host."""
+    return (t.float() / scale.float()).clamp(-FP8_KV_MAX, FP8_KV_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def decode_kv(coded: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Cached values back: ``dtype(e4m3 value * scale)`` (model.py:587-589)."""
+    return (coded.view(torch.float8_e4m3fn).to(dtype) * scale.to(dtype)).to(dtype)
+
+
 def round_e5m2(x: torch.Tensor) -> torch.Tensor:
     """Round to FP8 e5m2 and back, as `model.fp8_round` does (model.py:85-87)."""
     return x.to(torch.float8_e5m2).to(x.dtype)

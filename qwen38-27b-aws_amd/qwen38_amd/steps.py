@@ -42,13 +42,16 @@ class Engine:
     """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
 
     def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda",
-                 saved_states: bool = False, prefill_chunk: int = 0, weight_format: str = "e4m3"):
+                 saved_states: bool = False, prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16"):
         if not torch.cuda.is_available():
             raise RuntimeError("the verify path runs on the GPU only")
         self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
         self.saved_states, self.prefill_chunk, self.weight_format = saved_states, prefill_chunk, weight_format
+        self.kv_cache_format = kv_cache_format
         self.device = torch.device(device)
-        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format)
+        self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format,
+                                 kv_cache_format)
+        kv_dtype = torch.uint8 if kv_cache_format == "fp8" else DTYPE
         self.buffers: dict[tuple[str, int], torch.Tensor] = {}
         self.mtp_layer = cfg.num_hidden_layers
         self._bind_zeros("workspace", -1, torch.uint8)
@@ -64,11 +67,11 @@ class Engine:
                     self._bind_zeros("linear_attn.saved_state", i, DTYPE)
                     self._bind_zeros("linear_attn.saved_conv", i, DTYPE)
             else:
-                self._bind_zeros("self_attn.k_cache", i, DTYPE)
-                self._bind_zeros("self_attn.v_cache", i, DTYPE)
+                self._bind_zeros("self_attn.k_cache", i, kv_dtype)
+                self._bind_zeros("self_attn.v_cache", i, kv_dtype)
         if mtp:
-            self._bind_zeros("self_attn.k_cache", self.mtp_layer, DTYPE)
-            self._bind_zeros("self_attn.v_cache", self.mtp_layer, DTYPE)
+            self._bind_zeros("self_attn.k_cache", self.mtp_layer, kv_dtype)
+            self._bind_zeros("self_attn.v_cache", self.mtp_layer, kv_dtype)
 
     # ------------------------------------------------------------------------------------------------ buffers
 
@@ -193,8 +196,14 @@ class Engine:
         vc = self.buffer("self_attn.v_cache", layer).view(b, cfg.num_key_value_heads, s // 32, cfg.head_dim, 32)
         return kc, vc
 
+    def set_kv_scales(self, layer: int, k_scale: torch.Tensor, v_scale: torch.Tensor) -> None:
+        """An FP8 cache's static scales for one attention layer (the MTP layer included): bf16 ``[1]`` each, the
+        reference's ``self_attn.k_scale`` / ``v_scale`` (model.py:559-561, checkpoint.py:227-233)."""
+        self.bind("self_attn.k_scale", layer, k_scale.reshape(1).to(DTYPE))
+        self.bind("self_attn.v_scale", layer, v_scale.reshape(1).to(DTYPE))
+
     def set_kv(self, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
-        """Write reference-layout caches [B,Hkv,S,hd]."""
+        """Write reference-layout caches [B,Hkv,S,hd] (bf16, or e4m3 bytes for an FP8 cache)."""
         kc, vc = self.kv_cache(layer)
         kc.copy_(k_cache)
         b, h, s, d = v_cache.shape

@@ -225,6 +225,15 @@ def kv_states(cfg: TextConfig, batch: int, max_seq_len: int, context, seed: int,
     return out
 
 
+def kv_scales(cfg: TextConfig, seed: int, name: str, device="cpu") -> tuple[torch.Tensor, torch.Tensor]:
+    """One attention layer's FP8 KV-cache scales (k_scale, v_scale), bf16 ``[1]`` each, as a checkpoint's calibrated
+    static scales (reference checkpoint.py:227-233): about 3 / 240, so unit-RMS keys and values use e4m3's range and the
+    largest few clamp."""
+    u = torch.rand(2, generator=_gen(seed, f"{name}.kv_scales", device), device=device)
+    s = (0.0125 * (1.0 + 0.5 * u)).to(torch.bfloat16)
+    return s[0:1].clone(), s[1:2].clone()
+
+
 def hidden_states(shape, seed: int, name: str, device="cpu") -> torch.Tensor:
     """Unit-RMS bf16 activations (e.g. a step's input embeddings or an MTP seed's hidden states)."""
     return _randn(shape, seed, name, device).to(torch.bfloat16)

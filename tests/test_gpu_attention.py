@@ -3,9 +3,10 @@
 The golden scenario's contexts are short; these cases spread each (row, KV head) over many chunks (the tiny block at
 2048 positions), take the one-launch path with one and with two blocks of 512 positions per wave, take the
 64-query-row path (16 query heads over 2 KV heads, 8 tokens), and include an empty cache and an inactive row (which
-writes the cache tail). Checked: the MTP output (one layer, so the north-star 2e-2 per-row bound without a floor
-factor), the positions the step writes in both caches (1e-2: the keys are normed and rotated in bf16 by both sides),
-and every other cache position unchanged.
+writes the cache tail), each with a bf16 cache and with an FP8 one (e4m3 bytes with the layer's scales). Checked: the
+MTP output (one layer, so the north-star 2e-2 per-row bound without a floor factor), the positions the step writes in
+both caches (1e-2 on the values they read back: the keys are normed and rotated in bf16 by both sides), and every
+other cache position unchanged.
 """
 
 from __future__ import annotations
@@ -19,6 +20,7 @@ from oracle import model as om
 from qwen38_amd import synth
 from qwen38_amd.config import tiny_config
 from qwen38_amd.generate import mtp_step_inputs
+from qwen38_amd.quant import decode_kv, encode_kv
 from qwen38_amd.steps import Engine, MTPStep
 from scenario import oracle_weights
 
@@ -42,17 +44,22 @@ def row_rel(got: torch.Tensor, want: torch.Tensor) -> float:
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
 @pytest.mark.parametrize("case", list(CASES))
-def test_mtp_attention_at_long_context_matches_the_oracle(gpu, case):
+def test_mtp_attention_at_long_context_matches_the_oracle(gpu, case, kv):
     hq, b, k, s, context, active = CASES[case]
-    print(f"case {case}", flush=True)
+    print(f"case {case} kv {kv}", flush=True)
     cfg = dataclasses.replace(tiny_config(1), num_attention_heads=hq)
     seed = 11
     values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg), seed))
     _, mtp_w, _ = oracle_weights(values, cfg)
-    engine = Engine(cfg, b, k, s, mtp=True)
+    engine = Engine(cfg, b, k, s, mtp=True, kv_cache_format=kv)
     engine.load(values.items())
     mst = synth.kv_states(cfg, b, s, context, seed, "mtp")
+    if kv == "fp8":
+        ks, vs = synth.kv_scales(cfg, seed, "mtp")
+        mst = {"k_cache": encode_kv(mst["k_cache"], ks), "v_cache": encode_kv(mst["v_cache"], vs), "k_scale": ks, "v_scale": vs}
+        engine.set_kv_scales(engine.mtp_layer, ks, vs)
     engine.set_kv(engine.mtp_layer, mst["k_cache"], mst["v_cache"])
     before = {key: v.clone() for key, v in mst.items()}
 
@@ -72,10 +79,11 @@ def test_mtp_attention_at_long_context_matches_the_oracle(gpu, case):
 
     kc, vc = engine.get_kv(engine.mtp_layer)
     for name, got in (("k_cache", kc.cpu()), ("v_cache", vc.cpu())):
+        read = (lambda t: decode_kv(t, mst[name[0] + "_scale"])) if kv == "fp8" else (lambda t: t)
         for row in range(b):
             start = context[row] if active[row] else s - k
             own = slice(start, start + k)
-            assert row_rel(got[row, :, own].transpose(0, 1), mst[name][row, :, own].transpose(0, 1)) <= 1e-2, (name, row)
+            assert row_rel(read(got[row, :, own]).transpose(0, 1), read(mst[name][row, :, own]).transpose(0, 1)) <= 1e-2, (name, row)
             keep = torch.ones(s, dtype=torch.bool)
             keep[own] = False
             assert torch.equal(got[row, :, keep], before[name][row, :, keep]), (name, row)

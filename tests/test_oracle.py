@@ -4,6 +4,7 @@ forms that a plausible mistake (a dropped term, a wrong index or sign, a transpo
 from __future__ import annotations
 
 import hashlib
+import sys
 import json
 import math
 
@@ -452,3 +453,70 @@ def test_mxfp4_codec_matches_the_references_decode_kat_and_converts_exactly_to_e
     assert torch.equal(dequantize_mxfp4(packed, back), values)
     coded, s8 = mxfp4_to_e4m3(codes, scales)
     assert torch.equal(dequantize_e4m3(coded, s8), values)
+
+
+def _kv8_layer():
+    """The FP8 KV golden scenario's single attention layer: config, weights, oracle state (cache bytes + scales)."""
+    import make_golden_kv8 as g8
+
+    cfg = g8.layer_config()
+    values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg), g8.SEED))
+    layers, _, _ = oracle_weights(values, cfg)
+    ks, vs, kc, vc = g8.initial_cache(cfg)
+    return g8, cfg, values, layers[0], {"k_cache": kc, "v_cache": vc, "k_scale": ks, "v_scale": vs}
+
+
+def test_oracle_fp8_kv_cache_matches_the_reference_bit_for_bit():
+    """tests/golden/kv8_tiny.*: one attention layer with an FP8 e4m3 cache and per-layer scales through two verify
+    steps, a decode step and a prefill chunk, from the reference's own CPU path: hidden states and cache bytes."""
+    sys.path.insert(0, str(GOLDEN))
+    g8, cfg, values, w, st = _kv8_layer()
+    gold = load_file(GOLDEN / "kv8_tiny.safetensors")
+    meta = json.loads((GOLDEN / "kv8_tiny.json").read_text())
+    verify_ids, decode_ids, prefill_ids, positions_2, decode_positions = g8.scenario(cfg)
+    assert positions_2 == meta["positions_2"] and decode_positions == meta["decode_positions"]
+    embed, b, k, s = values["embed_tokens"], meta["batch"], meta["tokens"], meta["max_seq_len"]
+    kind = "full_attention"
+
+    def check(name, h):
+        assert torch.equal(h, gold[name]), name
+        assert _digest(st["k_cache"]) == meta["cache_sha256"][name]["k_cache"], name
+        assert _digest(st["v_cache"]) == meta["cache_sha256"][name]["v_cache"], name
+
+    for n, (pos, acc) in enumerate(((meta["positions_1"], [0] * b), (positions_2, meta["accepted_2"]))):
+        vi = verify_inputs(cfg, pos, k, s, torch.bfloat16, meta["active"], acc)
+        h = om.decoder_layer(cfg, kind, w, st, embed[verify_ids[n]], vi["cos"], vi["sin"], vi["position"], vi["active"],
+                             accepted=vi["accepted"])
+        check(f"verify{n + 1}", h)
+    di = batch_step_inputs(cfg, decode_positions, s, torch.bfloat16, meta["active"])
+    h = om.decoder_layer(cfg, kind, w, st, embed[decode_ids].unsqueeze(1), di["cos"], di["sin"], di["position"], di["active"])
+    check("decode", h)
+    p = meta["prefill"]
+    pi = prefill_inputs(cfg, p["slot"], p["start"], p["n_valid"], p["chunk"], torch.bfloat16)
+    h = om.decoder_layer(cfg, kind, w, st, embed[prefill_ids].unsqueeze(0), pi["cos"], pi["sin"], None, None,
+                         slot=pi["slot"], start=pi["start"], n_valid=pi["n_valid"])
+    check("prefill", h)
+
+
+def test_fp8_kv_round_trip_reencodes_to_the_same_bytes():
+    """A cached value read back (bf16 of e4m3 x scale) encodes to the bytes it came from, for every bf16 value and
+    several scales: so a kernel may keep only the read-back value of a step's own key or value and encode that into
+    the cache. (The bf16 rounding moves a value by at most 2^-9 relative; e4m3's rounding boundaries are at least
+    2^-5 relative away from its values.)"""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits[torch.isfinite(bits.float())]
+    for scale in (0.0125, 0.0173, 0.5, 3.0, 1e-3):
+        s = torch.tensor([scale], dtype=torch.bfloat16)
+        coded = om.kv_store(x, s)
+        back = om.kv_load(coded, s, torch.bfloat16)
+        assert torch.equal(om.kv_store(back, s), coded), scale
+        # and the codec is the bit-field definition: clamp to +-240, round to nearest even e4m3
+        ref = om.e4m3_to_float(coded)
+        want = (x.float() / s.float()).clamp(-240, 240)
+        assert bool(((ref - want).abs() <= _e4m3_half_step(want) + 1e-30).all()), scale
+
+
+def _e4m3_half_step(v: torch.Tensor) -> torch.Tensor:
+    """Half the spacing of e4m3 values around |v| (subnormal spacing 2^-9)."""
+    e = torch.floor(torch.log2(v.abs().clamp_min(2.0**-6)))
+    return torch.pow(2.0, e - 3) / 2
