@@ -427,8 +427,8 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
         if constexpr (A8) {
             // bf16 outputs: 128 x 128 tiles, two token blocks per weight tile on one XCD (their stream-K ranges split
             // fewer tiles; measured 4-8 % faster on the 16384- and 14336-wide projections than 128 x 256).
-            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
-            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 5, EPI, W4>(a, splits_out, stream);
+            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 9, EPI, W4>(a, splits_out, stream);
+            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 6, EPI, W4>(a, splits_out, stream);
             return launch<4, 2, 2, 4, true, 4, EPI, W4>(a, splits_out, stream);
         } else {
             return launch<4, 2, 2, 4, false, 3, EPI, W4>(a, splits_out, stream);
