@@ -440,8 +440,14 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
             return wide ? launch<8, 1, 2, 4, A8, 3, EPI, W4>(a, splits_out, stream)
                         : launch<4, 2, 2, 2, A8, 3, EPI, W4>(a, splits_out, stream);
         case 64:
-            if constexpr (A8)
+            // Measured per epilogue at 64 tokens (the decode step's projections): bf16 outputs fastest as 128 x 64
+            // tiles with a deep ring (qkvz 32 against 50 us as 512 x 64), split-K partials as 128 x 64 with 5 stages,
+            // the SwiGLU pair as 256 x 64 (50.9 against 56.4 us as 128 x 64).
+            if constexpr (A8) {
+                if (EPI == EPI_BF16 && balanced(128)) return launch<2, 2, 2, 1, true, 8, EPI, W4>(a, splits_out, stream);
+                if (EPI == EPI_PARTIAL && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
                 if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
+            }
             return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4>(a, splits_out, stream)
                         : launch<4, 2, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
         case 32:
