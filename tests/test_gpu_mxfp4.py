@@ -111,3 +111,36 @@ def test_an_mxfp4_engine_steps_bit_for_bit_like_the_e4m3_engine(gpu):
                 assert same(a, c), i
     for a, c in zip(f4.get_kv(f4.mtp_layer), f8.get_kv(f8.mtp_layer)):
         assert same(a, c)
+
+
+@pytest.mark.gpu
+def test_engines_loaded_from_an_mxfp4_checkpoint_agree_bit_for_bit(gpu, tmp_path):
+    """A Hugging Face layout checkpoint (tests/test_checkpoint.py) read by qwen38_amd.checkpoint into an "mxfp4" engine
+    (the checkpoint's bytes) and an "e4m3" engine (converted on the host): the same verify and MTP outputs."""
+    from qwen38_amd import checkpoint as ckpt
+    from test_checkpoint import fake_model
+
+    cfg, _, _ = fake_model(tmp_path)
+    meta = golden_meta()
+    b, k, s = meta["batch"], meta["tokens"], meta["max_seq_len"]
+    states = tiny_states(cfg, meta, meta["seed"])
+    outs = []
+    for fmt in ("mxfp4", "e4m3"):
+        print(f"engine {fmt}", flush=True)
+        e = Engine(cfg, b, k, s, mtp=True, weight_format=fmt)
+        e.load(ckpt.model_weights(tmp_path, cfg, fmt))
+        for i, kind in enumerate(cfg.layer_types):
+            if kind == "linear_attention":
+                e.set_gdn(i, states[i])
+            else:
+                e.set_kv(i, states[i]["k_cache"], states[i]["v_cache"])
+        embed = e.buffer("embed_tokens", -1).view(cfg.vocab_size, cfg.hidden_size).cpu()
+        ids = golden_tensors()["ids"].long()
+        vi = verify_inputs(cfg, meta["positions_1"], k, s, torch.bfloat16, meta["active"], [0] * b)
+        h = VerifyStep(e)(inputs_embeds=embed[ids[0]], **vi)
+        mi = mtp_step_inputs(cfg, meta["positions_1"], k, s, torch.bfloat16, meta["active"])
+        m = MTPStep(e)(hidden=h, inputs_embeds=embed[ids[1]], **mi)
+        torch.cuda.synchronize()
+        outs.append((h.clone(), m.clone()))
+    assert same(outs[0][0], outs[1][0]) and same(outs[0][1], outs[1][1])
+    assert torch.isfinite(outs[0][0].float()).all()
