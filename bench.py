@@ -35,7 +35,8 @@ on a 512-token chunk, x16.
 GEMMs directly: half the weight bytes of e4m3), the seeded e4m3 weights requantized; the MTP layer and the head stay
 e4m3, as an MXFP4 checkpoint holds them in bf16. The algorithmic bytes count the decoder weights at 4.25 bits.
 
-`--kv-fp8` keeps every attention layer's KV cache (the MTP layer's too) as e4m3 bytes with per-layer bf16 scales (the
+`--context N` starts every row from N cached positions instead of 512 (for long-context runs of the verify and
+decode steps; run those with --no-cpu-baseline). `--kv-fp8` keeps every attention layer's KV cache (the MTP layer's too) as e4m3 bytes with per-layer bf16 scales (the
 reference's kv_cache_format "fp8"): half the KV bytes; the synthetic caches are encoded with seeded scales.
 """
 
@@ -311,7 +312,7 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
         "vs_baseline": None,
         "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
-        "config": {"workload": "27b-64L-b64-decode-ctx512" + variant(args), "global_batch": batch, "tokens_per_row": 1, "context": context,
+        "config": {"workload": f"27b-64L-b64-decode-ctx{context}" + variant(args).replace(f"-ctx{context}", ""), "global_batch": batch, "tokens_per_row": 1, "context": context,
                    "parallelism": "none (one GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": alg},
@@ -448,7 +449,8 @@ def weight_dtype(args) -> str:
 
 
 def variant(args) -> str:
-    return ("-mxfp4" if args.mxfp4 else "") + ("-kvfp8" if args.kv_fp8 else "")
+    ctx = f"-ctx{args.context}" if getattr(args, "context", 512) != 512 else ""
+    return ("-mxfp4" if args.mxfp4 else "") + ("-kvfp8" if args.kv_fp8 else "") + ctx
 
 
 def main() -> int:
@@ -461,6 +463,8 @@ def main() -> int:
     ap.add_argument("--decode", action="store_true", help="time the one-token decode graph instead of the speculative step")
     ap.add_argument("--prefill", action="store_true", help="time the prefill form (one 4096-token prompt) instead")
     ap.add_argument("--mxfp4", action="store_true", help="decoder-layer projections as MXFP4 (half the weight bytes)")
+    ap.add_argument("--context", type=int, default=512,
+                    help="cached positions per row before the timed steps (BASELINE's configs use 512)")
     ap.add_argument("--kv-fp8", action="store_true", help="KV caches as e4m3 bytes with per-layer scales")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
@@ -474,7 +478,9 @@ def main() -> int:
 
     from qwen38_amd.config import qwen38_27b_config
 
-    batch, tokens, context, max_seq_len, seed = 64, 4, 512, 1024, args.seed
+    batch, tokens, seed = 64, 4, args.seed
+    context = args.context
+    max_seq_len = max(1024, (context + 512 + 31) // 32 * 32)
     cfg = qwen38_27b_config(16)
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.copy_probe:
@@ -553,7 +559,8 @@ def main() -> int:
         "dtype": weight_dtype(args),
         "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
         "config": {
-            "workload": "27b-64L-b64-k4-ctx512-mtp-head (BASELINE config 2)" + variant(args),
+            "workload": (f"27b-64L-b64-k4-ctx{context}-mtp-head" + variant(args).replace(f"-ctx{context}", "")
+                         + (" (BASELINE config 2)" if context == 512 else "")),
             "global_batch": batch,
             "tokens_per_row": tokens,
             "context": context,
