@@ -581,9 +581,10 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_sp_at = take(Tv * 4);
     h->off_sp_draft = take(Tv * 4);
     h->off_gemm = take(gemm_scratch_bytes(h->cus));
-    // Split-K partials: up to GEMM_SPLIT_MAX splits at the verify width, 2 at a prefill chunk's (whose tiles alone
-    // fill the CUs); gemm() caps the splits at what fits.
-    h->part_floats = std::max((size_t)GEMM_SPLIT_MAX * Tv, 2 * Tc) * H;
+    // Split-K partials: up to GEMM_SPLIT_MAX splits at the verify width, 4 at a prefill chunk's (whose tiles
+    // outnumber the CUs: the split count is chosen so the last round of workgroups is full); gemm() caps the splits at
+    // what fits.
+    h->part_floats = std::max((size_t)GEMM_SPLIT_MAX * Tv, 4 * Tc) * H;
     h->off_part = take(h->part_floats * 4);
     if (Tc) {
         h->off_pqn = take(Tc * h->Hk * h->dk * 4);

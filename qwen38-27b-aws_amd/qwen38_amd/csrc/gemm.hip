@@ -394,7 +394,19 @@ hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
     int grid;
     if (EPI == EPI_PARTIAL) {
         int s = a.cus / (NF * NTB);
-        s = s < 1 ? 1 : s;
+        if (s < 1) {
+            // More tiles than CUs (prefill widths): the split count whose rounds of workgroups come out fullest, as
+            // K-steps per CU = ceil(tiles * s / cus) * KS / s (320 tiles on 256 CUs: 4 splits, 5 full rounds, instead
+            // of 1 split in 1.25 rounds); ties to fewer splits (less partial traffic).
+            const long tiles = (long)NF * NTB;
+            const int most = a.splits_max > 0 ? a.splits_max : 1;
+            s = 1;
+            double best = (double)((tiles + a.cus - 1) / a.cus);
+            for (int c = 2; c <= most && c <= 4 && c <= KS; ++c) {
+                const double cost = (double)((tiles * c + a.cus - 1) / a.cus) / c;
+                if (cost < best * 0.97) best = cost, s = c;
+            }
+        }
         s = s > GEMM_SPLIT_MAX ? GEMM_SPLIT_MAX : s;
         s = s > KS ? KS : s;
         if (a.splits_max > 0 && s > a.splits_max) s = a.splits_max;
