@@ -460,6 +460,7 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
                 if (EPI == EPI_PARTIAL && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
                 if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
             }
+            if constexpr (!A8) return launch<4, 2, 2, 1, false, 6, EPI, W4>(a, splits_out, stream);
             return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4>(a, splits_out, stream)
                         : launch<4, 2, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
         case 32:
