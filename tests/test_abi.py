@@ -53,3 +53,43 @@ def test_unsupported_shapes_and_names_are_refused():
     lib = ext.library()
     assert lib.q38_bind(h.h, b"linear_attn.recurrent_state", 0, ctypes.c_void_p(4096), 3) != 0
     assert b"needs" in lib.q38_last_error()
+
+
+def test_weight_and_kv_cache_formats_size_their_buffers():
+    cfg = tiny_config(1)  # layers 0-2 gated delta, 3 attention; MTP layer 4
+    e4, f4 = ext.Handle(cfg, 4, 4, 128, True), ext.Handle(cfg, 4, 4, 128, True, weight_format="mxfp4")
+    h, i = cfg.hidden_size, cfg.intermediate_size
+    assert e4.buffer_size("mlp.gate_up.tiles", 0) == 2 * i * h
+    assert f4.buffer_size("mlp.gate_up.tiles", 0) == i * h  # E2M1: half a byte per weight
+    assert f4.buffer_size("mlp.gate_up.scales", 0) == e4.buffer_size("mlp.gate_up.scales", 0)
+    assert f4.buffer_size("self_attn.o_proj.tiles", 3) * 2 == e4.buffer_size("self_attn.o_proj.tiles", 3)
+    # the MTP layer and the head stay e4m3 in an MXFP4 engine
+    assert f4.buffer_size("mtp.fc.tiles", 4) == e4.buffer_size("mtp.fc.tiles", 4)
+    assert f4.buffer_size("mlp.down.tiles", 4) == e4.buffer_size("mlp.down.tiles", 4)
+    assert f4.buffer_size("head.lm_head.tiles", -1) == e4.buffer_size("head.lm_head.tiles", -1)
+
+    kv8 = ext.Handle(cfg, 4, 4, 128, True, kv_cache_format="fp8")
+    assert kv8.buffer_size("self_attn.k_cache", 3) * 2 == e4.buffer_size("self_attn.k_cache", 3)
+    assert kv8.buffer_size("self_attn.v_cache", 4) * 2 == e4.buffer_size("self_attn.v_cache", 4)
+    assert kv8.buffer_size("self_attn.k_scale", 3) == 2 and kv8.buffer_size("self_attn.v_scale", 4) == 2
+    with pytest.raises(RuntimeError, match="no buffer"):
+        e4.buffer_size("self_attn.k_scale", 3)  # a bf16 cache has no scales
+
+    c = ext.make_config(cfg, 4, 4, 128, True)
+    lib, out = ext.library(), ctypes.c_void_p()
+    for field in ("weight_format", "kv_cache_format"):
+        bad = ext.make_config(cfg, 4, 4, 128, True)
+        setattr(bad, field, 2)
+        assert lib.q38_create(ctypes.byref(bad), ctypes.byref(out)) != 0
+        assert b"unknown " + field.encode() in lib.q38_last_error()
+    assert lib.q38_create(ctypes.byref(c), ctypes.byref(out)) == 0
+    lib.q38_destroy(out)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2 and "one GPU" in r.stderr
