@@ -1,9 +1,9 @@
 """Full attention at long contexts, through the MTP step (one fc + full-attention layer + norm) against the oracle.
 
 The golden scenario's contexts are short; these cases spread each (row, KV head) over many chunks (the tiny block at
-2048 positions), take the one-launch path with one and with two blocks of 512 positions per wave, take the
-64-query-row path (16 query heads over 2 KV heads, 8 tokens), and include an empty cache and an inactive row (which
-writes the cache tail), each with a bf16 cache and with an FP8 one (e4m3 bytes with the layer's scales). Checked: the
+2048 positions, with 4 tokens per row and with 1 as in decode), take the one-launch path with one and with two blocks
+of 512 positions per wave, take the 64-query-row path (16 query heads over 2 KV heads, 8 tokens), and include an
+empty cache and an inactive row (which writes the cache tail), each with a bf16 cache and with an FP8 one (e4m3 bytes with the layer's scales). Checked: the
 MTP output (one layer, so the north-star 2e-2 per-row bound without a floor factor), the positions the step writes in
 both caches (1e-2 on the values they read back: the keys are normed and rotated in bf16 by both sides), and every
 other cache position unchanged.
@@ -31,6 +31,8 @@ CASES = {
     "tail-edge": (8, 2, 4, 512, [507, 511], [True, False]),
     # contexts between one and two blocks of 512 positions per wave (the one-launch path up to 1024)
     "fused-two-blocks": (8, 4, 4, 1024, [1019, 513, 767, 1000], [True, True, True, False]),
+    # one token per row, as the decode step runs it, over many chunks
+    "one-token-2048": (8, 4, 1, 2048, [2000, 1025, 0, 600], [True, True, True, False]),
 }
 
 
