@@ -52,3 +52,62 @@ def tiny_states(cfg, meta, seed):
 
 def clone_states(states):
     return [{k: v.clone() for k, v in st.items()} for st in states]
+
+
+# Two tokens whose lm_head rows are +c*u and -c*u for one unit direction u: the model's picks and the MTP drafts then
+# mostly land on these two, so drafts match the model's picks about half the time and a speculative step accepts
+# 1..K tokens per row. With independent random rows a random-init model accepts no draft at all.
+STEER_TOKENS = (1000, 2000)
+STEER_SCALE = 50.0
+
+
+def steer_head(values: dict, cfg, seed: int) -> dict:
+    """``values`` with ``head.lm_head`` rows STEER_TOKENS replaced by +-STEER_SCALE * u (e4m3 + E8M0)."""
+    from qwen38_amd.quant import quantize_e4m3
+
+    g = torch.Generator().manual_seed(seed * 7919 + 17)
+    u = torch.randn(cfg.hidden_size, generator=g)
+    u = u / u.norm()
+    coded, scales = (t.clone() for t in values["head.lm_head"])
+    rc, rs = quantize_e4m3(torch.stack((STEER_SCALE * u, -STEER_SCALE * u)))
+    for i, token in enumerate(STEER_TOKENS):
+        coded[token], scales[token] = rc[i], rs[i]
+    out = dict(values)
+    out["head.lm_head"] = (coded, scales)
+    return out
+
+
+# The speculative-step scenario (tests/golden/make_golden_spec.py, tests/test_oracle_spec.py, tests/test_gpu_spec.py):
+# config 0 shapes, four slots of which three run, seeded as a prefill of prompts of 40, 64 and 1 tokens leaves them.
+SPEC = {"seed": 0, "batch": 4, "tokens": 4, "max_seq_len": 128, "chunk": 16, "prompt_lens": [40, 64, 1, None], "steps": 5}
+
+
+def spec_start(cfg, spec=SPEC):
+    """The starting rows: prompt ids plus the first new token, and the prompt's last hidden state, per running slot
+    (None for an empty slot)."""
+    g = torch.Generator().manual_seed(4321)
+    rows = []
+    for slot, n in enumerate(spec["prompt_lens"]):
+        if n is None:
+            rows.append(None)
+            continue
+        ids = torch.randint(0, cfg.vocab_size, (n + 1,), generator=g).tolist()
+        hidden = synth.hidden_states((1, cfg.hidden_size), spec["seed"], f"spec.seed.{slot}")
+        rows.append({"ids": ids, "prompt_len": n, "hidden": hidden})
+    return rows
+
+
+def spec_states(cfg, spec=SPEC):
+    """Decoder-layer states and the MTP layer's cache as a prefill of each prompt leaves them in shape: caches filled
+    below the prompt length (the MTP cache below the last MTP index), seeded gated-delta and conv states, empty
+    snapshots (the first verify step commits none of them)."""
+    b, k, s, seed = spec["batch"], spec["tokens"], spec["max_seq_len"], spec["seed"]
+    context = [n or 0 for n in spec["prompt_lens"]]
+    states = []
+    for i, kind in enumerate(cfg.layer_types):
+        if kind == "linear_attention":
+            states.append(synth.gdn_states(cfg, b, k, seed, f"spec.layers.{i}"))
+        else:
+            states.append(synth.kv_states(cfg, b, s, context, seed, f"spec.layers.{i}"))
+    mtp = synth.kv_states(cfg, b, s, [max(n - 1, 0) for n in context], seed, "spec.mtp")
+    return states, mtp
