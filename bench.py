@@ -109,7 +109,6 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
     import torch
 
     from qwen38_amd import synth
-    from qwen38_amd.generate import rope_table
     from qwen38_amd.quant import encode_kv
     from qwen38_amd.steps import Engine
 
@@ -142,7 +141,6 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
         else:
             set_kv(i, f"kv.{i}")
     set_kv(engine.mtp_layer, "kv.mtp")
-    engine.bind("rope_table", -1, rope_table(cfg, max_seq_len))
     torch.cuda.synchronize()
     log(f"model and state ready in {time.time() - started:.0f}s")
     g = torch.Generator(device=dev).manual_seed(seed)

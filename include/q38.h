@@ -94,7 +94,13 @@ void q38_destroy(q38_handle* h);
  *   with kv_cache_format FP8 the same layouts of e4m3 bytes, and self_attn.k_scale, self_attn.v_scale (bf16 [1], the
  *   checkpoint's static scales, reference checkpoint.py:227-233) among the layer's weights
  *   with saved_states: linear_attn.saved_state bf16 [B][Hv][128][128], linear_attn.saved_conv bf16 [B][C][3]
- * Scratch: workspace (model-wide; its GEMM counters are zeroed when it is bound). */
+ * Scratch: workspace (model-wide; its GEMM counters are zeroed when it is bound).
+ * Optional, per decoder layer: probe, which a q38_verify call fills when it is bound (size from q38_buffer_size): as
+ *   bf16 [B*K][.], the layer's normed input (gated-delta layers), the mixer's projection output (the gated-delta
+ *   in_proj_z part, Hv*128 wide; or the attention q|gate|k|v projection) and the residual stream after the mixer; then
+ *   the e5m2 activation tiles of the out_proj/o_proj input, the MLP input and the down projection's input, for the
+ *   first B*K tokens rounded up to 32. For stage-by-stage comparison with another implementation; unbound, nothing is
+ *   copied. */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
 int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
 

@@ -167,13 +167,16 @@ def _gdn_gates(w: dict, x: torch.Tensor):
     return beta, -w["linear_attn.A_log"].float().exp() * F.softplus(a + w["linear_attn.dt_bias"].float())
 
 
-def _gdn_finish(cfg, w: dict, out: torch.Tensor, z: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+def _gdn_finish(cfg, w: dict, out: torch.Tensor, z: torch.Tensor, dtype: torch.dtype, trace=None) -> torch.Tensor:
     """`GatedDeltaNetStep._finish` (model.py:339-345): gated RMS norm per value head (weight without 1+), then
-    out_proj. ``out``, ``z`` ``[tokens, v_heads, v_head]``."""
+    out_proj. ``out``, ``z`` ``[tokens, v_heads, v_head]``. ``trace`` (tests only) receives ``finish``, out_proj's input
+    before its e5m2 rounding."""
     h = out.float()
     h = h * torch.rsqrt((h * h).mean(-1, keepdim=True) + cfg.rms_norm_eps)
     h = w["linear_attn.norm_weight"] * h.to(dtype)
     h = (h * silu(z.float())).to(dtype)
+    if trace is not None:
+        trace["finish"] = h.reshape(out.shape[0], cfg.linear_value_dim)
     return linear_fp8(h.reshape(out.shape[0], 1, cfg.linear_value_dim), w["linear_attn.out_proj"])
 
 
@@ -184,13 +187,21 @@ def commit_and_read(state, scale, weighted, deltas, reads):
     return committed, reads.transpose(1, 2) @ committed.float()
 
 
-def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
+def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted, force=None, trace=None):
     """`GatedDeltaNetStep.verify` (model.py:376-454), tp 1. ``x`` ``[B, K, H]`` (the input norm's output).
 
     ``st`` holds ``recurrent_state [B,Hv,d,d]``, ``conv_state [B,C,3]``, ``pending_key_state [B,K,Hv,d]`` (f32),
     ``pending_delta_state [B,K,Hv,d]`` (f32), ``pending_decay_state [B,K,Hv]`` (f32), ``pending_input_state [B,K,C]``;
     the entries are replaced by their new values. Returns ``[B, K, H]``.
+
+    ``force`` and ``trace`` serve tests that compare another implementation stage by stage. ``force`` may hold that
+    implementation's ``qkv`` (the in_proj_qkv output ``[B, K, C]``), ``z`` (the in_proj_z output ``[B, K, Hv*d]``),
+    ``committed`` (the committed state
+    ``[B, Hv, d, d]``), ``log_decay`` (``[B, K, Hv]``) or ``delta`` (``[B, K, Hv, d]``), used in place of this function's
+    own values from that point on. ``trace``, a dict, receives the in-step quantities (``query``, ``key``, ``value``,
+    ``cumulative`` ``[B, K, Hv]``, ``query_state`` = q·S', ``key_state`` = k·S', ``beta``, ``delta``, ``out``).
     """
+    force = force or {}
     dtype = x.dtype
     batch, tokens = x.shape[:2]
     kernel = cfg.linear_conv_kernel_dim
@@ -209,7 +220,7 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
     history = torch.where(on.reshape(batch, 1, 1), history, st["conv_state"])
     st["conv_state"] = history
 
-    qkv = linear_fp8(x, w["linear_attn.in_proj_qkv"])
+    qkv = force["qkv"].to(dtype) if "qkv" in force else linear_fp8(x, w["linear_attn.in_proj_qkv"])
     window = torch.cat((history, qkv.transpose(1, 2)), dim=-1)
     conv_weight = w["linear_attn.conv_weight"]
     mixed = torch.stack([(window[:, :, t : t + kernel] * conv_weight).sum(dim=-1) for t in range(tokens)], dim=1)
@@ -217,21 +228,28 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
         part.reshape(batch, tokens, *part.shape[1:]) for part in _gdn_split(cfg, silu(mixed).reshape(batch * tokens, -1))
     )
     heads = cfg.linear_num_value_heads
-    z = linear_fp8(x, w["linear_attn.in_proj_z"]).reshape(batch * tokens, heads, -1)
+    z = force["z"].to(dtype) if "z" in force else linear_fp8(x, w["linear_attn.in_proj_z"])
+    z = z.reshape(batch * tokens, heads, -1)
     beta, log_decay = _gdn_gates(w, x.reshape(batch * tokens, -1))
     beta = beta.reshape(batch, tokens, -1) * active.reshape(batch, 1, 1)
     log_decay = log_decay.reshape(batch, tokens, -1) * active.reshape(batch, 1, 1)
+    if "log_decay" in force:
+        log_decay = force["log_decay"].float()
 
     state = st["recurrent_state"]
     k_head, v_head = state.shape[2:]
     pairs = batch * heads
+    reads = torch.cat((key, query), dim=1).permute(0, 2, 3, 1).reshape(pairs, k_head, 2 * tokens)
     committed, products = commit_and_read(
         state.reshape(pairs, k_head, v_head),
         scale.reshape(pairs, 1, 1).expand(-1, k_head, -1),
         torch.stack(weighted, dim=2).reshape(pairs, -1, k_head),
         st["pending_delta_state"].transpose(1, 2).reshape(pairs, -1, v_head),
-        torch.cat((key, query), dim=1).permute(0, 2, 3, 1).reshape(pairs, k_head, 2 * tokens),
+        reads,
     )
+    if "committed" in force:
+        committed = force["committed"].to(state.dtype).reshape(pairs, k_head, v_head)
+        products = reads.transpose(1, 2) @ committed.float()
     st["recurrent_state"] = committed.reshape(batch, heads, k_head, v_head)
     products = products.reshape(batch, heads, 2 * tokens, v_head).transpose(1, 2)
     key_state, query_state = products[:, :tokens], products[:, tokens:]
@@ -245,13 +263,16 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
         for s in range(t):
             coupling = (cumulative[t] - cumulative[s]).exp() * (key[:, t] * key[:, s]).sum(dim=-1)
             delta = delta - coupling.unsqueeze(-1) * deltas[s]
-        deltas.append(delta * beta[:, t].unsqueeze(-1))
+        deltas.append(force["delta"][:, t].float() if "delta" in force else delta * beta[:, t].unsqueeze(-1))
         out = cumulative[t].exp().unsqueeze(-1) * query_state[:, t]
         for s in range(t + 1):
             attend = (cumulative[t] - cumulative[s]).exp() * (query[:, t] * key[:, s]).sum(dim=-1)
             out = out + attend.unsqueeze(-1) * deltas[s]
         outs.append(out)
     delta, out = torch.stack(deltas, dim=1), torch.stack(outs, dim=1)
+    if trace is not None:
+        trace.update(query=query, key=key, value=value, cumulative=torch.stack(cumulative, dim=1), query_state=query_state,
+                     key_state=key_state, beta=beta, delta=delta, out=out)
     # The reference adds the commit kernel's zero output to order these writes after its reads (model.py:449-452);
     # adding 0.0 also turns -0.0 into +0.0, which the stored bits show.
     st["pending_key_state"] = key.float() + 0.0
@@ -259,7 +280,7 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted):
     st["pending_decay_state"] = log_decay.float() + 0.0
     st["pending_input_state"] = qkv + torch.zeros((), dtype=qkv.dtype)
     out = out.reshape(batch * tokens, heads, -1).to(dtype)
-    return _gdn_finish(cfg, w, out, z, dtype).reshape(batch, tokens, -1)
+    return _gdn_finish(cfg, w, out, z, dtype, trace).reshape(batch, tokens, -1)
 
 
 def gdn_decode(cfg, w: dict, st: dict, x, position, active):
@@ -337,9 +358,10 @@ def _write_both(st: dict, key, value, positions):
     st["v_cache"] = st["v_cache"].scatter(2, at, value)
 
 
-def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active):
+def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active, trace=None):
     """`FullAttentionStep.verify` CPU branch (model.py:641-672), tp 1. ``st`` holds ``k_cache``/``v_cache``
-    ``[B, Hkv, S, hd]`` (bf16, or e4m3 bytes with ``k_scale``/``v_scale``), replaced by the written caches."""
+    ``[B, Hkv, S, hd]`` (bf16, or e4m3 bytes with ``k_scale``/``v_scale``), replaced by the written caches. ``trace``
+    (tests only) receives ``finish``, o_proj's input before its e5m2 rounding."""
     head = cfg.head_dim
     batch, tokens = x.shape[:2]
     max_seq_len = st["k_cache"].shape[2]
@@ -361,7 +383,10 @@ def attention_verify(cfg, w: dict, st: dict, x, cos, sin, position, active):
     out = torch.matmul(weights[..., :max_seq_len], values) + torch.matmul(weights[..., max_seq_len:], own_value)
     out = out.permute(0, 3, 1, 2, 4).reshape(batch, tokens, cfg.num_attention_heads * head)
     _write_both(st, kv_store(key, ks), kv_store(value, vs), where)
-    return linear_fp8(out * torch.sigmoid(gate), w["self_attn.o_proj"])
+    gated = out * torch.sigmoid(gate)
+    if trace is not None:
+        trace["finish"] = gated.reshape(batch * tokens, -1)
+    return linear_fp8(gated, w["self_attn.o_proj"])
 
 
 def attention_decode(cfg, w: dict, st: dict, x, cos, sin, position, active):
@@ -388,9 +413,9 @@ def attention_decode(cfg, w: dict, st: dict, x, cos, sin, position, active):
 
 
 def decoder_layer(cfg, layer_type: str, w: dict, st: dict, x, cos, sin, position, active, accepted=None, slot=None,
-                  start=None, n_valid=None):
+                  start=None, n_valid=None, gdn_force=None, gdn_trace=None):
     """`DecoderLayer.forward` (model.py:918-930): verify when ``accepted`` is given, prefill when ``slot`` is, else
-    decode."""
+    decode. ``gdn_force`` / ``gdn_trace`` (tests only) go to `gdn_verify` as ``force`` / ``trace``."""
     eps = cfg.rms_norm_eps
     h = rms_norm(x, w["input_layernorm_weight"], eps)
     if slot is not None and accepted is None:
@@ -400,7 +425,7 @@ def decoder_layer(cfg, layer_type: str, w: dict, st: dict, x, cos, sin, position
             mixer = attention_prefill(cfg, w, st, h, cos, sin, slot, start, n_valid)
     elif layer_type == "linear_attention":
         if accepted is not None:
-            mixer = gdn_verify(cfg, w, st, h, position, active, accepted)
+            mixer = gdn_verify(cfg, w, st, h, position, active, accepted, gdn_force, gdn_trace)
         else:
             mixer = gdn_decode(cfg, w, st, h, position, active)
     else:

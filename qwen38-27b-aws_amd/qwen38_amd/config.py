@@ -2,11 +2,13 @@
 
 Differences from the reference, all because this build runs one GPU holding the whole model:
 * no `validate_tp` and no `tp_degree`: nothing is split across devices;
-* `weight_format` is always "fp8": FP8 e4m3 bytes with one E8M0 power-of-two scale per 32 input elements;
-* `recurrent_state_format` is always "bf16" and `kv_cache_format` always "bf16".
+* `weight_format` and `kv_cache_format` here are the reference's field values and only describe the reference's
+  numerics ("fp8": e5m2 activations into FP8 projections); the engine's own storage formats are chosen when it is built
+  (`steps.Engine(weight_format="e4m3" | "mxfp4", kv_cache_format="bf16" | "fp8")`);
+* `recurrent_state_format` is always "bf16".
 
-`verify_configs()` gives the workloads the benchmark and parity tests run (tiny block, one 27B block, the whole
-64-layer model, long context and high batch).
+`verify_configs()` gives BASELINE's five workloads: the parity tests run configs 0, 1, 3 and 4 one block deep
+(tests/test_gpu_layers.py) and `bench.py` measures config 2.
 """
 
 from __future__ import annotations

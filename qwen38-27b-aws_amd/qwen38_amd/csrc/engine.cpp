@@ -116,6 +116,37 @@ bool fp4_layer(const q38_handle* h, int layer) {
     return h->cfg.weight_format == Q38_WEIGHTS_MXFP4 && layer >= 0 && layer < h->cfg.num_layers;
 }
 
+// The optional per-layer probe a verify call fills when it is bound, for the step's T = B*K tokens: as bf16, the
+// layer's normed input [T][H] (gated-delta layers; left as it is for attention layers), the mixer's projection output
+// [T][P] (the gated-delta in_proj_z part, P = Hv*dk, or the attention q|gate|k|v projection, P = Hq*hd*2 + 2*Hkv*hd),
+// the gated-delta in-step output before its gated norm [T][Hv*dk] (gated-delta layers only), and the residual stream
+// after the mixer [T][H]; then, as the e5m2 activation tiles the GEMMs read (for the first T32 = T rounded up to 32
+// tokens), the out_proj input (M = Hv*dk or Hq*hd inputs), the MLP input (H) and the down projection's input (I). For
+// comparing the layer stage by stage against another implementation; a verify call with no probe bound does no extra
+// work.
+size_t probe_width(const q38_handle* h, int layer) {
+    return is_linear(h, layer) ? (size_t)h->Hv * h->dk : (size_t)h->Hq * h->hd * 2 + 2 * (size_t)h->Hkv * h->hd;
+}
+
+size_t probe_mid(const q38_handle* h, int layer) { return is_linear(h, layer) ? (size_t)h->Hv * h->dk : (size_t)h->Hq * h->hd; }
+
+size_t probe_inner(const q38_handle* h, int layer) { return is_linear(h, layer) ? (size_t)h->Hv * h->dk : 0; }
+
+size_t probe_tiles_at(const q38_handle* h, int layer) {
+    const size_t T = (size_t)h->cfg.batch_size * h->cfg.verify_tokens;
+    return T * (2 * (size_t)h->H + probe_width(h, layer) + probe_inner(h, layer)) * 2;
+}
+
+size_t probe_bytes(const q38_handle* h, int layer) {
+    const size_t T32 = ((size_t)h->cfg.batch_size * h->cfg.verify_tokens + 31) / 32 * 32;
+    return probe_tiles_at(h, layer) + T32 * (probe_mid(h, layer) + h->H + h->I);
+}
+
+uint16_t* probe_of(q38_handle* h, int layer) {
+    auto it = h->layer[layer].find("probe");
+    return it == h->layer[layer].end() ? nullptr : (uint16_t*)it->second.p;
+}
+
 // Expected size of a named buffer, or 0 if the name does not exist for that layer.
 size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     const size_t H = h->H, I = h->I, V = h->V, B = h->B, K = h->K, S = h->S;
@@ -137,6 +168,7 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     if (layer < 0 || layer > h->cfg.num_layers) return 0;
     if (layer == h->cfg.num_layers && !h->cfg.mtp) return 0;
     if (name == "input_layernorm" || name == "post_attention_layernorm") return H * 2;
+    if (name == "probe" && layer < h->cfg.num_layers) return probe_bytes(h, layer);
     if ((r = fp8("mlp.gate_up", 2 * I, H))) return r;
     if ((r = fp8("mlp.down", H, I))) return r;
     if (is_linear(h, layer)) {
@@ -265,6 +297,7 @@ struct TokensScope {
 int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream_t stream) {
     bool ok = true;
     const int H = h->H;
+    uint16_t* probe = li < h->cfg.num_layers ? probe_of(h, li) : nullptr;
     uint8_t* act_h = h->ws(h->off_act_h);
     uint8_t* act_mid = h->ws(h->off_act_mid);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
@@ -296,6 +329,10 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         uint16_t* qkv_out = io.decode || io.slot ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
         if (gemm(h, li, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
             return 1;
+        if (probe && !io.decode && !io.slot) {
+            HIP_TRY(hipMemcpyAsync(probe, h->ws(h->off_hbf), (size_t)h->T * H * 2, hipMemcpyDeviceToDevice, stream));
+            HIP_TRY(hipMemcpyAsync(probe + (size_t)h->T * H, z, (size_t)h->T * h->Hv * h->dk * 2, hipMemcpyDeviceToDevice, stream));
+        }
         GatesArgs ga{};
         ga.x = (const bf16_t*)h->ws(h->off_hbf);
         ga.wb = wb;
@@ -370,6 +407,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         g.decay_new = pdecay + wr * decayn;
         g.act = act_mid;
         g.eps = h->cfg.rms_norm_eps;
+        g.out_probe = probe && !io.decode ? (bf16_t*)probe + (size_t)h->T * (H + h->Hv * h->dk) : nullptr;
         HIP_TRY(io.decode ? q38_gdn_decode(g, stream) : q38_gdn_verify(g, stream));
         kmid = h->Hv * h->dk;
         }
@@ -389,6 +427,8 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         const int nqkv = h->Hq * h->hd * 2 + 2 * h->Hkv * h->hd;
         uint16_t* qkv = (uint16_t*)h->ws(h->off_qkv);
         if (gemm(h, li, qkv_t, qkv_s, act_h, H, nqkv, EPI_BF16, qkv, nqkv, nqkv, nullptr, 0, stream)) return 1;
+        if (probe && !io.decode && !io.slot)
+            HIP_TRY(hipMemcpyAsync(probe + (size_t)h->T * H, qkv, (size_t)h->T * nqkv * 2, hipMemcpyDeviceToDevice, stream));
         if (io.slot) {
             PrefillAttnArgs p{};
             p.L = h->T;
@@ -447,11 +487,18 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         kmid = h->Hq * h->hd;
     }
 out_proj:
+    if (probe && !io.decode && !io.slot)
+        HIP_TRY(hipMemcpyAsync((uint8_t*)probe + probe_tiles_at(h, li), act_mid, (size_t)(h->T + 31) / 32 * 32 * kmid,
+                               hipMemcpyDeviceToDevice, stream));
     // x += o_proj(mixer): split-K partials, then residual add and the post-mixer norm in one row kernel.
     if (gemm(h, li, otiles, oscales, act_mid, kmid, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     auto post = get<uint16_t>(h, "post_attention_layernorm", li, &ok);
     if (!ok) return 1;
-    return norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, x, x, post, act_h, H, 0, nullptr, nullptr, stream);
+    if (norm_rows(h, (const float*)h->ws(h->off_part), splits, nullptr, x, x, post, act_h, H, 0, nullptr, nullptr, stream)) return 1;
+    if (probe && !io.decode && !io.slot)
+        HIP_TRY(hipMemcpyAsync(probe + (size_t)h->T * (H + probe_width(h, li) + probe_inner(h, li)), x, (size_t)h->T * H * 2,
+                               hipMemcpyDeviceToDevice, stream));
+    return 0;
 }
 
 // MLP of layer `li` on act_h, then the residual; `next` is the following layer (its input norm is fused), or -1 for
@@ -471,6 +518,12 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     if (timed) HIP_TRY(hipEventRecord(timed[0], stream));
     if (gemm(h, li, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
     if (timed) HIP_TRY(hipEventRecord(timed[1], stream));
+    uint8_t* probe = li < h->cfg.num_layers && h->T == h->cfg.batch_size * h->cfg.verify_tokens ? (uint8_t*)probe_of(h, li) : nullptr;
+    if (probe) {
+        const size_t t32 = (size_t)(h->T + 31) / 32 * 32, at = probe_tiles_at(h, li) + t32 * probe_mid(h, li);
+        HIP_TRY(hipMemcpyAsync(probe + at, act_h, t32 * H, hipMemcpyDeviceToDevice, stream));
+        HIP_TRY(hipMemcpyAsync(probe + at + t32 * H, act_ffn, t32 * I, hipMemcpyDeviceToDevice, stream));
+    }
     int splits = 0;
     if (gemm(h, li, dn_t, dn_s, act_ffn, I, H, EPI_PARTIAL, nullptr, 0, 0, nullptr, 0, stream, &splits)) return 1;
     const float* part = (const float*)h->ws(h->off_part);

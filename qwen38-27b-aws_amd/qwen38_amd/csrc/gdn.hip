@@ -373,6 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
 #pragma unroll
             for (int s = 0; s <= t; ++s) out = out + (expf(cum[t] - cum[s]) * qk[t][s]) * dl[s];
             ob[t][j] = rbf(out);
+            if (a.out_probe) a.out_probe[((size_t)b * K + t) * Hv * D + h * D + j] = f2bf(ob[t][j]);
             a.delta_new[(((size_t)b * K + t) * Hv + h) * D + j] = dl[t];
             if (owner) a.key_new[(((size_t)b * K + t) * Hk + kh) * D + j] = kn[t][j] + 0.0f;
         }

@@ -79,6 +79,7 @@ struct GdnArgs {
     float* decay_new;
     uint8_t* act;            // e5m2 activation tiles of width Hv*128 for out_proj
     float eps;
+    bf16_t* out_probe;       // optional [B*K][Hv*128]: the in-step output o (bf16) before the gated norm
 };
 
 // Gated delta net over one prefill chunk of one row (prefill.hip).

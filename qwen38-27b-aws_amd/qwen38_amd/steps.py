@@ -72,6 +72,10 @@ class Engine:
         if mtp:
             self._bind_zeros("self_attn.k_cache", self.mtp_layer, kv_dtype)
             self._bind_zeros("self_attn.v_cache", self.mtp_layer, kv_dtype)
+            # cos/sin of every position, which the on-device speculative step gathers by the positions it computes.
+            from .generate import rope_table
+
+            self.bind("rope_table", -1, rope_table(cfg, max_seq_len))
 
     # ------------------------------------------------------------------------------------------------ buffers
 
@@ -189,6 +193,34 @@ class Engine:
             "pending_input_state": get("pending_input").view(2, b, k, c)[half],
         }
 
+    def enable_probe(self, layer: int) -> None:
+        """Bind layer ``layer``'s optional probe: later verify calls copy the layer's intermediate activations into it
+        (include/q38.h), read back with `probe`."""
+        self._bind_zeros("probe", layer, torch.uint8)
+
+    def probe(self, layer: int) -> dict:
+        """The last verify call's intermediates of layer ``layer``, for ``T = B*K`` tokens: ``normed`` [T, H] (gated-delta
+        layers), ``projection`` [T, P] (in_proj_z, or the attention q|gate|k|v projection), ``inner`` [T, Hv*128] (the
+        gated-delta in-step output before its gated norm; empty for attention), ``mixed`` [T, H] (the residual after
+        the mixer), all bf16; and the e5m2 GEMM inputs as bf16 values: ``mid`` (out_proj/o_proj input),
+        ``mlp_in`` [T, H], ``ffn`` [T, I]."""
+        cfg = self.cfg
+        t, hsz = self.batch_size * self.verify_tokens, cfg.hidden_size
+        linear = cfg.layer_types[layer] == LINEAR
+        width = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim * 2 + 2 * cfg.num_key_value_heads * cfg.head_dim
+        mid = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim
+        inner = cfg.linear_value_dim if linear else 0
+        flat = self.buffer("probe", layer)
+        bf = flat[: t * (2 * hsz + width + inner) * 2].view(DTYPE)
+        out = {"normed": bf[: t * hsz].view(t, hsz), "projection": bf[t * hsz : t * (hsz + width)].view(t, width),
+               "inner": bf[t * (hsz + width) : t * (hsz + width + inner)].view(t, inner),
+               "mixed": bf[t * (hsz + width + inner) :].view(t, hsz)}
+        at, t32 = t * (2 * hsz + width + inner) * 2, (t + 31) // 32 * 32
+        for name, k in (("mid", mid), ("mlp_in", hsz), ("ffn", cfg.intermediate_size)):
+            out[name] = act_tiles_to_rows(flat[at : at + t32 * k], t32, k)[:t]
+            at += t32 * k
+        return out
+
     def kv_cache(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
         """(k_cache [B,Hkv,S,hd], v_cache stored transposed [B,Hkv,S/32,hd,32])."""
         cfg, b, s = self.cfg, self.batch_size, self.max_seq_len
@@ -224,6 +256,18 @@ class Engine:
             if key == "pending_key_state":
                 value = value[:, :, ::rep]
             mine[key].copy_(value)
+
+
+def act_tiles_to_rows(tiles: torch.Tensor, tokens: int, k: int) -> torch.Tensor:
+    """e5m2 activation tiles (the GEMMs' input layout: tiles of 32 tokens x 64 inputs, token-block major; inside a
+    tile ``[m][lane][8]`` with lane = t % 32 + 32 * ((k % 32) // 16) and byte e = 16 * ((k % 64) // 32) + k % 16,
+    m = e // 8) as bf16 values ``[tokens, k]``."""
+    t = torch.arange(tokens, device=tiles.device).unsqueeze(1)
+    c = torch.arange(k, device=tiles.device).unsqueeze(0)
+    e = ((c % 64) // 32) * 16 + (c % 16)
+    lane = t % 32 + 32 * ((c % 32) // 16)
+    offset = ((t // 32) * (k // 64) + c // 64) * 2048 + (e // 8) * 512 + lane * 8 + e % 8
+    return tiles[offset.reshape(-1)].view(torch.float8_e5m2).to(DTYPE).reshape(tokens, k)
 
 
 def _dev(t: torch.Tensor, dtype: torch.dtype, device) -> torch.Tensor:
