@@ -46,6 +46,8 @@ typedef struct q38_handle q38_handle;
 #define Q38_WEIGHTS_MXFP4 1 /* decoder-layer projections bound as q38_pack_weight_fp4 tiles (MTP layer, head: e4m3) */
 #define Q38_KV_BF16 0
 #define Q38_KV_FP8 1 /* KV caches of e4m3 bytes of value / scale, clamped to +-240, with bf16 scales per layer */
+#define Q38_MFMA_BF16 0
+#define Q38_MFMA_FP8 1
 
 /* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
  * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
@@ -63,6 +65,10 @@ typedef struct q38_config {
     int prefill_chunk; /* most tokens of one q38_prefill call (a multiple of 32; 0: no prefill workspace) */
     int weight_format; /* Q38_WEIGHTS_E4M3 or Q38_WEIGHTS_MXFP4 (the reference's weight_format, config.py:28-30) */
     int kv_cache_format; /* Q38_KV_BF16 or Q38_KV_FP8 (the reference's kv_cache_format, config.py:33-34, model.py:557-601) */
+    int projection_mfma; /* Q38_MFMA_FP8: decoder and MTP projections (e4m3 weights x e5m2 activations) on the scaled FP8
+                            MFMA, each 64-input block summed to about 2^-15.5 of its sum |x w|; Q38_MFMA_BF16: both widened
+                            exactly to bf16 for the bf16 MFMA (float32-grade sums, twice the MFMA time). The head's
+                            group maxima always run on the bf16 MFMA (bf16 activations). */
 } q38_config;
 
 const char* q38_last_error(void);
@@ -131,6 +137,11 @@ int q38_pack_weight_fp4(const uint8_t* packed, const uint8_t* scales, int n, int
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                    uint8_t* scratch, uint16_t* out, void* stream);
 size_t q38_fp8_linear_scratch(int rows, int k);
+/* q38_fp8_linear (f32_out 0: bf16 [rows][n]) or q38_fp8_linear_f32 (f32_out 1: float32 [rows][n], rows as there) with
+ * the products on the MFMA `mfma` names (Q38_MFMA_FP8 or Q38_MFMA_BF16); q38_fp8_linear itself is Q38_MFMA_BF16. Same
+ * scratch. No counterpart in the reference: for measuring the two MFMAs' sums on the same projection. */
+int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int mfma,
+                        int f32_out, uint8_t* scratch, void* out, void* stream);
 /* q38_fp8_linear with an MXFP4 weight from q38_pack_weight_fp4: e5m2(x) times the exact E2M1 x E8M0 values, which is
  * `FP8Linear.forward` on the weights `fp4.to_fp8` makes from the checkpoint (model.py:211-229) wherever that conversion
  * is exact. Same scratch. */

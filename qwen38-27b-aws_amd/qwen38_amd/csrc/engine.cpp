@@ -221,6 +221,7 @@ int gemm(q38_handle* h, int li, const uint8_t* tiles, const uint8_t* scales, con
     GemmArgs a{};
     a.w = tiles;
     a.w4 = fp4_layer(h, li);
+    a.f8 = !a.w4 && h->cfg.projection_mfma == Q38_MFMA_FP8;
     a.ws = scales;
     a.act = act;
     a.K = K;
@@ -568,6 +569,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     if (c.prefill_chunk < 0 || c.prefill_chunk % 32 || c.prefill_chunk > c.max_seq_len) bad += "prefill_chunk must be a multiple of 32 up to max_seq_len; ";
     if (c.weight_format != Q38_WEIGHTS_E4M3 && c.weight_format != Q38_WEIGHTS_MXFP4) bad += "unknown weight_format; ";
     if (c.kv_cache_format != Q38_KV_BF16 && c.kv_cache_format != Q38_KV_FP8) bad += "unknown kv_cache_format; ";
+    if (c.projection_mfma != Q38_MFMA_BF16 && c.projection_mfma != Q38_MFMA_FP8) bad += "unknown projection_mfma; ";
     for (int i = 0; i < c.num_layers && i < Q38_MAX_LAYERS; ++i)
         if (c.layer_types[i] != Q38_LINEAR && c.layer_types[i] != Q38_FULL) bad += "unknown layer type; ";
     if (!bad.empty()) return fail(bad);
@@ -748,7 +750,7 @@ namespace {
 
 // One projection outside a handle: e5m2 tiles of x (unless x is null: the scratch already holds them), then the GEMM.
 int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
-               uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0) {
+               uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0, int f8 = 0) {
     if (!tiles || !tile_scales || !scratch || !out) return fail("null argument");
     if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
     if (x) HIP_TRY(q38_act_tiles(x, rows, k, scratch, stream));
@@ -762,6 +764,7 @@ int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const u
     a.Tpad = pad_tokens(rows);
     a.splits_max = splits_max;
     a.w4 = w4;
+    a.f8 = f8;
     if (epi == EPI_PARTIAL)
         a.part = (float*)out;
     else {
@@ -779,6 +782,14 @@ int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const u
 int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                    uint8_t* scratch, uint16_t* out, void* stream) {
     return standalone(x, rows, k, tiles, tile_scales, n, EPI_BF16, scratch, out, 0, (hipStream_t)stream);
+}
+
+int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int mfma,
+                        int f32_out, uint8_t* scratch, void* out, void* stream) {
+    if (mfma != Q38_MFMA_FP8 && mfma != Q38_MFMA_BF16) return fail("mfma must be Q38_MFMA_FP8 or Q38_MFMA_BF16");
+    if (f32_out && pad_tokens(rows) != rows) return fail("float32 output needs rows in {32, 64, 128} or a multiple of 256");
+    return standalone(x, rows, k, tiles, tile_scales, n, f32_out ? EPI_PARTIAL : EPI_BF16, scratch, out, f32_out ? 1 : 0,
+                      (hipStream_t)stream, 0, mfma == Q38_MFMA_FP8);
 }
 
 int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,

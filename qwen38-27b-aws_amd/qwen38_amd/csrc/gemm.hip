@@ -7,9 +7,12 @@
 // widened by v_cvt_scalef32_pk_bf16_fp4 with the same E8M0 scales, also exactly (half the weight bytes); projection activations are e5m2 bytes (the reference rounds every
 // projection input to e5m2) widened exactly by v_cvt_scalef32_pk_bf16_bf8; the head's activations are bf16. Products
 // run on the bf16 MFMA, v_mfma_f32_32x32x16_bf16, whose float32 accumulation is as precise as a float32 dot product
-// (measured: about 1e-8 of sum |x w|). The FP8 MFMA accumulates internally to only about 2^-14 of that sum, and the
-// reference's e5m2 rounding at every projection input turns such last-bit differences into percent-level divergence
-// within a layer, so it is not used.
+// (measured: about 1e-8 of sum |x w|). An opt-in variant (F8, the engine's projection_mfma = FP8) feeds the tiles as
+// they are to the scaled FP8 MFMA, v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 weights with their E8M0 bytes as block
+// scales, e5m2 activations): no conversions and half the MFMA time, but its internal accumulation is only about
+// 2^-15.5 of a 64-input block's sum |x w| (about 1e-6 of the whole sum at K = 5120), so about 1% of bf16 outputs land
+// on the other neighbour of the reference's, and the reference's e5m2 rounding at every projection input amplifies
+// such last-bit differences to several percent per layer. The bf16 MFMA is the default.
 //
 // Data movement. A workgroup owns a (WF*FR*32 features) x (WT*TR*32 tokens) output tile; every K-step of 64 inputs, its
 // weight tiles (2 KiB of e4m3, or 1 KiB of E2M1 in the same element order), their scales and its activation tiles go straight from global memory into one stage of an S-deep LDS
@@ -89,7 +92,7 @@ __device__ __forceinline__ v8bf widen_e2m1(uint32_t w, float scale) {
     return __builtin_bit_cast(v8bf, r);
 }
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4>
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8>
 __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a) {
     constexpr int NW = WF * WT, NTH = NW * 64;
     constexpr int TT = WT * TR, FT = WF * FR;  // 32-token and 32-feature tiles per workgroup
@@ -107,6 +110,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     static_assert(SC_CHUNKS >= 1 && NW % SC_CHUNKS == 0, "scale stage splits evenly over the waves");
     static_assert(OPS * (S - 2) <= 63 && S >= 2, "vmcnt range");
     static_assert(EPI != EPI_SWIGLU || FR == 2, "gate and up tiles pair up");
+    static_assert(!F8 || (A8 && !W4), "the FP8 MFMA takes e4m3 weight tiles and e5m2 activation tiles");
     constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
     __shared__ int s_arrived;
@@ -184,9 +188,48 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                 for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.0f;
     };
 
+    // One K-step with the FP8 MFMA: a weight tile's 64 inputs per lane as 32 bytes (its four 8-byte MFMA-step
+    // fragments: inputs 16 (l / 32) + [0, 16) and 32 + 16 (l / 32) + [0, 16), the operand order of
+    // v_mfma_scale_f32_32x32x64_f8f6f4), the lane's E8M0 byte for (row l % 32, MX block l / 32) as the weight scale, the
+    // activation tile's 32 bytes the same way with scale 1 (127).
+    auto compute_f8 = [&](int st) {
+        const uint8_t* sb = lds + st * STAGE;
+        const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * 8;
+        const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2 + (lane >> 5);
+        v8i wv[FR];
+        int ws[FR];
+#pragma unroll
+        for (int f = 0; f < FR; ++f) {
+            ws[f] = sl[f * 64];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
+                wv[f][2 * m] = (int)r[0];
+                wv[f][2 * m + 1] = (int)r[1];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+            v8i xv;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const u2 r = *(const u2*)(sb + (wt * TR + t) * 2048 + m * 512 + lane * 8);
+                xv[2 * m] = (int)r[0];
+                xv[2 * m + 1] = (int)r[1];
+            }
+#pragma unroll
+            for (int f = 0; f < FR; ++f)
+                acc[f][t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wv[f], xv, acc[f][t], 0, 1, 0, ws[f], 0, 127);
+        }
+    };
+
     // One K-step: per MFMA step m, each weight fragment is 8 contiguous bytes (4 for E2M1) per lane, each activation
     // fragment 8 (16 for bf16 activations).
     auto compute = [&](int st) {
+        if constexpr (F8) {
+            compute_f8(st);
+            return;
+        }
         const uint8_t* sb = lds + st * STAGE;
         const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * (WTB / 256);
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
@@ -385,7 +428,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
 constexpr int MIN_UNITS = 8;  // smallest K range worth a stream-K group
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4>
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8>
 hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
     GemmArgs a = a0;
     constexpr int BF = WF * FR * 32, BT = WT * TR * 32, NTH = WF * WT * 64;
@@ -425,47 +468,47 @@ hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
         a.splits = 1;
     }
     if (splits_out) *splits_out = a.splits;
-    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI, W4>), dim3(grid), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI, W4, F8>), dim3(grid), dim3(NTH), 0, stream, a);
     return hipGetLastError();
 }
 
 // Tile shape: 256 tokens per workgroup from 256 tokens up (128 for bf16 outputs), Tpad tokens below. Features per workgroup: with e5m2
 // activations 128 when N / 128 is a multiple of 8 (an equal share of tiles per XCD; as fast per tile as 256 and twice
 // the tiles), else 256; with bf16 activations (the head) 256, and 512 below 256 tokens when N allows.
-template <bool A8, int EPI, bool W4>
+template <bool A8, int EPI, bool W4, bool F8>
 hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
     auto balanced = [&](int bf) { return a.N % bf == 0 && (a.N / bf) % 8 == 0; };
     if (a.Tpad % 256 == 0) {
         if constexpr (A8) {
             // bf16 outputs: 128 x 128 tiles, two token blocks per weight tile on one XCD (their stream-K ranges split
             // fewer tiles; measured 4-8 % faster on the 16384- and 14336-wide projections than 128 x 256).
-            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 9, EPI, W4>(a, splits_out, stream);
-            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 6, EPI, W4>(a, splits_out, stream);
-            return launch<4, 2, 2, 4, true, 4, EPI, W4>(a, splits_out, stream);
+            if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 9, EPI, W4, F8>(a, splits_out, stream);
+            if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 6, EPI, W4, F8>(a, splits_out, stream);
+            return launch<4, 2, 2, 4, true, 4, EPI, W4, F8>(a, splits_out, stream);
         } else {
-            return launch<4, 2, 2, 4, false, 3, EPI, W4>(a, splits_out, stream);
+            return launch<4, 2, 2, 4, false, 3, EPI, W4, F8>(a, splits_out, stream);
         }
     }
     const bool wide = a.N % 512 == 0 && (balanced(512) || !balanced(256));
     switch (a.Tpad) {
         case 128:
-            return wide ? launch<8, 1, 2, 4, A8, 3, EPI, W4>(a, splits_out, stream)
-                        : launch<4, 2, 2, 2, A8, 3, EPI, W4>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 4, A8, 3, EPI, W4, F8>(a, splits_out, stream)
+                        : launch<4, 2, 2, 2, A8, 3, EPI, W4, F8>(a, splits_out, stream);
         case 64:
             // Measured per epilogue at 64 tokens (the decode step's projections): bf16 outputs fastest as 128 x 64
             // tiles with a deep ring (qkvz 32 against 50 us as 512 x 64), split-K partials as 128 x 64 with 5 stages,
             // the SwiGLU pair as 256 x 64 (50.9 against 56.4 us as 128 x 64).
             if constexpr (A8) {
-                if (EPI == EPI_BF16 && balanced(128)) return launch<2, 2, 2, 1, true, 8, EPI, W4>(a, splits_out, stream);
-                if (EPI == EPI_PARTIAL && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
-                if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4>(a, splits_out, stream);
+                if (EPI == EPI_BF16 && balanced(128)) return launch<2, 2, 2, 1, true, 8, EPI, W4, F8>(a, splits_out, stream);
+                if (EPI == EPI_PARTIAL && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4, F8>(a, splits_out, stream);
+                if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4, F8>(a, splits_out, stream);
             }
-            if constexpr (!A8) return launch<4, 2, 2, 1, false, 6, EPI, W4>(a, splits_out, stream);
-            return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4>(a, splits_out, stream)
-                        : launch<4, 2, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
+            if constexpr (!A8) return launch<4, 2, 2, 1, false, 6, EPI, W4, F8>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4, F8>(a, splits_out, stream)
+                        : launch<4, 2, 2, 1, A8, 4, EPI, W4, F8>(a, splits_out, stream);
         case 32:
-            return wide ? launch<8, 1, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream)
-                        : launch<4, 1, 2, 1, A8, 4, EPI, W4>(a, splits_out, stream);
+            return wide ? launch<8, 1, 2, 1, A8, 4, EPI, W4, F8>(a, splits_out, stream)
+                        : launch<4, 1, 2, 1, A8, 4, EPI, W4, F8>(a, splits_out, stream);
         default:
             return hipErrorInvalidValue;
     }
@@ -507,17 +550,25 @@ int q38_gemm_l2_local() {
 hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream) {
     if (a.w4) {
         switch (epi) {
-            case EPI_BF16: return dispatch<true, EPI_BF16, true>(a, splits_out, stream);
-            case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, true>(a, splits_out, stream);
-            case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, true>(a, splits_out, stream);
+            case EPI_BF16: return dispatch<true, EPI_BF16, true, false>(a, splits_out, stream);
+            case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, true, false>(a, splits_out, stream);
+            case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, true, false>(a, splits_out, stream);
             default: return hipErrorInvalidValue;  // the head's weights are e4m3
         }
     }
+    if (a.f8) {
+        switch (epi) {
+            case EPI_BF16: return dispatch<true, EPI_BF16, false, true>(a, splits_out, stream);
+            case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, false, true>(a, splits_out, stream);
+            case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, false, true>(a, splits_out, stream);
+            default: break;  // the head's activations are bf16: the bf16 MFMA below
+        }
+    }
     switch (epi) {
-        case EPI_BF16: return dispatch<true, EPI_BF16, false>(a, splits_out, stream);
-        case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, false>(a, splits_out, stream);
-        case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, false>(a, splits_out, stream);
-        case EPI_GROUPMAX: return dispatch<false, EPI_GROUPMAX, false>(a, splits_out, stream);
+        case EPI_BF16: return dispatch<true, EPI_BF16, false, false>(a, splits_out, stream);
+        case EPI_SWIGLU: return dispatch<true, EPI_SWIGLU, false, false>(a, splits_out, stream);
+        case EPI_PARTIAL: return dispatch<true, EPI_PARTIAL, false, false>(a, splits_out, stream);
+        case EPI_GROUPMAX: return dispatch<false, EPI_GROUPMAX, false, false>(a, splits_out, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -28,6 +28,7 @@ struct GemmArgs {
     int l2_local;        // workgroup i runs on XCD i % 8 (q38_gemm_l2_local()): stream-K partials stay in L2
     int splits;          // EPI_PARTIAL split count (set by the launcher)
     int w4;              // weight tiles hold MXFP4 (q38_pack_fp4) rather than e4m3
+    int f8;              // e4m3 weights x e5m2 activations on the FP8 MFMA (else widened to bf16 for the bf16 MFMA)
 };
 
 struct NormArgs {

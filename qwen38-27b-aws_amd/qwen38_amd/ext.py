@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
     "q38_kernel_timer",
 )
 
@@ -34,7 +34,7 @@ class Q38Config(ctypes.Structure):
         ("linear_conv_kernel_dim", ctypes.c_int), ("rms_norm_eps", ctypes.c_float),
         ("batch_size", ctypes.c_int), ("verify_tokens", ctypes.c_int), ("max_seq_len", ctypes.c_int), ("mtp", ctypes.c_int),
         ("saved_states", ctypes.c_int), ("prefill_chunk", ctypes.c_int), ("weight_format", ctypes.c_int),
-        ("kv_cache_format", ctypes.c_int),
+        ("kv_cache_format", ctypes.c_int), ("projection_mfma", ctypes.c_int),
     ]
 
 
@@ -43,6 +43,7 @@ _lib = None
 
 WEIGHT_FORMATS = {"e4m3": 0, "mxfp4": 1}
 KV_CACHE_FORMATS = {"bf16": 0, "fp8": 1}
+PROJECTION_MFMA = {"bf16": 0, "fp8": 1}
 
 
 def library() -> ctypes.CDLL:
@@ -69,6 +70,7 @@ def library() -> ctypes.CDLL:
     lib.q38_mxfp4_linear.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_fp8_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_fp8_linear_mfma.argtypes = [p, i, i, p, p, i, i, i, p, p, p]
     lib.q38_mlp_up.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_tiles_size.argtypes = [i, i]
     lib.q38_kernel_timer.argtypes = [p, i, ctypes.POINTER(i), ctypes.POINTER(ctypes.c_float)]
@@ -110,7 +112,8 @@ def stream() -> int:
 
 
 def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16") -> Q38Config:
+                prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16",
+                projection_mfma: str = "bf16") -> Q38Config:
     c = Q38Config()
     c.hidden_size, c.intermediate_size, c.vocab_size = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     if cfg.num_hidden_layers > MAX_LAYERS:
@@ -129,6 +132,7 @@ def make_config(cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp:
     c.prefill_chunk = prefill_chunk
     c.weight_format = WEIGHT_FORMATS[weight_format]
     c.kv_cache_format = KV_CACHE_FORMATS[kv_cache_format]
+    c.projection_mfma = PROJECTION_MFMA[projection_mfma]
     return c
 
 
@@ -136,9 +140,10 @@ class Handle:
     """One q38_handle: shapes fixed at creation, every buffer bound by the owner."""
 
     def __init__(self, cfg: TextConfig, batch: int, tokens: int, max_seq_len: int, mtp: bool, saved_states: bool = False,
-                 prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16"):
+                 prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16", projection_mfma: str = "bf16"):
         self.lib = library()
-        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format, kv_cache_format)
+        self.c = make_config(cfg, batch, tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format, kv_cache_format,
+                             projection_mfma)
         h = ctypes.c_void_p()
         check(self.lib.q38_create(ctypes.byref(self.c), ctypes.byref(h)))
         self.h = h
@@ -238,6 +243,17 @@ def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: in
     scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
     check(library().q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def fp8_linear_mfma(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, mfma: str, f32_out: bool = False,
+                    scratch=None) -> torch.Tensor:
+    """The FP8 projection with its products on the named MFMA ("fp8" or "bf16"), bf16 or float32 output."""
+    rows, k = x.shape
+    scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
+    out = torch.empty(rows, n, dtype=torch.float32 if f32_out else torch.bfloat16, device=x.device)
+    check(library().q38_fp8_linear_mfma(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, PROJECTION_MFMA[mfma],
+                                        int(f32_out), ptr(scratch), ptr(out), stream()))
     return out
 
 

@@ -42,15 +42,17 @@ class Engine:
     """Device state of one loaded model: a q38 handle plus the tensors bound to it."""
 
     def __init__(self, cfg: TextConfig, batch_size: int, verify_tokens: int, max_seq_len: int, mtp: bool = True, device="cuda",
-                 saved_states: bool = False, prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16"):
+                 saved_states: bool = False, prefill_chunk: int = 0, weight_format: str = "e4m3", kv_cache_format: str = "bf16",
+                 projection_mfma: str = "bf16"):
         if not torch.cuda.is_available():
             raise RuntimeError("the verify path runs on the GPU only")
         self.cfg, self.batch_size, self.verify_tokens, self.max_seq_len, self.mtp = cfg, batch_size, verify_tokens, max_seq_len, mtp
         self.saved_states, self.prefill_chunk, self.weight_format = saved_states, prefill_chunk, weight_format
         self.kv_cache_format = kv_cache_format
         self.device = torch.device(device)
+        self.projection_mfma = projection_mfma
         self.handle = ext.Handle(cfg, batch_size, verify_tokens, max_seq_len, mtp, saved_states, prefill_chunk, weight_format,
-                                 kv_cache_format)
+                                 kv_cache_format, projection_mfma)
         kv_dtype = torch.uint8 if kv_cache_format == "fp8" else DTYPE
         self.buffers: dict[tuple[str, int], torch.Tensor] = {}
         self.mtp_layer = cfg.num_hidden_layers

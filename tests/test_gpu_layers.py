@@ -20,14 +20,15 @@ WORKLOADS = {w.name: (i, w) for i, w in enumerate(verify_configs()) if i != 2}
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("mfma", ["fp8", "bf16"])
 @pytest.mark.parametrize("name", list(WORKLOADS))
-def test_verify_layers_match_the_oracle_teacher_forced(gpu, name):
+def test_verify_layers_match_the_oracle_teacher_forced(gpu, name, mfma):
     index, w = WORKLOADS[name]
     cfg, b, k, s, ctx = w.cfg, w.batch, w.tokens, w.max_seq_len, w.context
     seed = 11 + index
-    print(f"config {index} ({name}): B={b} K={k} context {ctx}", flush=True)
+    print(f"config {index} ({name}): B={b} K={k} context {ctx}, projections on the {mfma} MFMA", flush=True)
     values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg, mtp=False, head=False), seed, device="cuda"))
-    stack = LayerStack(cfg, values, b, k, s, seeded_states(cfg, b, k, s, [ctx] * b, seed))
+    stack = LayerStack(cfg, values, b, k, s, seeded_states(cfg, b, k, s, [ctx] * b, seed), projection_mfma=mfma)
     del values
     accepted = accepted_uniform(b, k, seed) if index == 4 else accepted_like_corrupted_drafts(b, k, seed)
     positions = [ctx] * b

@@ -88,3 +88,36 @@ def test_bf16_outputs_round_to_nearest_even_like_torch(gpu):
     ties = (f32.view(torch.int32) & 0xFFFF) == 0x8000
     assert int(ties.sum()) > 100
     assert torch.equal(bf.view(torch.int16), f32.to(torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,k,n", [(256, 5120, 512), (64, 17408, 256), (256, 256, 256)])
+def test_fp8_mfma_projection_sums_within_its_accumulation_bound(gpu, rows, k, n):
+    """The projection on the scaled FP8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4 reading the e4m3 weight and e5m2
+    activation tiles as they are, the weight's E8M0 bytes as the block scales): float32 outputs within 2^-14 of
+    sum |x w| of the exact float64 sum (its measured internal accumulation is about 2^-15.5 of a 64-input block's
+    sum |x w|), against the bf16 MFMA path's float32-grade sums on the same inputs; the bf16 outputs of the two paths equal except
+    where the exact sum lies within that bound of a bf16 rounding boundary; and the same identity and one-hot checks as
+    the bf16 path (every MX block scaled by its own scale)."""
+    g = torch.Generator().manual_seed(rows + k)
+    coded, scales = quantize_e4m3(torch.randn(n, k, generator=g) * 0.02)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    xq = round_e5m2(x).double()
+    wd = dequantize_e4m3(coded, scales).double()
+    exact, abs_sum = xq @ wd.T, xq.abs() @ wd.abs().T
+    f8 = ext.fp8_linear_mfma(x.cuda(), tiles, words, n, "fp8", f32_out=True).cpu().double()
+    bf = ext.fp8_linear_mfma(x.cuda(), tiles, words, n, "bf16", f32_out=True).cpu().double()
+    e8, eb = float(((f8 - exact).abs() / abs_sum).max()), float(((bf - exact).abs() / abs_sum).max())
+    print(f"rows {rows} k {k}: fp8 MFMA max err / sum|xw| {e8:.3g} (2^{torch.log2(torch.tensor(e8)):.1f}), bf16 MFMA {eb:.3g}")
+    assert e8 <= 2.0**-14 and eb <= 2.0**-22
+    o8 = ext.fp8_linear_mfma(x.cuda(), tiles, words, n, "fp8").cpu()
+    ob = ext.fp8_linear_mfma(x.cuda(), tiles, words, n, "bf16").cpu()
+    assert torch.equal(ob, ext.fp8_linear(x.cuda(), tiles, words, n).cpu())
+    differ = o8 != ob
+    if differ.any():
+        ulp = bf16_ulp(exact[differ])
+        lo = torch.floor(exact[differ] / ulp) * ulp  # the two bf16 neighbours of the exact sum (within a binade)
+        boundary = torch.minimum((exact[differ] - lo - ulp / 2).abs(), (exact[differ] - lo + ulp / 2).abs())
+        assert bool((boundary <= 2.0**-14 * abs_sum[differ]).all())
+    print(f"  bf16 outputs differing between the MFMAs: {int(differ.sum())} of {differ.numel()}")
