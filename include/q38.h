@@ -48,6 +48,9 @@ typedef struct q38_handle q38_handle;
 #define Q38_KV_FP8 1 /* KV caches of e4m3 bytes of value / scale, clamped to +-240, with bf16 scales per layer */
 #define Q38_MFMA_BF16 0
 #define Q38_MFMA_FP8 1
+/* Or'ed into q38_fp8_linear_mfma's `mfma`: finish every stream-K tile by recomputing its contributors' partials, the
+ * path the GEMM takes when a tile's contributors run on different XCDs (so do not share an L2). */
+#define Q38_GEMM_RECOMPUTE 4
 
 /* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
  * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
@@ -138,8 +141,9 @@ int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, con
                    uint8_t* scratch, uint16_t* out, void* stream);
 size_t q38_fp8_linear_scratch(int rows, int k);
 /* q38_fp8_linear (f32_out 0: bf16 [rows][n]) or q38_fp8_linear_f32 (f32_out 1: float32 [rows][n], rows as there) with
- * the products on the MFMA `mfma` names (Q38_MFMA_FP8 or Q38_MFMA_BF16); q38_fp8_linear itself is Q38_MFMA_BF16. Same
- * scratch. No counterpart in the reference: for measuring the two MFMAs' sums on the same projection. */
+ * the products on the MFMA `mfma` names (Q38_MFMA_FP8 or Q38_MFMA_BF16, optionally | Q38_GEMM_RECOMPUTE);
+ * q38_fp8_linear itself is Q38_MFMA_BF16. Same scratch. No counterpart in the reference: for measuring the two MFMAs'
+ * sums on the same projection, and the GEMM's two ways of finishing a tile split between workgroups. */
 int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int mfma,
                         int f32_out, uint8_t* scratch, void* out, void* stream);
 /* q38_fp8_linear with an MXFP4 weight from q38_pack_weight_fp4: e5m2(x) times the exact E2M1 x E8M0 values, which is

@@ -65,13 +65,12 @@ int device_cus() {
 }
 
 // GEMM scratch behind the activation tiles: stream-K arrival counters, then partial slots.
-size_t gemm_scratch_bytes(int cus) { return (size_t)GEMM_COUNTERS * 4 + (size_t)2 * cus * GEMM_SLOT_FLOATS * 4; }
+size_t gemm_scratch_bytes(int cus) { return (size_t)GEMM_COUNTERS * 8 + (size_t)2 * cus * GEMM_SLOT_FLOATS * 4; }
 
 void gemm_scratch(GemmArgs& a, uint8_t* base, int cus) {
-    a.l2_local = q38_gemm_l2_local();
-    a.counters = (int*)base;
+    a.counters = (unsigned long long*)base;
     a.counters_n = GEMM_COUNTERS;
-    a.fix = (float*)(base + (size_t)GEMM_COUNTERS * 4);
+    a.fix = (float*)(base + (size_t)GEMM_COUNTERS * 8);
     a.fix_floats = (size_t)2 * cus * GEMM_SLOT_FLOATS;
     a.cus = cus;
 }
@@ -702,10 +701,8 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
         return fail(std::string("buffer '") + name + "' needs " + std::to_string(n) + " bytes, got " + std::to_string(nbytes));
     if ((uintptr_t)dev_ptr % 16) return fail(std::string("buffer '") + name + "' is not 16-byte aligned");
     if (layer < 0 && std::string(name) == "workspace") {
-        // The GEMMs' arrival counters start at zero; the one-time XCD placement check (a small allocation) runs
-        // here rather than inside a step.
-        HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 4));
-        (void)q38_gemm_l2_local();
+        // The GEMMs' arrival counters start at zero.
+        HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 8));
     }
     Buf b;
     b.p = dev_ptr;
@@ -750,7 +747,7 @@ namespace {
 
 // One projection outside a handle: e5m2 tiles of x (unless x is null: the scratch already holds them), then the GEMM.
 int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
-               uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0, int f8 = 0) {
+               uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0, int f8 = 0, int recompute = 0) {
     if (!tiles || !tile_scales || !scratch || !out) return fail("null argument");
     if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
     if (x) HIP_TRY(q38_act_tiles(x, rows, k, scratch, stream));
@@ -765,6 +762,7 @@ int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const u
     a.splits_max = splits_max;
     a.w4 = w4;
     a.f8 = f8;
+    a.recompute = recompute;
     if (epi == EPI_PARTIAL)
         a.part = (float*)out;
     else {
@@ -786,10 +784,11 @@ int q38_fp8_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, con
 
 int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int mfma,
                         int f32_out, uint8_t* scratch, void* out, void* stream) {
-    if (mfma != Q38_MFMA_FP8 && mfma != Q38_MFMA_BF16) return fail("mfma must be Q38_MFMA_FP8 or Q38_MFMA_BF16");
+    const int kind = mfma & ~Q38_GEMM_RECOMPUTE;
+    if (kind != Q38_MFMA_FP8 && kind != Q38_MFMA_BF16) return fail("mfma must be Q38_MFMA_FP8 or Q38_MFMA_BF16");
     if (f32_out && pad_tokens(rows) != rows) return fail("float32 output needs rows in {32, 64, 128} or a multiple of 256");
     return standalone(x, rows, k, tiles, tile_scales, n, f32_out ? EPI_PARTIAL : EPI_BF16, scratch, out, f32_out ? 1 : 0,
-                      (hipStream_t)stream, 0, mfma == Q38_MFMA_FP8);
+                      (hipStream_t)stream, 0, kind == Q38_MFMA_FP8, (mfma & Q38_GEMM_RECOMPUTE) != 0);
 }
 
 int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     static_assert(!F8 || (A8 && !W4), "the FP8 MFMA takes e4m3 weight tiles and e5m2 activation tiles");
     constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
-    __shared__ int s_arrived;
+    __shared__ unsigned long long s_arrived;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses stay in scalar registers
@@ -121,8 +121,8 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     const int KS = a.K >> 6;
     const int NF = a.N / (FT * 32), NTB = a.Tpad / (TT * 32);
 
-    // Workgroup -> (group, token block). Workgroups are dealt to the 8 XCDs round-robin (workgroup i on XCD i % 8);
-    // when the grid allows, the NTB token blocks of one group get ids 8 apart, so they share an XCD and its L2.
+    // Workgroup -> (group, token block). Workgroups are dealt to the 8 XCDs round-robin, so workgroups with equal
+    // blockIdx.x % 8 share an XCD and its L2; when the grid allows, the NTB token blocks of one group get ids 8 apart.
     const int groups = gridDim.x / NTB;
     int grp, tb;
     if (gridDim.x % (8 * NTB) == 0) {
@@ -138,6 +138,9 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     // ranges of its units (tile-major), so the contributors of a tile share an L2. Local unit ux is tile
     // fb = x + 8 (ux / KS), K-step ux % KS.
     const int xcd = grp & 7, gi = grp >> 3, gx = groups >> 3;
+    uint32_t xcc_id;  // the XCD this workgroup actually runs on (0-7 on gfx950's 8 XCDs)
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_id));
+    const unsigned long long own_byte = 0xffull << (8 * (xcc_id & 7));
     const int Ux = ((NF - xcd + 7) >> 3) * KS;
     int u0, u1, z = 0, fstep = 8, fbase = xcd;
     if constexpr (EPI == EPI_PARTIAL) {
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     };
 
     v16f acc[FR][TR];
-    auto zero = [&]() {
+    auto zero = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int f = 0; f < FR; ++f)
 #pragma unroll
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     // fragments: inputs 16 (l / 32) + [0, 16) and 32 + 16 (l / 32) + [0, 16), the operand order of
     // v_mfma_scale_f32_32x32x64_f8f6f4), the lane's E8M0 byte for (row l % 32, MX block l / 32) as the weight scale, the
     // activation tile's 32 bytes the same way with scale 1 (127).
-    auto compute_f8 = [&](int st) {
+    auto compute_f8 = [&](int st) __attribute__((always_inline)) {
         const uint8_t* sb = lds + st * STAGE;
         const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * 8;
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2 + (lane >> 5);
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
     // One K-step: per MFMA step m, each weight fragment is 8 contiguous bytes (4 for E2M1) per lane, each activation
     // fragment 8 (16 for bf16 activations).
-    auto compute = [&](int st) {
+    auto compute = [&](int st) __attribute__((always_inline)) {
         if constexpr (F8) {
             compute_f8(st);
             return;
@@ -271,7 +274,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
     // Accumulator layout of a 32x32 MFMA: lane l holds token column l % 32 and feature rows
     // 8 * (i / 4) + 4 * (l / 32) + i % 4 for i = 0..15.
-    auto epilogue = [&](int fb) {
+    auto epilogue = [&](int fb) __attribute__((always_inline)) {
         const int rowq = (lane >> 5) * 4;
         const int ft0 = fb * FT + wf * FR;
 #pragma unroll
@@ -330,50 +333,36 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
         }
     };
 
-    // Stream-K fixup of tile (fb, tb) from a partial range. The contributors (groups g_first..g_last of this XCD, in K
-    // order) share the XCD's L2: a partial is plain stores (through to L2) completed before a device-scope arrival
-    // count, and the last arrival reads the others past its L1 (sc0 buffer loads), adds all partials in K order and
-    // finishes the tile. Fast path: the tile's first contributor, finding every other partial already counted, adds
-    // them to its own sums without storing them (the same additions in the same order). Without the round-robin XCD
-    // placement (a.l2_local == 0) the stores are released and the loads acquired at device scope.
-    auto fixup = [&](int fb) {
-        const int t0 = ((fb - xcd) >> 3) * KS;  // first local unit of the tile
-        auto group_of = [&](int u) { return (int)(((long)(u + 1) * gx - 1) / Ux); };
-        auto slot_of = [&](int g) {  // g: group index within the XCD
-            const int start = (int)((long)g * Ux / gx);
-            return ((size_t)((g * 8 + xcd) * NTB + tb) * 2 + (start > t0 ? 0 : 1)) * SLOT;
-        };
-        const int g_first = group_of(t0), g_last = group_of(t0 + KS - 1);
-        int* const counter = a.counters + fb * NTB + tb;
-        bool fast = false;
-        if (gi == g_first) {
-            if (tid == 0) s_arrived = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __syncthreads();
-            fast = s_arrived == g_last - g_first;
-            __syncthreads();  // s_arrived is read by every thread before it is written again
-        }
-        if (!fast) {
-            v4f* mine = (v4f*)(a.fix + slot_of(gi));
+    // Stream-K fixup of tile (fb, tb) from a partial range. The contributors (groups g_first..g_last of index xcd, in K
+    // order) are meant to share that XCD's L2. Each arrival adds one to the byte of the tile's counter that belongs to
+    // the XCD it actually runs on. A partial is plain stores (through to L2) completed before the arrival; the last
+    // arrival, finding every other count in its own XCD's byte, reads the others past its L1 (sc0 buffer loads), adds
+    // all partials in K order and finishes the tile. Fast path: the tile's first contributor, finding every other
+    // partial already counted, adds them to its own sums without storing its own (the same additions in the same
+    // order). Should contributors ever run on different XCDs, their partials may sit in another L2: the last arrival
+    // then reads none of them and returns true, and finishes the tile after its own range (`recompute`).
+    auto start_of = [&](int g) { return (int)((long)g * Ux / gx); };  // g: group index within the XCD
+    auto group_of = [&](int u) { return (int)(((long)(u + 1) * gx - 1) / Ux); };
+    auto slot_of = [&](int g, int t0) {
+        return ((size_t)((g * 8 + xcd) * NTB + tb) * 2 + (start_of(g) > t0 ? 0 : 1)) * SLOT;
+    };
+    auto store_partial = [&](size_t slot) __attribute__((always_inline)) {
+        v4f* mine = (v4f*)(a.fix + slot);
 #pragma unroll
-            for (int f = 0; f < FR; ++f)
+        for (int f = 0; f < FR; ++f)
 #pragma unroll
-                for (int t = 0; t < TR; ++t)
+            for (int t = 0; t < TR; ++t)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        mine[((f * TR + t) * 4 + q) * NTH + tid] =
-                            (v4f){acc[f][t][4 * q], acc[f][t][4 * q + 1], acc[f][t][4 * q + 2], acc[f][t][4 * q + 3]};
-            if (!a.l2_local) __threadfence();
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (tid == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __syncthreads();
-            if (s_arrived != g_last - g_first) return;
-        }
-        if (!a.l2_local) __threadfence();
-        // acc = partial g_first + ... + partial g_last, added in that order (the fast path holds g_first's already).
+                for (int q = 0; q < 4; ++q)
+                    mine[((f * TR + t) * 4 + q) * NTH + tid] =
+                        (v4f){acc[f][t][4 * q], acc[f][t][4 * q + 1], acc[f][t][4 * q + 2], acc[f][t][4 * q + 3]};
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    // acc = partial g_first + ... + partial g_last, added in that order (from g_first + 1 when acc holds g_first's).
+    auto sum_partials = [&](int t0, int g_from, int g_first, int g_last) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t fix = __builtin_amdgcn_make_buffer_rsrc(a.fix, 0, 0x7fffffff, 0x00020000);
-        for (int g = fast ? g_first + 1 : g_first; g <= g_last; ++g) {
-            const uint32_t base = (uint32_t)(slot_of(g) * 4);
+        for (int g = g_from; g <= g_last; ++g) {
+            const uint32_t base = (uint32_t)(slot_of(g, t0) * 4);
 #pragma unroll
             for (int f = 0; f < FR; ++f)
 #pragma unroll
@@ -386,14 +375,74 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                         for (int e = 0; e < 4; ++e) acc[f][t][4 * q + e] = g == g_first ? v[e] : acc[f][t][4 * q + e] + v[e];
                     }
         }
+    };
+    auto fixup = [&](int fb) __attribute__((always_inline)) -> bool {
+        const int t0 = ((fb - xcd) >> 3) * KS;  // first local unit of the tile
+        const int g_first = group_of(t0), g_last = group_of(t0 + KS - 1);
+        unsigned long long* const counter = a.counters + fb * NTB + tb;
+        auto arrivals = [](unsigned long long c) {
+            int total = 0;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) total += (int)((c >> (8 * x)) & 0xff);
+            return total;
+        };
+        unsigned long long others = 0;  // the other contributors' arrivals
+        bool fast = false;
+        if (gi == g_first) {
+            if (tid == 0) s_arrived = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            others = s_arrived;
+            fast = arrivals(others) == g_last - g_first;
+            __syncthreads();  // s_arrived is read by every thread before it is written again
+        }
+        if (!fast) {
+            store_partial(slot_of(gi, t0));
+            __syncthreads();
+            if (tid == 0)
+                s_arrived = __hip_atomic_fetch_add(counter, own_byte & 0x0101010101010101ull, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            others = s_arrived;
+            if (arrivals(others) != g_last - g_first) return false;
+        }
+        if (a.recompute || (others & ~own_byte) != 0) return true;
+        sum_partials(t0, fast ? g_first + 1 : g_first, g_first, g_last);
         epilogue(fb);
-        if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(counter, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    };
+
+    // Finishes tile fb whose contributors did not all share this workgroup's L2, after the main loop (the ring is
+    // idle): each contributor's partial again, its K-steps one at a time through stage 0 from zero sums, stored in its
+    // slot here; then the partials added in K order as above. The same MFMAs and additions, so the same bits.
+    auto recompute = [&](int fb) __attribute__((always_inline)) {
+        const int t0 = ((fb - xcd) >> 3) * KS;
+        const int g_first = group_of(t0), g_last = group_of(t0 + KS - 1);
+        int st0 = 0;  // stage 0, opaque to the compiler: addresses of a constant stage would be computed at the top of
+        asm volatile("" : "+s"(st0));  // the kernel and held in registers through the main loop
+#pragma unroll 1
+        for (int g = g_first; g <= g_last; ++g) {
+            const int kb = max(start_of(g) - t0, 0), ke = min(start_of(g + 1) - t0, KS);
+            zero();
+#pragma unroll 1
+            for (int k = kb; k < ke; ++k) {
+                issue(fb, k, st0);
+                wait_and_barrier<0>();
+                compute(st0);
+                __syncthreads();  // every wave is done with stage 0 before it is loaded again
+            }
+            store_partial(slot_of(g, t0));
+        }
+        sum_partials(t0, g_first, g_first, g_last);
+        epilogue(fb);
+        if (tid == 0) __hip_atomic_store(a.counters + fb * NTB + tb, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
 
     // Cursors (feature tile, K-step) of the next unit to load and of the unit being computed.
     int ifb = fbase + fstep * (u0 / KS), ik = u0 % KS;
     int cfb = ifb, ck = ik;
     bool partial_start = ik != 0;  // the current tile segment began inside the tile
+    int later0 = -1, later1 = -1;  // tiles to finish by recomputation (at most the range's first and last)
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
         if (i < n) {
@@ -417,12 +466,22 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
         if (ck == KS - 1 || i == n - 1) {
             if (EPI == EPI_PARTIAL || (!partial_start && ck == KS - 1))
                 epilogue(cfb);
-            else
-                fixup(cfb);
+            else if (fixup(cfb))
+                (later0 < 0 ? later0 : later1) = cfb;
             zero();
             partial_start = false;
         }
         if (++ck == KS) ck = 0, cfb += fstep;
+    }
+    if constexpr (EPI != EPI_PARTIAL) {
+        if (later0 >= 0) {
+            wait_and_barrier<0>();  // every wave is done with the ring
+#pragma unroll 1
+            for (int d = 0; d < 2; ++d) {
+                const int fb = d ? later1 : later0;
+                if (fb >= 0) recompute(fb);
+            }
+        }
     }
 }
 
@@ -514,38 +573,7 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
     }
 }
 
-__global__ void xcc_probe_kernel(int* out) {
-    if (threadIdx.x == 0) {
-        uint32_t id;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(id));
-        out[blockIdx.x] = (int)(id & 0xf);
-    }
-}
-
 }  // namespace
-
-// Whether workgroup i of a launch runs on XCD i % 8 on the current device (measured once per device with the
-// XCC_ID hardware register). The stream-K fixup keeps partial sums in one XCD's L2 only when it does.
-int q38_gemm_l2_local() {
-    static int known[64];  // 0 unknown, 1 no, 2 yes
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (!known[dev]) {
-        constexpr int n = 64;
-        int* d = nullptr;
-        int h[n];
-        bool ok = hipMalloc(&d, n * sizeof(int)) == hipSuccess;
-        if (ok) {
-            hipLaunchKernelGGL(xcc_probe_kernel, dim3(n), dim3(64), 0, 0, d);
-            ok = hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
-            for (int i = 0; ok && i < n; ++i) ok = h[i] == i % 8;
-        }
-        if (d) (void)hipFree(d);
-        (void)hipGetLastError();
-        known[dev] = ok ? 2 : 1;
-    }
-    return known[dev] == 2;
-}
 
 hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream) {
     if (a.w4) {

@@ -6,7 +6,7 @@
 enum { EPI_BF16 = 0, EPI_SWIGLU = 1, EPI_PARTIAL = 2, EPI_GROUPMAX = 3 };
 
 constexpr int GEMM_SPLIT_MAX = 8;      // split-K partial buffers (EPI_PARTIAL)
-constexpr int GEMM_COUNTERS = 65536;   // stream-K arrival counters
+constexpr int GEMM_COUNTERS = 65536;   // stream-K arrival counters (8 bytes each)
 constexpr int GEMM_SLOT_FLOATS = 65536;  // floats of one stream-K partial (largest workgroup tile)
 
 struct GemmArgs {
@@ -21,11 +21,12 @@ struct GemmArgs {
     float* part;         // EPI_PARTIAL: [split][Tpad][N]; EPI_GROUPMAX: maxima [T][N/32]
     float* fix;          // stream-K partial slots: 2 per workgroup of GEMM_SLOT_FLOATS
     size_t fix_floats;
-    int* counters;       // stream-K arrival counters, zero between launches (each launch leaves them zero)
+    unsigned long long* counters;  // stream-K arrivals per tile, one byte per XCD; zero between launches (each
+                                   // launch leaves them zero)
     int counters_n;
     int cus;             // compute units: one persistent workgroup each
     int splits_max;      // EPI_PARTIAL: at most this many splits (0: as many as fill the CUs)
-    int l2_local;        // workgroup i runs on XCD i % 8 (q38_gemm_l2_local()): stream-K partials stay in L2
+    int recompute;       // finish every split tile by recomputing its partials (as when contributors share no L2)
     int splits;          // EPI_PARTIAL split count (set by the launcher)
     int w4;              // weight tiles hold MXFP4 (q38_pack_fp4) rather than e4m3
     int f8;              // e4m3 weights x e5m2 activations on the FP8 MFMA (else widened to bf16 for the bf16 MFMA)
@@ -174,7 +175,6 @@ struct PickArgs {
 };
 
 hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream);
-int q38_gemm_l2_local();
 hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream);
 hipError_t q38_head_norm(const bf16_t* hidden, const bf16_t* w, float eps, int H, int rows, bf16_t* tiles, float* x32,
                          hipStream_t stream);

@@ -246,13 +246,19 @@ def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: in
     return out
 
 
+GEMM_RECOMPUTE = 4  # Q38_GEMM_RECOMPUTE
+
+
 def fp8_linear_mfma(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, mfma: str, f32_out: bool = False,
-                    scratch=None) -> torch.Tensor:
-    """The FP8 projection with its products on the named MFMA ("fp8" or "bf16"), bf16 or float32 output."""
+                    scratch=None, recompute: bool = False) -> torch.Tensor:
+    """The FP8 projection with its products on the named MFMA ("fp8" or "bf16"), bf16 or float32 output; with
+    ``recompute`` every tile split between workgroups is finished by recomputing its partials (the GEMM's path for
+    contributors on different XCDs)."""
     rows, k = x.shape
     scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.float32 if f32_out else torch.bfloat16, device=x.device)
-    check(library().q38_fp8_linear_mfma(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, PROJECTION_MFMA[mfma],
+    flags = PROJECTION_MFMA[mfma] | (GEMM_RECOMPUTE if recompute else 0)
+    check(library().q38_fp8_linear_mfma(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, flags,
                                         int(f32_out), ptr(scratch), ptr(out), stream()))
     return out
 

@@ -121,3 +121,25 @@ def test_fp8_mfma_projection_sums_within_its_accumulation_bound(gpu, rows, k, n)
         boundary = torch.minimum((exact[differ] - lo - ulp / 2).abs(), (exact[differ] - lo + ulp / 2).abs())
         assert bool((boundary <= 2.0**-14 * abs_sum[differ]).all())
     print(f"  bf16 outputs differing between the MFMAs: {int(differ.sum())} of {differ.numel()}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mfma", ["bf16", "fp8"])
+@pytest.mark.parametrize("rows,k,n", [(256, 5120, 16384), (256, 2048, 768), (128, 5120, 4096), (64, 17408, 5120), (32, 1024, 2560)])
+def test_split_tiles_finished_by_recomputation_equal_the_l2_partials(gpu, rows, k, n, mfma):
+    """The stream-K GEMM finishes a tile split between workgroups from their float32 partials in the XCD's L2; if the
+    contributors ever ran on different XCDs it recomputes every contributor's partial itself. Forced on every split
+    tile, that path gives the same bits as the partials (the same MFMAs from zero sums, added in the same order), at
+    each workgroup tile shape (128 x 256 and 256 x 256 features x tokens at 256 rows, 512 x 128 at 128, 128 x 64 at 64,
+    512 x 32 at 32) and on both MFMAs; two calls in a row leave the arrival counters at zero."""
+    g = torch.Generator().manual_seed(rows + k + n)
+    coded, scales = quantize_e4m3(torch.randn(n, k, generator=g) * 0.02)
+    tiles, words = ext.pack_weight(coded.cuda(), scales.cuda())
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).cuda()
+    scratch = ext.linear_scratch(rows, k, x.device)
+    plain = ext.fp8_linear_mfma(x, tiles, words, n, mfma, scratch=scratch)
+    redo = ext.fp8_linear_mfma(x, tiles, words, n, mfma, scratch=scratch, recompute=True)
+    again = ext.fp8_linear_mfma(x, tiles, words, n, mfma, scratch=scratch)
+    torch.cuda.synchronize()
+    assert torch.equal(plain.view(torch.int16), redo.view(torch.int16))
+    assert torch.equal(plain.view(torch.int16), again.view(torch.int16))
