@@ -151,6 +151,12 @@ int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles
  * is exact. Same scratch. */
 int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                      uint8_t* scratch, uint16_t* out, void* stream);
+/* q38_fp8_linear for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops):
+ * the same outputs, with the scratch in the library's own static device array (66.5 MiB, held by each GPU the call
+ * runs on until the process ends) instead of an argument. 1 to 64 rows, K <= 32768, n % 256 == 0; other sizes are
+ * refused. Calls share their GPU's array, so calls that overlap on one GPU race. No counterpart in the reference. */
+int q38_fp8_linear_noalloc(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                           uint16_t* out, void* stream);
 /* The same with float32 output [rows][n] (no bf16 rounding); rows in {32, 64, 128} or a multiple of 256. */
 int q38_fp8_linear_f32(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                        uint8_t* scratch, float* out, void* stream);

@@ -29,7 +29,8 @@ FLAGS = [
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["gemm.hip", "norm.hip", "gdn.hip", "attn.hip", "prefill.hip", "pick.hip", "pack.hip", "spec.hip", "engine.cpp"]
+SOURCES = ["gemm.hip", "norm.hip", "gdn.hip", "attn.hip", "prefill.hip", "pick.hip", "pack.hip", "spec.hip", "noalloc.hip",
+           "engine.cpp"]
 
 
 def _compile(src: str) -> Path:

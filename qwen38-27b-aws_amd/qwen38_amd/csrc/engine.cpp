@@ -542,6 +542,43 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
 
 }  // namespace
 
+int q38_report(const char* msg) { return fail(msg); }
+
+int q38_device_cus() { return device_cus(); }
+
+// One projection outside a handle: e5m2 tiles of x into `act` (unless x is null: act already holds them), then the
+// GEMM with its counters and partial slots at `gemm` (fix_floats floats of slots after the counters).
+int q38_projection(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
+                   uint8_t* act, uint8_t* gemm, size_t fix_floats, void* out, int splits_max, hipStream_t stream, int w4,
+                   int f8, int recompute) {
+    if (!tiles || !tile_scales || !act || !gemm || !out) return fail("null argument");
+    if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+    if (x) HIP_TRY(q38_act_tiles(x, rows, k, act, stream));
+    GemmArgs a{};
+    a.w = tiles;
+    a.ws = tile_scales;
+    a.act = act;
+    a.K = k;
+    a.N = n;
+    a.T = rows;
+    a.Tpad = pad_tokens(rows);
+    a.splits_max = splits_max;
+    a.w4 = w4;
+    a.f8 = f8;
+    a.recompute = recompute;
+    if (epi == EPI_PARTIAL)
+        a.part = (float*)out;
+    else {
+        a.out0 = out;
+        a.ld0 = n;
+        a.n0 = n;
+    }
+    gemm_scratch(a, gemm, device_cus());
+    a.fix_floats = fix_floats;
+    HIP_TRY(q38_gemm(a, epi, nullptr, stream));
+    return 0;
+}
+
 extern "C" {
 
 const char* q38_last_error(void) { return g_error.c_str(); }
@@ -745,34 +782,12 @@ size_t q38_fp8_linear_scratch(int rows, int k) { return q38_tiles_size(rows, k) 
 
 namespace {
 
-// One projection outside a handle: e5m2 tiles of x (unless x is null: the scratch already holds them), then the GEMM.
+// A projection with the caller's scratch: the input tiles, then the GEMM's counters and slots for every CU.
 int standalone(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
                uint8_t* scratch, void* out, int splits_max, hipStream_t stream, int w4 = 0, int f8 = 0, int recompute = 0) {
-    if (!tiles || !tile_scales || !scratch || !out) return fail("null argument");
-    if (rows < 1 || n % 256 || k % 256) return fail("projection needs rows >= 1, N % 256 == 0 and K % 256 == 0");
-    if (x) HIP_TRY(q38_act_tiles(x, rows, k, scratch, stream));
-    GemmArgs a{};
-    a.w = tiles;
-    a.ws = tile_scales;
-    a.act = scratch;
-    a.K = k;
-    a.N = n;
-    a.T = rows;
-    a.Tpad = pad_tokens(rows);
-    a.splits_max = splits_max;
-    a.w4 = w4;
-    a.f8 = f8;
-    a.recompute = recompute;
-    if (epi == EPI_PARTIAL)
-        a.part = (float*)out;
-    else {
-        a.out0 = out;
-        a.ld0 = n;
-        a.n0 = n;
-    }
-    gemm_scratch(a, scratch + q38_tiles_size(rows, k), device_cus());
-    HIP_TRY(q38_gemm(a, epi, nullptr, stream));
-    return 0;
+    if (!scratch) return fail("null argument");
+    return q38_projection(x, rows, k, tiles, tile_scales, n, epi, scratch, scratch + q38_tiles_size(rows, k),
+                          (size_t)2 * device_cus() * GEMM_SLOT_FLOATS, out, splits_max, stream, w4, f8, recompute);
 }
 
 }  // namespace

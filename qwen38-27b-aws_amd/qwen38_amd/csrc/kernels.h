@@ -210,6 +210,14 @@ hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, u
 hipError_t q38_pack_fp4(const uint8_t* packed, const uint8_t* scales, int N, int K, uint8_t* tiles, uint8_t* tile_scales,
                         hipStream_t stream);
 hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);
+
+// Host helpers of the C ABI (engine.cpp): the thread's q38_last_error message (returns 1), the device's CUs, and one
+// projection outside a handle (input tiles into act, GEMM counters then fix_floats floats of partial slots at gemm).
+int q38_report(const char* msg);
+int q38_device_cus();
+int q38_projection(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
+                   uint8_t* act, uint8_t* gemm, size_t fix_floats, void* out, int splits_max, hipStream_t stream, int w4,
+                   int f8, int recompute);
 hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
                            hipStream_t s);
 hipError_t q38_select_rows(const bf16_t* rows, const int* idx, int B, int K, int H, bf16_t* out, hipStream_t s);

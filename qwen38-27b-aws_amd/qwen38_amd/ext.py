@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
     "q38_kernel_timer",
 )
 
@@ -71,6 +71,7 @@ def library() -> ctypes.CDLL:
     lib.q38_fp8_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_fp8_linear_mfma.argtypes = [p, i, i, p, p, i, i, i, p, p, p]
+    lib.q38_fp8_linear_noalloc.argtypes = [p, i, i, p, p, i, p, p]
     lib.q38_mlp_up.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_tiles_size.argtypes = [i, i]
     lib.q38_kernel_timer.argtypes = [p, i, ctypes.POINTER(i), ctypes.POINTER(ctypes.c_float)]
@@ -243,6 +244,14 @@ def fp8_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: in
     scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
     check(library().q38_fp8_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def fp8_linear_noalloc(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, out=None) -> torch.Tensor:
+    """`fp8_linear` with the library's static scratch (no device allocation by the library): 1 to 64 rows."""
+    rows, k = x.shape
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device) if out is None else out
+    check(library().q38_fp8_linear_noalloc(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(out), stream()))
     return out
 
 
