@@ -109,7 +109,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                   "weight stage splits evenly over the waves, each load inside one tile");
     static_assert(SC_CHUNKS >= 1 && NW % SC_CHUNKS == 0, "scale stage splits evenly over the waves");
     static_assert(OPS * (S - 2) <= 63 && S >= 2, "vmcnt range");
-    static_assert(EPI != EPI_SWIGLU || FR == 2, "gate and up tiles pair up");
+    static_assert(EPI != EPI_SWIGLU || FR % 2 == 0, "gate and up tiles pair up");
     static_assert(!F8 || (A8 && !W4), "the FP8 MFMA takes e4m3 weight tiles and e5m2 activation tiles");
     constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
@@ -295,20 +295,23 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                     }
                 }
             } else if constexpr (EPI == EPI_SWIGLU) {
+                // Feature tiles 2p and 2p + 1 are the gate and up rows of the same 32 inner features.
                 const int inner = a.N >> 1;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    float h[4];
+                for (int pr = 0; pr < FR / 2; ++pr)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float gv = rbf(acc[0][t][g * 4 + e]), uv = rbf(acc[1][t][g * 4 + e]);
-                        const float act = rbf(gv * rbf(sigmoidf_(gv)));
-                        h[e] = rbf(act * uv);
+                    for (int g = 0; g < 4; ++g) {
+                        float h[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float gv = rbf(acc[2 * pr][t][g * 4 + e]), uv = rbf(acc[2 * pr + 1][t][g * 4 + e]);
+                            const float act = rbf(gv * rbf(sigmoidf_(gv)));
+                            h[e] = rbf(act * uv);
+                        }
+                        const uint32_t packed = pk_e5m2(h[0], h[1], h[2], h[3]);
+                        const int col = ((ft0 >> 1) + pr) * 32 + g * 8 + rowq;
+                        *(uint32_t*)((uint8_t*)a.out0 + act_offset(tok, col, inner)) = packed;
                     }
-                    const uint32_t packed = pk_e5m2(h[0], h[1], h[2], h[3]);
-                    const int col = (ft0 >> 1) * 32 + g * 8 + rowq;
-                    *(uint32_t*)((uint8_t*)a.out0 + act_offset(tok, col, inner)) = packed;
-                }
             } else if constexpr (EPI == EPI_PARTIAL) {
                 float* dst = a.part + ((size_t)z * a.Tpad + tok) * a.N;
 #pragma unroll
