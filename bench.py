@@ -4,8 +4,9 @@
 One step = the reference's Scheduler._verify_step with MTP drafts (qwen38_inf2/scheduler.py:160-193, 269-301) for
 all 64 rows: 3 MTP calls and 3 one-group head passes to draft 3 tokens per row, the 64-layer verify of 4 tokens per
 row (512-token contexts), the head's group maxima and exact top-4-group recheck over 256 rows, greedy acceptance and
-the state advance. It runs as one library call, `q38_spec_step`, on torch's current HIP stream; inputs and state are
-resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
+the state advance. It runs as one library call, `q38_spec_step_graph` (the step captured once per gated-delta parity
+as a HIP graph and replayed), on torch's current HIP stream; `ms_per_step_launches` is the same step as individual
+launches (`q38_spec_step`). Inputs and state are resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill] [--mxfp4] [--kv-fp8]
@@ -305,6 +306,7 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_launches": round(ms_launches, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -510,26 +512,35 @@ def main() -> int:
         print(json.dumps(result), flush=True)
         return 0
 
-    def step():
+    def step(graph: bool = True):
         engine.handle.spec_step(st["position"], st["index"], st["match"], st["accepted"], st["active"], st["hidden"],
-                                st["picks"], st["drafts"])
+                                st["picks"], st["drafts"], graph=graph)
 
+    def timed(graph: bool) -> tuple[float, int]:
+        start_pos = st["position"].clone()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            step(graph)
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / args.steps, int((st["position"] - start_pos).sum())
+
+    # Warmup as launches, then the captured graph's first use for each gated-delta parity (capture + instantiate).
     for i in range(args.warmup):
-        step()
+        step(graph=False)
         torch.cuda.synchronize()
         log(f"warmup step {i + 1}/{args.warmup} done")
-    start_pos = st["position"].clone()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(2):
+        step(graph=True)
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    end.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    accepted = int((st["position"] - start_pos).sum())
+    log("graph captured for both gated-delta parities")
+    ms, accepted = timed(graph=True)
     value = accepted / (ms * args.steps / 1000.0)
-    log(f"{ms:.3f} ms/step, {accepted} accepted tokens over {args.steps} steps")
+    log(f"{ms:.3f} ms/step as one HIP graph per step, {accepted} accepted tokens over {args.steps} steps")
+    ms_launches, _ = timed(graph=False)
+    log(f"{ms_launches:.3f} ms/step as individual launches")
 
     # The dominant kernel inside real steps: the same number of steps again with HIP events around every gate/up GEMM
     # launch on the step's stream (64 layers + 3 MTP calls per step).
@@ -551,6 +562,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_launches": round(ms_launches, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -234,6 +234,13 @@ int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const
  * embeddings and a bound "rope_table" (bf16 [max_seq_len][2][rotary_dim]: cos then sin of each position). */
 int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
                   uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
+/* q38_spec_step as one HIP graph: the step is captured on first use for the current gated-delta parity and these
+ * argument pointers (at most one graph per parity is kept; other pointers, or any q38_bind, capture again) and
+ * replayed with hipGraphLaunch on `stream`, the host's parity flipping as after q38_spec_step. The same kernels with
+ * the same arguments, so the same results. While the kernel timer is on or a probe is bound it runs q38_spec_step.
+ * No counterpart in the reference (its step is one compiled Neuron graph per shape). */
+int q38_spec_step_graph(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted,
+                        const float* active, uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
 
 /* Measurement hook, with no counterpart in the reference (for benchmarks that time one kernel inside the step):
  * on != 0 starts bracketing every gate/up projection GEMM launched by q38_verify, q38_mtp_step and q38_spec_step with

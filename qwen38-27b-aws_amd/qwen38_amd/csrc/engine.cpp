@@ -101,8 +101,21 @@ struct q38_handle {
     int timer_used = 0;
     bool timer_on = false;
     int act_h_k;  // width of act_h: 2H with the MTP layer (its fc input), else H
+    // q38_spec_step_graph: the step captured once per gated-delta parity (the two halves give different kernel
+    // arguments), for the argument pointers it was captured with; a private stream to capture on.
+    struct StepGraph {
+        hipGraphExec_t exec = nullptr;
+        const void* args[8] = {};
+    } graphs[2];
+    hipStream_t capture_stream = nullptr;
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
+    void drop_graphs() {
+        for (StepGraph& g : graphs) {
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+            g = StepGraph{};
+        }
+    }
 };
 
 namespace {
@@ -694,6 +707,8 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
 void q38_destroy(q38_handle* h) {
     if (!h) return;
     for (hipEvent_t e : h->timer_events) (void)hipEventDestroy(e);
+    h->drop_graphs();
+    if (h->capture_stream) (void)hipStreamDestroy(h->capture_stream);
     delete h;
 }
 
@@ -745,6 +760,7 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
     b.p = dev_ptr;
     b.n = nbytes;
     (layer < 0 ? h->global : h->layer[layer])[name] = b;
+    h->drop_graphs();  // captured steps hold the old pointers
     return 0;
 }
 
@@ -1123,6 +1139,47 @@ int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* mat
     if (q38_head_pick(h, hidden, B * K, 4, picks, stream_)) return 1;
     HIP_TRY(q38_accept(picks, drafts, active, B, K, match, accepted, stream));
     HIP_TRY(q38_advance(position, index, accepted, B, stream));
+    return 0;
+}
+
+int q38_spec_step_graph(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted,
+                        const float* active, uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream_) {
+    if (!h || !position || !index || !match || !accepted || !active || !hidden || !picks || !drafts)
+        return fail("null argument");
+    hipStream_t stream = (hipStream_t)stream_;
+    // The kernel timer records events and the probe copies per call: those steps run as launches.
+    bool probed = false;
+    for (const auto& l : h->layer) probed = probed || l.count("probe");
+    if (h->timer_on || probed)
+        return q38_spec_step(h, position, index, match, accepted, active, hidden, picks, drafts, stream_);
+    const int parity = h->parity;
+    q38_handle::StepGraph& g = h->graphs[parity];
+    const void* args[8] = {position, index, match, accepted, active, hidden, picks, drafts};
+    if (!g.exec || memcmp(g.args, args, sizeof(args))) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        g = q38_handle::StepGraph{};
+        if (!h->capture_stream) HIP_TRY(hipStreamCreateWithFlags(&h->capture_stream, hipStreamNonBlocking));
+        // Capturing runs nothing: the recorded step starts from the current parity, and so does the state after it.
+        HIP_TRY(hipStreamBeginCapture(h->capture_stream, hipStreamCaptureModeThreadLocal));
+        const int rc = q38_spec_step(h, position, index, match, accepted, active, hidden, picks, drafts, h->capture_stream);
+        hipGraph_t graph = nullptr;
+        const hipError_t e = hipStreamEndCapture(h->capture_stream, &graph);
+        h->parity = parity;
+        if (rc) {
+            if (e == hipSuccess && graph) (void)hipGraphDestroy(graph);
+            return 1;
+        }
+        HIP_TRY(e);
+        const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ei != hipSuccess) {
+            g.exec = nullptr;
+            return fail(std::string("hipGraphInstantiate: ") + hipGetErrorString(ei));
+        }
+        memcpy(g.args, args, sizeof(args));
+    }
+    HIP_TRY(hipGraphLaunch(g.exec, stream));
+    h->parity = 1 - parity;
     return 0;
 }
 

@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph",
     "q38_kernel_timer",
 )
 
@@ -86,6 +86,7 @@ def library() -> ctypes.CDLL:
     lib.q38_embed.argtypes = [p, p, i, p, p]
     lib.q38_accept.argtypes = [p, p, p, p, p, p, p]
     lib.q38_spec_step.argtypes = [p] * 10
+    lib.q38_spec_step_graph.argtypes = [p] * 10
     for name in EXPORTS:
         if name not in ("q38_last_error", "q38_destroy"):
             getattr(lib, name).restype = ctypes.c_size_t if name in ("q38_fp8_linear_scratch", "q38_tiles_size") else ctypes.c_int
@@ -202,8 +203,10 @@ class Handle:
     def accept(self, picks, drafts, active, match, accepted) -> None:
         check(self.lib.q38_accept(self.h, *map(ptr, (picks, drafts, active, match, accepted)), stream()))
 
-    def spec_step(self, position, index, match, accepted, active, hidden, picks, drafts) -> None:
-        check(self.lib.q38_spec_step(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
+    def spec_step(self, position, index, match, accepted, active, hidden, picks, drafts, graph: bool = False) -> None:
+        """One speculative step on the device (`q38_spec_step`), or its captured HIP graph (`q38_spec_step_graph`)."""
+        fn = self.lib.q38_spec_step_graph if graph else self.lib.q38_spec_step
+        check(fn(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
 
     def kernel_timer(self, on: bool) -> tuple[int, float]:
         """Start (on) or stop bracketing the gate/up GEMM launches with HIP events; stopping returns (launches, total

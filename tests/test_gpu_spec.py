@@ -213,3 +213,33 @@ def test_device_step_against_the_cpu_oracle_from_the_devices_state(spec):
     print(f"picks agree {picks_same}/{picks_n} ({identical} from bit-identical hidden states), drafts {drafts_same}/{drafts_n}", flush=True)
     assert identical >= picks_n // 2
     assert picks_same >= 0.9 * picks_n and drafts_same >= 0.9 * drafts_n
+
+
+@pytest.mark.gpu
+def test_graph_replays_of_the_step_equal_its_launches(spec):
+    """`q38_spec_step_graph` (the step captured once per gated-delta parity, then replayed) against `q38_spec_step`
+    on a second engine from the same state: after every one of five steps, with eager work and synchronisations between
+    the replays, the drafts, picks, matches, accepted counts, positions, indices and verify hidden states are equal bit
+    for bit, and so is every state buffer at the end."""
+    cfg, values = spec
+    eager_engine, _ = load_engine(cfg, values)
+    graph_engine, _ = load_engine(cfg, values)
+    eager, graph = DeviceStep(cfg, eager_engine), DeviceStep(cfg, graph_engine)
+    for n in range(SPEC["steps"]):
+        print(f"step {n}", flush=True)
+        eager()
+        graph.engine.handle.spec_step(graph.position, graph.index, graph.match, graph.accepted, graph.active, graph.hidden,
+                                      graph.picks, graph.drafts, graph=True)
+        torch.cuda.synchronize()
+        _ = torch.ones(1024, device="cuda").sum().item()  # eager work between replays
+        for name in ("drafts", "picks", "match", "accepted", "position", "index", "hidden"):
+            assert torch.equal(getattr(eager, name), getattr(graph, name)), (n, name)
+        assert eager_engine.handle.parity == graph_engine.handle.parity
+    for i, kind in enumerate(cfg.layer_types):
+        if kind == "linear_attention":
+            got, want = graph_engine.gdn_state(i), eager_engine.gdn_state(i)
+            for key in got:
+                assert torch.equal(got[key], want[key]), (i, key)
+        else:
+            for a, b in zip(graph_engine.get_kv(i), eager_engine.get_kv(i)):
+                assert torch.equal(a, b), i
