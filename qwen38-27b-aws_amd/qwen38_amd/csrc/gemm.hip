@@ -14,10 +14,11 @@
 // on the other neighbour of the reference's, and the reference's e5m2 rounding at every projection input amplifies
 // such last-bit differences to several percent per layer. The bf16 MFMA is the default.
 //
-// Data movement. A workgroup owns a (WF*FR*32 features) x (WT*TR*32 tokens) output tile; every K-step of 64 inputs, its
-// weight tiles (2 KiB of e4m3, or 1 KiB of E2M1 in the same element order), their scales and its activation tiles go straight from global memory into one stage of an S-deep LDS
-// ring (global_load_lds, no VGPR staging), S-1 K-steps ahead of the MFMAs. One barrier per K-step: the stage a wave
-// loads into is the one every wave finished reading before that barrier. Weight and activation tiles are both
+// Data movement. A workgroup owns a (WF*FR*32 features) x (WT*TR*32 tokens) output tile; for every unit of KU K-steps
+// of 64 inputs, its weight tiles (2 KiB of e4m3, or 1 KiB of E2M1 in the same element order per K-step), their scales
+// and its activation tiles go straight from global memory into one stage of an S-deep LDS ring (global_load_lds, no
+// VGPR staging), S-1 units ahead of the MFMAs. One barrier per unit: the stage a wave loads into is the one every wave
+// finished reading before that barrier. Weight and activation tiles are both
 // MFMA-step-major (common.h), so every operand read is 8 (or 16) contiguous bytes per lane, free of bank conflicts.
 //
 // Schedule. Workgroups are persistent, one per CU. For outputs that need complete sums the (feature tile, K-step) units
@@ -92,18 +93,19 @@ __device__ __forceinline__ v8bf widen_e2m1(uint32_t w, float scale) {
     return __builtin_bit_cast(v8bf, r);
 }
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8>
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8, int KU>
 __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a) {
     constexpr int NW = WF * WT, NTH = NW * 64;
     constexpr int TT = WT * TR, FT = WF * FR;  // 32-token and 32-feature tiles per workgroup
     constexpr int AT = A8 ? 2048 : 4096;       // bytes of one activation tile (32 tokens x 64 inputs)
     constexpr int WTB = W4 ? 1024 : 2048;      // bytes of one weight tile (32 features x 64 inputs)
     constexpr int ACT_B = TT * AT, W_B = FT * WTB, SC_B = FT * 64;
-    constexpr int STAGE = ACT_B + W_B + SC_B;
+    constexpr int SUB = ACT_B + W_B + SC_B;  // one K-step of 64 inputs
+    constexpr int STAGE = KU * SUB;           // a unit: KU consecutive K-steps
     constexpr int ACT_DMA = ACT_B >= NW * 1024 ? 16 : 4;  // bytes per lane of one activation load
     constexpr int W_DMA = W_B >= NW * 1024 ? 16 : 4;      // bytes per lane of one weight load
     constexpr int N_ACT = ACT_B / (NW * 64 * ACT_DMA), N_W = W_B / (NW * 64 * W_DMA), SC_CHUNKS = SC_B / 256;
-    constexpr int OPS = N_ACT + N_W + 1;  // loads per wave per stage
+    constexpr int OPS = KU * (N_ACT + N_W + 1);  // loads per wave per stage
     static_assert(N_ACT >= 1 && N_ACT * NW * 64 * ACT_DMA == ACT_B, "activation stage splits evenly over the waves");
     static_assert(N_W >= 1 && N_W * NW * 64 * W_DMA == W_B && WTB % (64 * W_DMA) == 0,
                   "weight stage splits evenly over the waves, each load inside one tile");
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: addresses stay in scalar registers
     const int wf = wave % WF, wt = wave / WF;
-    const int KS = a.K >> 6;
+    const int KS64 = a.K >> 6, KS = KS64 / KU;  // K-steps of 64 inputs, units of KU K-steps
     const int NF = a.N / (FT * 32), NTB = a.Tpad / (TT * 32);
 
     // Workgroup -> (group, token block). Workgroups are dealt to the 8 XCDs round-robin, so workgroups with equal
@@ -159,26 +161,30 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
     // Loads of one stage. Each wave moves N_ACT activation chunks, N_W weight chunks of 64 * W_DMA bytes and one scale
     // chunk of 256 bytes (waves with the same chunk index load identical bytes to the same place).
-    const uint8_t* act_base = (const uint8_t*)a.act + (size_t)tb * TT * KS * AT;
+    const uint8_t* act_base = (const uint8_t*)a.act + (size_t)tb * TT * KS64 * AT;
     const int sc_c = wave % SC_CHUNKS;
-    const uint32_t sc_lane = (uint32_t)((lane >> 4) * KS * 64 + (lane & 15) * 4);
+    const uint32_t sc_lane = (uint32_t)((lane >> 4) * KS64 * 64 + (lane & 15) * 4);
     const uint32_t lds_addr = (uint32_t)(uintptr_t)LDS_PTR(lds);
     auto issue = [&](int fb, int k, int st) {
-        const uint32_t sb = lds_addr + st * STAGE;
 #pragma unroll
-        for (int j = 0; j < N_ACT; ++j) {
-            const int off = (j * NW + wave) * (64 * ACT_DMA);
-            const uint8_t* g = act_base + ((size_t)(off / AT) * KS + k) * AT + off % AT;
-            lds_load<ACT_DMA>(g + lane * ACT_DMA, sb + off);
-        }
+        for (int j = 0; j < KU; ++j) {
+            const int k64 = k * KU + j;
+            const uint32_t sb = lds_addr + st * STAGE + j * SUB;
 #pragma unroll
-        for (int j = 0; j < N_W; ++j) {
-            const int off = (j * NW + wave) * (64 * W_DMA);
-            const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS + k) * WTB + off % WTB;
-            lds_load<W_DMA>(g + lane * W_DMA, sb + ACT_B + off);
+            for (int i = 0; i < N_ACT; ++i) {
+                const int off = (i * NW + wave) * (64 * ACT_DMA);
+                const uint8_t* g = act_base + ((size_t)(off / AT) * KS64 + k64) * AT + off % AT;
+                lds_load<ACT_DMA>(g + lane * ACT_DMA, sb + off);
+            }
+#pragma unroll
+            for (int i = 0; i < N_W; ++i) {
+                const int off = (i * NW + wave) * (64 * W_DMA);
+                const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS64 + k64) * WTB + off % WTB;
+                lds_load<W_DMA>(g + lane * W_DMA, sb + ACT_B + off);
+            }
+            const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS64 + k64) * 64;
+            lds_load<4>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
         }
-        const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS + k) * 64;
-        lds_load<4>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
     };
 
     v16f acc[FR][TR];
@@ -195,8 +201,8 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     // fragments: inputs 16 (l / 32) + [0, 16) and 32 + 16 (l / 32) + [0, 16), the operand order of
     // v_mfma_scale_f32_32x32x64_f8f6f4), the lane's E8M0 byte for (row l % 32, MX block l / 32) as the weight scale, the
     // activation tile's 32 bytes the same way with scale 1 (127).
-    auto compute_f8 = [&](int st) __attribute__((always_inline)) {
-        const uint8_t* sb = lds + st * STAGE;
+    auto compute_f8 = [&](int st, int j) __attribute__((always_inline)) {
+        const uint8_t* sb = lds + st * STAGE + j * SUB;
         const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * 8;
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2 + (lane >> 5);
         v8i wv[FR];
@@ -228,12 +234,12 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
     // One K-step: per MFMA step m, each weight fragment is 8 contiguous bytes (4 for E2M1) per lane, each activation
     // fragment 8 (16 for bf16 activations).
-    auto compute = [&](int st) __attribute__((always_inline)) {
+    auto compute_sub = [&](int st, int j) __attribute__((always_inline)) {
         if constexpr (F8) {
-            compute_f8(st);
+            compute_f8(st, j);
             return;
         }
-        const uint8_t* sb = lds + st * STAGE;
+        const uint8_t* sb = lds + st * STAGE + j * SUB;
         const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * (WTB / 256);
         const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
         float scl[FR][2];  // 2^(scale byte - 127) of the K-step's two MX blocks (inputs 0-31, 32-63)
@@ -270,6 +276,10 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                 for (int f = 0; f < FR; ++f) acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[f], xb, acc[f][t], 0, 0, 0);
             }
         }
+    };
+    auto compute = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < KU; ++j) compute_sub(st, j);
     };
 
     // Accumulator layout of a 32x32 MFMA: lane l holds token column l % 32 and feature rows
@@ -490,12 +500,13 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 
 constexpr int MIN_UNITS = 8;  // smallest K range worth a stream-K group
 
-template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8>
+template <int WF, int WT, int FR, int TR, bool A8, int S, int EPI, bool W4, bool F8, int KU = 1>
 hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
     GemmArgs a = a0;
     constexpr int BF = WF * FR * 32, BT = WT * TR * 32, NTH = WF * WT * 64;
     if (a.N % BF || a.Tpad % BT || a.K % 64 || a.cus < 1) return hipErrorInvalidValue;
-    const int NF = a.N / BF, NTB = a.Tpad / BT, KS = a.K / 64;
+    if (a.K % (64 * KU)) return hipErrorInvalidValue;
+    const int NF = a.N / BF, NTB = a.Tpad / BT, KS = a.K / (64 * KU);
     int grid;
     if (EPI == EPI_PARTIAL) {
         int s = a.cus / (NF * NTB);
@@ -530,7 +541,7 @@ hipError_t launch(const GemmArgs& a0, int* splits_out, hipStream_t stream) {
         a.splits = 1;
     }
     if (splits_out) *splits_out = a.splits;
-    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI, W4, F8>), dim3(grid), dim3(NTH), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<WF, WT, FR, TR, A8, S, EPI, W4, F8, KU>), dim3(grid), dim3(NTH), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -543,7 +554,14 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
     if (a.Tpad % 256 == 0) {
         if constexpr (A8) {
             // bf16 outputs: 128 x 128 tiles, two token blocks per weight tile on one XCD (their stream-K ranges split
-            // fewer tiles; measured 4-8 % faster on the 16384- and 14336-wide projections than 128 x 256).
+            // fewer tiles; measured 4-8 % faster on the 16384- and 14336-wide projections than 128 x 256). Units of
+            // two K-steps (128 inputs) per ring stage when K allows: half the barriers and waits per MFMA, measured
+            // 6-8 % faster on every projection of the 27B verify step than one K-step per stage with deeper rings.
+            if (a.K % 128 == 0) {
+                if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 3, EPI, W4, F8, 2>(a, splits_out, stream);
+                if (balanced(128) || (a.N % 256 && a.N % 128 == 0))
+                    return launch<2, 4, 2, 2, true, 3, EPI, W4, F8, 2>(a, splits_out, stream);
+            }
             if (EPI == EPI_BF16 && balanced(128)) return launch<2, 4, 2, 1, true, 9, EPI, W4, F8>(a, splits_out, stream);
             if (balanced(128) || (a.N % 256 && a.N % 128 == 0)) return launch<2, 4, 2, 2, true, 6, EPI, W4, F8>(a, splits_out, stream);
             return launch<4, 2, 2, 4, true, 4, EPI, W4, F8>(a, splits_out, stream);
