@@ -141,10 +141,10 @@ def model_weights(directory: str | Path, cfg: TextConfig, weight_format: str = "
         yield from mtp_weights(Checkpoint(Path(directory) / MTP_FILE, exclude=()))
 
 
-def kv_scales(directory: str | Path, cfg: TextConfig) -> dict[int, tuple[torch.Tensor, torch.Tensor]]:
+def kv_scales(directory, cfg: TextConfig) -> dict[int, tuple[torch.Tensor, torch.Tensor]]:
     """Each attention layer's (k_scale, v_scale), bf16 ``[1]``, stretched for the cache's 240 limit (reference
-    checkpoint.py:227-233)."""
-    ck = Checkpoint(directory)
+    checkpoint.py:227-233). ``directory`` may also be an open `Checkpoint` (anything with ``get(name)``)."""
+    ck = directory if hasattr(directory, "get") else Checkpoint(directory)
     out = {}
     for i, kind in enumerate(cfg.layer_types):
         if kind == FULL:
