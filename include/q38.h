@@ -215,6 +215,9 @@ int q38_mtp_step(q38_handle* h, const uint16_t* hidden, const uint16_t* embeds, 
  * them itself and writes ids int32 [R] (-1: no finite logit) after rechecking the best `groups` (1..4) groups. */
 int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* maxima, void* stream);
 int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, int32_t* ids, void* stream);
+/* (q38_head_pick rechecks the best groups against lm_head's bf16 rows when the optional global buffer
+ * "head.lm_head.rows" (bf16 [V][H], the checkpoint's lm_head) is bound, as the reference's ChipHead rechecks against
+ * the checkpoint's rows (generate.py:196-206); without it, against the e4m3 tiles dequantized exactly.) */
 
 /* Embedding rows for ids int32 [n] into bf16 [n][H]. */
 int q38_embed(q38_handle* h, const int32_t* ids, int n, uint16_t* out, void* stream);

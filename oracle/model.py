@@ -652,14 +652,17 @@ def head_group_maxima(cfg, norm_weight, lm_head: FP8Weight, hidden, group_rows: 
     return torch.stack([g.amax(dim=-1) for g in logits.split(group_rows, dim=-1)], dim=-1)
 
 
-def chip_next_tokens(cfg, norm_weight, lm_head: FP8Weight, hidden, maxima, recheck_groups: int = 4, group_rows: int = 32):
+def chip_next_tokens(cfg, norm_weight, lm_head: FP8Weight, hidden, maxima, recheck_groups: int = 4, group_rows: int = 32,
+                     rows_bf16: torch.Tensor | None = None):
     """`ChipHead.next_tokens` after the graph (generate.py:194-208): the best ``recheck_groups`` groups by maxima,
-    exact float32 logits inside them from float32-normed hidden, the first strictly larger in top-k order wins."""
+    exact float32 logits inside them from float32-normed hidden, the first strictly larger in top-k order wins. The
+    reference rechecks against the checkpoint's bf16 lm_head (its ``self.lm_head``); ``rows_bf16`` is that matrix
+    [V, H], else the FP8 weight's values stand in for it (a synthetic lm_head that is e4m3 to begin with)."""
     rows = hidden.shape[0]
     maxima = maxima[:rows].float()
     best_groups = maxima.topk(min(recheck_groups, maxima.shape[-1]), dim=-1).indices.tolist()
     norm = rms_norm(hidden.float(), norm_weight, cfg.rms_norm_eps).squeeze(1)
-    dense = lm_head.dense().contiguous().to(torch.bfloat16)
+    dense = lm_head.dense().contiguous().to(torch.bfloat16) if rows_bf16 is None else rows_bf16
     tokens = []
     for row, groups in enumerate(best_groups):
         best_token, best_logit = -1, -torch.inf

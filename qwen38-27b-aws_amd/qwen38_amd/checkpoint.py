@@ -102,10 +102,13 @@ def layer_weights(ck: Checkpoint, cfg: TextConfig, index: int, weight_format: st
 
 
 def head_weights(ck: Checkpoint) -> list[tuple[str, object]]:
-    """Final norm, lm_head (e4m3 + E8M0) and the embedding table (reference checkpoint.py:324-342)."""
+    """Final norm, lm_head (e4m3 + E8M0 for the group maxima, and its bf16 rows for the exact recheck, which the
+    reference reads from the checkpoint: generate.py:196-206) and the embedding table (reference checkpoint.py:324-342)."""
+    lm_head = ck.get(LM_HEAD).to(torch.bfloat16)
     return [
         ("head.norm_weight", ck.get(FINAL_NORM).to(torch.bfloat16)),
-        ("head.lm_head", e4m3_from_bf16(ck.get(LM_HEAD))),
+        ("head.lm_head", e4m3_from_bf16(lm_head)),
+        ("head.lm_head_rows", lm_head),
         ("embed_tokens", ck.get(EMBED_TOKENS).to(torch.bfloat16)),
     ]
 

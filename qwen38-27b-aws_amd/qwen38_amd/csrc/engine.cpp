@@ -172,6 +172,7 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     if (layer == -1) {
         if (name == "head.norm") return H * 2;
         if ((r = fp8("head.lm_head", V, H))) return r;
+        if (name == "head.lm_head.rows") return V * H * 2;
         if (name == "embed_tokens") return V * H * 2;
         if (name == "rope_table") return S * 2 * 64 * 2;
         if (name == "workspace") return h->workspace_bytes;
@@ -1083,6 +1084,7 @@ int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, i
     a.x32 = (const float*)h->ws(h->off_x32);
     a.w = wt;
     a.ws = wsc;
+    a.rows = h->global.count("head.lm_head.rows") ? (const bf16_t*)h->global.at("head.lm_head.rows").p : nullptr;
     a.H = h->H;
     a.R = rows;
     a.groups = groups;

@@ -170,6 +170,7 @@ struct PickArgs {
     const float* x32;      // [R][H]
     const uint8_t* w;      // lm_head tiles [V/32][H/64][64][32]
     const uint8_t* ws;     // lm_head scales [V/32][H/64][32][2]
+    const bf16_t* rows;    // lm_head's bf16 rows [V][H] for the recheck, or null (then the tiles, dequantized)
     int H, R, groups;
     int* ids;              // [R]
 };

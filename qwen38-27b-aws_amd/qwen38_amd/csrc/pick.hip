@@ -1,7 +1,8 @@
 // Token choice from the head's group maxima: `ChipHead.next_tokens` after its graph (reference
 // qwen38_inf2/generate.py:186-208), on the GPU so only ids go back to the host.
 //   1. the `groups` best groups of 32 vocabulary rows by group maximum (torch.topk order: largest first);
-//   2. exact float32 logits of their rows against the float32-normed hidden state (lm_head rows dequantized exactly);
+//   2. exact float32 logits of their rows against the float32-normed hidden state: lm_head's bf16 rows when they are
+//      bound (the checkpoint's own rows, which the reference rechecks against), else the e4m3 tiles dequantized;
 //   3. the best row of each group, and across groups the first strictly larger in top-k order.
 // A row with no finite logit gets id -1, which the host turns into the reference's FloatingPointError.
 // Greedy acceptance (scheduler.py:291-300) is here too, for the on-device speculative step.
@@ -96,7 +97,28 @@ __global__ __launch_bounds__(PICK_THREADS) void head_pick_kernel(const PickArgs 
     if (gk < G) {
         const int grp = li[0][gk];
         float acc = 0.0f;
-        if (grp >= 0 && grp < a.ngroups) {
+        if (grp >= 0 && grp < a.ngroups && a.rows) {
+            // bf16 row grp * 32 + l % 32; lane half h reads inputs [16h, 16h + 16) and [32 + 16h, 48 + 16h) of each
+            // K-step, 32 bytes each (the two half-waves together cover 128 contiguous bytes of the row).
+            const bf16_t* wr = a.rows + ((size_t)grp * 32 + (lane & 31)) * a.H + (lane >> 5) * 16;
+            const float* xp = xrow + (lane >> 5) * 16;
+            const int k0 = sp * KS / SPL, k1 = (sp + 1) * KS / SPL;
+#pragma unroll 2
+            for (int ks = k0; ks < k1; ++ks) {
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+                    const uint4* src = (const uint4*)(wr + ks * 64 + blk * 32);
+                    const uint4 q0 = src[0], q1 = src[1];
+                    const uint32_t wv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    const float* xv = xp + ks * 64 + blk * 32;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        acc += __uint_as_float(wv[e] << 16) * xv[2 * e];
+                        acc += __uint_as_float(wv[e] & 0xffff0000u) * xv[2 * e + 1];
+                    }
+                }
+            }
+        } else if (grp >= 0 && grp < a.ngroups) {
             const uint8_t* tile = a.w + (size_t)grp * KS * 2048 + lane * 8;
             const uint8_t* sc = a.ws + (size_t)grp * KS * 64 + (lane & 31) * 2;
             const float* xp = xrow + (lane >> 5) * 16;

@@ -157,6 +157,9 @@ class Engine:
                 self.bind("head.norm", -1, value)
             elif name == "head.lm_head":
                 self._fp8("head.lm_head", -1, *value)
+            elif name == "head.lm_head_rows":
+                # The checkpoint's bf16 lm_head: the head's exact recheck reads these rows (the maxima use the tiles).
+                self.bind("head.lm_head.rows", -1, value)
             elif name == "embed_tokens":
                 self.bind("embed_tokens", -1, value)
             else:

@@ -75,7 +75,9 @@ def fake_model(tmp_path):
 def test_checkpoint_reader_yields_the_engine_names_and_the_checkpoints_own_bytes(tmp_path):
     cfg, values, scales = fake_model(tmp_path)
     got = dict(ckpt.model_weights(tmp_path, cfg, "mxfp4"))
-    assert set(got) == set(values)
+    # lm_head also comes as the file's own bf16 rows, which the head's exact recheck reads.
+    assert set(got) == set(values) | {"head.lm_head_rows"}
+    assert torch.equal(got["head.lm_head_rows"], dequantize_e4m3(*values["head.lm_head"]).to(torch.bfloat16))
     for name, want in values.items():
         value = got[name]
         if name.startswith("layers.") and isinstance(want, tuple):

@@ -86,10 +86,13 @@ def test_head_embeddings_and_kv_scales(cfg, header, monkeypatch):
                                    torch.empty(w.shape[0], w.shape[1] // 32, dtype=torch.uint8, device="meta")))
     got = dict(checkpoint.head_weights(source))
     specs = {s.name: s for s in synth.head_specs(cfg)}
-    assert set(got) == set(specs)
+    # Besides the engine's head weights, lm_head's bf16 rows for the exact recheck.
+    assert set(got) == set(specs) | {"head.lm_head_rows"}
     for name, spec in specs.items():
         value = got[name][0] if spec.kind == "fp8" else got[name]
         assert tuple(value.shape) == tuple(spec.shape), name
+    assert got["head.lm_head_rows"].dtype == torch.bfloat16
+    assert tuple(got["head.lm_head_rows"].shape) == (cfg.vocab_size, cfg.hidden_size)
     scales = checkpoint.kv_scales(source, cfg)
     assert sorted(scales) == [i for i, kind in enumerate(cfg.layer_types) if kind == FULL]
     assert all(tuple(k.shape) == (1,) and tuple(v.shape) == (1,) for k, v in scales.values())
