@@ -207,7 +207,44 @@ def cpu_baseline(cfg_block, batch: int, tokens: int, max_seq_len: int, context: 
         om.step_verify(cfg_block, layers, states, x, inp["cos"], inp["sin"], inp["position"], inp["active"], inp["accepted"])
         times.append(time.perf_counter() - started)
         log(f"cpu block {times[-1]:.2f}s")
-    step = times[-1] * n_blocks
+    del layers, states, values
+
+    # The MTP layer: one call over the B x K rows, three per step (the device step calls it with every row's K slots).
+    mtp_vals = {}
+    for spec in synth.mtp_specs(cfg_block) + [s for s in synth.head_specs(cfg_block) if s.name == "head.norm_weight"]:
+        v = synth.make(spec, seed, "cuda")
+        mtp_vals[spec.name] = tuple(t.cpu() for t in v) if isinstance(v, tuple) else v.cpu()
+    mw = {n[len("mtp."):]: (om.FP8Weight(*v) if isinstance(v, tuple) else v) for n, v in mtp_vals.items() if n.startswith("mtp.")}
+    mw["final_norm_weight"] = mtp_vals["head.norm_weight"]
+    mst = {k: v.cpu() for k, v in synth.kv_states(cfg_block, batch, max_seq_len, [context] * batch, seed, "cpu.mtp", "cuda").items()}
+    minp = verify_inputs(cfg_block, [context] * batch, tokens, max_seq_len, torch.bfloat16, [True] * batch, [0] * batch)
+    emb = synth.hidden_states((batch, tokens, cfg_block.hidden_size), seed, "cpu.e")
+    mtp_s = 0.0
+    for _ in range(2):
+        started = time.perf_counter()
+        om.mtp_forward(cfg_block, mw, mst, x, emb, minp["cos"], minp["sin"], minp["position"], minp["active"])
+        mtp_s = time.perf_counter() - started
+    log(f"cpu MTP call {mtp_s:.2f}s")
+    del mw, mst, mtp_vals
+
+    # The head's group maxima: HEAD_ROWS rows against a 1/HEAD_VOCAB_PART slice of lm_head, scaled to the step's
+    # B x K verify rows plus three draft passes of B rows (linear in rows and in vocabulary).
+    head_rows, part = 16, 8
+    vs = cfg_block.vocab_size // part // 32 * 32
+    spec = [s for s in synth.head_specs(cfg_block) if s.name == "head.lm_head"][0]
+    spec = synth.Spec(spec.name, spec.kind, (vs, cfg_block.hidden_size))
+    coded, scales = (t.cpu() for t in synth.make(spec, seed, "cuda"))
+    lm = om.FP8Weight(coded, scales)
+    hx = synth.hidden_states((head_rows, 1, cfg_block.hidden_size), seed, "cpu.h")
+    nw = synth.make([s for s in synth.head_specs(cfg_block) if s.name == "head.norm_weight"][0], seed, "cpu")
+    lm.dense_t()
+    started = time.perf_counter()
+    om.head_group_maxima(cfg_block, nw, lm, hx)
+    head_sample = time.perf_counter() - started
+    head_rows_step = batch * tokens + (tokens - 1) * batch
+    head_s = head_sample * part * head_rows_step / head_rows
+    log(f"cpu head sample {head_sample:.2f}s ({head_rows} rows, 1/{part} of the vocabulary) -> {head_s:.2f}s per step")
+    step = times[-1] * n_blocks + 3 * mtp_s + head_s
     cpu_name = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -221,9 +258,11 @@ def cpu_baseline(cfg_block, batch: int, tokens: int, max_seq_len: int, context: 
         "unit": "accepted tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"one block (3 gated-delta + 1 attention layer) of the B={batch}, K={tokens}, context-{context} verify "
-        f"on the CPU oracle in bf16 ({times[-1]:.2f} s after one warm-up), x{n_blocks} for 64 layers; MTP and head "
-        f"passes not included; host {cpu_name}",
+        "sample": f"the CPU oracle in bf16, timed after one warm-up: one block (3 gated-delta + 1 attention layer) of the "
+        f"B={batch}, K={tokens}, context-{context} verify ({times[-1]:.2f} s) x{n_blocks} for 64 layers, plus 3 MTP calls "
+        f"over the B x K rows ({mtp_s:.2f} s each), plus the head's group maxima for {head_rows_step} rows scaled from "
+        f"{head_rows} rows against 1/{part} of lm_head ({head_sample:.2f} s -> {head_s:.2f} s): {step:.2f} s per step; "
+        f"host {cpu_name}",
     }
 
 
