@@ -52,6 +52,10 @@ typedef struct q38_handle q38_handle;
  * path the GEMM takes when a tile's contributors run on different XCDs (so do not share an L2). */
 #define Q38_GEMM_RECOMPUTE 4
 
+/* Bits of the step status word (q38_step_status). */
+#define Q38_STATUS_NONFINITE 1 /* a head row had no finite logit (the reference raises FloatingPointError) */
+#define Q38_STATUS_POSITION 2  /* an active row's tokens passed the last usable position (the reference: ValueError) */
+
 /* Model shapes (reference TextConfig, qwen38_inf2/config.py:11-62) plus the build's batch (rows), verify tokens per
  * row, cache length and whether the MTP layer is present (reference build_info keys batch_size, verify_tokens,
  * max_seq_len, mtp_tokens; neuron.py:128-140,182-185). */
@@ -244,6 +248,11 @@ int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* mat
  * No counterpart in the reference (its step is one compiled Neuron graph per shape). */
 int q38_spec_step_graph(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted,
                         const float* active, uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
+/* The step status word and, with clear != 0, its reset: the errors the reference raises on the host
+ * (FloatingPointError for a row with no finite logit, generate.py:206-207; ValueError for tokens past the last usable
+ * position, generate.py:78-79), which q38_spec_step (and q38_head_pick) record on the device instead of producing
+ * silently wrong ids or positions. Reads back one int: a synchronisation of `stream`. */
+int q38_step_status(q38_handle* h, int* status, int clear, void* stream);
 
 /* Measurement hook, with no counterpart in the reference (for benchmarks that time one kernel inside the step):
  * on != 0 starts bracketing every gate/up projection GEMM launched by q38_verify, q38_mtp_step and q38_spec_step with

@@ -90,7 +90,8 @@ struct q38_handle {
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
         off_scores, off_astats, off_aown, off_akv, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos,
-        off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, workspace_bytes;
+        off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, off_status,
+        workspace_bytes;
     // prefill scratch (with a prefill chunk in the config)
     size_t off_pqn = 0, off_pkn = 0, off_pv = 0, off_po = 0, off_pbeta = 0, off_pg = 0, off_pqs = 0;
     size_t part_floats;  // capacity of the split-K partial buffer
@@ -686,6 +687,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_sp_at = take(Tv * 4);
     h->off_sp_draft = take(Tv * 4);
     h->off_gemm = take(gemm_scratch_bytes(h->cus));
+    h->off_status = take(16);
     // Split-K partials: up to GEMM_SPLIT_MAX splits at the verify width, 4 at a prefill chunk's (whose tiles
     // outnumber the CUs: the split count is chosen so the last round of workgroups is full); gemm() caps the splits at
     // what fits.
@@ -754,8 +756,9 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
         return fail(std::string("buffer '") + name + "' needs " + std::to_string(n) + " bytes, got " + std::to_string(nbytes));
     if ((uintptr_t)dev_ptr % 16) return fail(std::string("buffer '") + name + "' is not 16-byte aligned");
     if (layer < 0 && std::string(name) == "workspace") {
-        // The GEMMs' arrival counters start at zero.
+        // The GEMMs' arrival counters and the step status word start at zero.
         HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 8));
+        HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_status, 0, 16));
     }
     Buf b;
     b.p = dev_ptr;
@@ -1085,6 +1088,7 @@ int q38_head_pick(q38_handle* h, const uint16_t* hidden, int rows, int groups, i
     a.w = wt;
     a.ws = wsc;
     a.rows = h->global.count("head.lm_head.rows") ? (const bf16_t*)h->global.at("head.lm_head.rows").p : nullptr;
+    a.status = (int*)h->ws(h->off_status);
     a.H = h->H;
     a.R = rows;
     a.groups = groups;
@@ -1119,7 +1123,8 @@ int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* mat
     // positions; the draft comes from its output at each row's match; each further draft from an MTP call on the
     // previous draft alone.
     if (q38_embed(h, picks, B * K, embeds, stream_)) return 1;
-    HIP_TRY(q38_rope_gather(index, 1, B, K, S, rope, cos, sin, stream));
+    int* status = (int*)h->ws(h->off_status);
+    HIP_TRY(q38_rope_gather(index, 1, B, K, S, rope, cos, sin, stream, active, status));
     if (q38_mtp_step(h, hidden, embeds, cos, sin, index, active, out, stream_)) return 1;
     HIP_TRY(q38_select_rows(out, match, B, K, H, current, stream));
     for (int j = 0; j < K - 1; ++j) {
@@ -1129,14 +1134,14 @@ int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* mat
         HIP_TRY(q38_mtp_followup(current, draft, B, K, H, states, ids, stream));
         if (q38_embed(h, ids, B * K, embeds, stream_)) return 1;
         HIP_TRY(q38_offset_positions(index, match, j, B, at, stream));
-        HIP_TRY(q38_rope_gather(at, 1, B, K, S, rope, cos, sin, stream));
+        HIP_TRY(q38_rope_gather(at, 1, B, K, S, rope, cos, sin, stream, active, status));
         if (q38_mtp_step(h, states, embeds, cos, sin, at, active, out, stream_)) return 1;
         HIP_TRY(q38_select_rows(out, nullptr, B, K, H, current, stream));
     }
     // Verify (scheduler.py:276-301): [last emitted token, drafts] per row, the head over all B*K rows, acceptance.
     HIP_TRY(q38_verify_tokens(picks, match, drafts, B, K, ids, stream));
     if (q38_embed(h, ids, B * K, embeds, stream_)) return 1;
-    HIP_TRY(q38_rope_gather(position, 0, B, K, S, rope, cos, sin, stream));
+    HIP_TRY(q38_rope_gather(position, 0, B, K, S, rope, cos, sin, stream, active, status));
     if (q38_verify(h, embeds, cos, sin, position, active, accepted, hidden, stream_)) return 1;
     if (q38_head_pick(h, hidden, B * K, 4, picks, stream_)) return 1;
     HIP_TRY(q38_accept(picks, drafts, active, B, K, match, accepted, stream));
@@ -1182,6 +1187,19 @@ int q38_spec_step_graph(q38_handle* h, int32_t* position, int32_t* index, int32_
     }
     HIP_TRY(hipGraphLaunch(g.exec, stream));
     h->parity = 1 - parity;
+    return 0;
+}
+
+int q38_step_status(q38_handle* h, int* status, int clear, void* stream_) {
+    if (!h || !status) return fail("null argument");
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    if (!ok) return 1;
+    hipStream_t stream = (hipStream_t)stream_;
+    int* word = (int*)h->ws(h->off_status);
+    HIP_TRY(hipMemcpyAsync(status, word, sizeof(int), hipMemcpyDeviceToHost, stream));
+    HIP_TRY(hipStreamSynchronize(stream));
+    if (clear) HIP_TRY(hipMemsetAsync(word, 0, sizeof(int), stream));
     return 0;
 }
 

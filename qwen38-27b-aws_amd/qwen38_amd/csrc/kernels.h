@@ -171,6 +171,7 @@ struct PickArgs {
     const uint8_t* w;      // lm_head tiles [V/32][H/64][64][32]
     const uint8_t* ws;     // lm_head scales [V/32][H/64][32][2]
     const bf16_t* rows;    // lm_head's bf16 rows [V][H] for the recheck, or null (then the tiles, dequantized)
+    int* status;           // or null: Q38_STATUS_NONFINITE is or'ed in for a row with no finite logit
     int H, R, groups;
     int* ids;              // [R]
 };
@@ -219,8 +220,13 @@ int q38_device_cus();
 int q38_projection(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n, int epi,
                    uint8_t* act, uint8_t* gemm, size_t fix_floats, void* out, int splits_max, hipStream_t stream, int w4,
                    int f8, int recompute);
+// Step status bits (include/q38.h): a row with no finite logit, a row whose tokens pass the last usable position.
+#ifndef Q38_STATUS_NONFINITE
+#define Q38_STATUS_NONFINITE 1
+#define Q38_STATUS_POSITION 2
+#endif
 hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
-                           hipStream_t s);
+                           hipStream_t s, const float* active = nullptr, int* status = nullptr);
 hipError_t q38_select_rows(const bf16_t* rows, const int* idx, int B, int K, int H, bf16_t* out, hipStream_t s);
 hipError_t q38_mtp_followup(const bf16_t* current, const int* draft, int B, int K, int H, bf16_t* states, int* ids,
                             hipStream_t s);

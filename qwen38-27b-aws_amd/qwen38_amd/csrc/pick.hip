@@ -185,6 +185,7 @@ __global__ __launch_bounds__(PICK_THREADS) void head_pick_kernel(const PickArgs 
             }
         }
         a.ids[r] = best;
+        if (best < 0 && a.status) atomicOr(a.status, Q38_STATUS_NONFINITE);
     }
 }
 

@@ -7,9 +7,14 @@
 //   advance        index <- position, position += accepted  (scheduler.py:296-300)
 #include "kernels.h"
 
+// An active row whose K tokens from `base` pass the last usable position (the reference's verify_inputs raises
+// ValueError when position + tokens > max_seq_len - 1, generate.py:78-79) sets Q38_STATUS_POSITION in *status; the
+// gather itself clamps to the table.
 __global__ void rope_gather_kernel(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos,
-                                   bf16_t* sin) {
+                                   bf16_t* sin, const float* active, int* status) {
     const int row = blockIdx.x, t = row % K, b = row / K, d = threadIdx.x;  // 64 threads: rotary dims
+    if (status && t == 0 && d == 0 && active && active[b] > 0.5f && (base[b] < 0 || base[b] + K > S - 1))
+        atomicOr(status, Q38_STATUS_POSITION);
     int p = base[b] + offset + t;
     p = min(max(p, 0), S - 1);
     cos[(size_t)row * 64 + d] = table[((size_t)p * 2 + 0) * 64 + d];
@@ -59,8 +64,9 @@ __global__ void column_kernel(const int* ids, int K, int B, int j, int* drafts) 
 }
 
 hipError_t q38_rope_gather(const int* base, int offset, int B, int K, int S, const bf16_t* table, bf16_t* cos, bf16_t* sin,
-                           hipStream_t s) {
-    hipLaunchKernelGGL(rope_gather_kernel, dim3(B * K), dim3(64), 0, s, base, offset, B, K, S, table, cos, sin);
+                           hipStream_t s, const float* active, int* status) {
+    hipLaunchKernelGGL(rope_gather_kernel, dim3(B * K), dim3(64), 0, s, base, offset, B, K, S, table, cos, sin, active,
+                       status);
     return hipGetLastError();
 }
 

@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph", "q38_step_status",
     "q38_kernel_timer",
 )
 
@@ -87,6 +87,7 @@ def library() -> ctypes.CDLL:
     lib.q38_accept.argtypes = [p, p, p, p, p, p, p]
     lib.q38_spec_step.argtypes = [p] * 10
     lib.q38_spec_step_graph.argtypes = [p] * 10
+    lib.q38_step_status.argtypes = [p, ctypes.POINTER(i), i, p]
     for name in EXPORTS:
         if name not in ("q38_last_error", "q38_destroy"):
             getattr(lib, name).restype = ctypes.c_size_t if name in ("q38_fp8_linear_scratch", "q38_tiles_size") else ctypes.c_int
@@ -208,6 +209,22 @@ class Handle:
         fn = self.lib.q38_spec_step_graph if graph else self.lib.q38_spec_step
         check(fn(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
 
+    def step_status(self, clear: bool = True) -> int:
+        """The device's step status word (`q38_step_status`: STATUS_NONFINITE, STATUS_POSITION), then reset."""
+        v = ctypes.c_int(0)
+        check(self.lib.q38_step_status(self.h, ctypes.byref(v), int(clear), stream()))
+        return v.value
+
+    def raise_step_errors(self) -> None:
+        """The reference's host-side errors for what the last steps recorded on the device: FloatingPointError for a
+        row with no finite logit (generate.py:206-207), ValueError for tokens past the last usable position
+        (generate.py:78-79)."""
+        status = self.step_status()
+        if status & STATUS_NONFINITE:
+            raise FloatingPointError("a row's logits are not finite, so the step produced NaN or infinity")
+        if status & STATUS_POSITION:
+            raise ValueError("a row's tokens pass max_seq_len")
+
     def kernel_timer(self, on: bool) -> tuple[int, float]:
         """Start (on) or stop bracketing the gate/up GEMM launches with HIP events; stopping returns (launches, total
         milliseconds)."""
@@ -259,6 +276,7 @@ def fp8_linear_noalloc(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tenso
 
 
 GEMM_RECOMPUTE = 4  # Q38_GEMM_RECOMPUTE
+STATUS_NONFINITE, STATUS_POSITION = 1, 2  # Q38_STATUS_*
 
 
 def fp8_linear_mfma(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, mfma: str, f32_out: bool = False,

@@ -243,3 +243,25 @@ def test_graph_replays_of_the_step_equal_its_launches(spec):
         else:
             for a, b in zip(graph_engine.get_kv(i), eager_engine.get_kv(i)):
                 assert torch.equal(a, b), i
+
+
+@pytest.mark.gpu
+def test_step_errors_are_recorded_on_the_device_and_raised_as_the_references(spec):
+    """A row whose tokens would pass the last usable position, and a head row with no finite logit, are recorded in
+    the device's status word and raised as the reference raises them on the host (ValueError, FloatingPointError);
+    a clean step leaves the word at zero."""
+    cfg, values = spec
+    engine, _ = load_engine(cfg, values)
+    device = DeviceStep(cfg, engine)
+    device()
+    assert engine.handle.step_status() == 0
+    device.position[0] = S - K  # position + K > max_seq_len - 1 for an active row
+    device()
+    with pytest.raises(ValueError, match="max_seq_len"):
+        engine.handle.raise_step_errors()
+    assert engine.handle.step_status() == 0  # cleared by the read
+    hidden = torch.full((4, 1, cfg.hidden_size), float("nan"), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(FloatingPointError):
+        HeadGraph(engine).pick(hidden, 4)
+    with pytest.raises(FloatingPointError):
+        engine.handle.raise_step_errors()
