@@ -617,7 +617,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": f"gemm_kernel<2,4,2,2,e5m2,6,SWIGLU,{'e2m1' if args.mxfp4 else 'e4m3'}> (MLP gate/up, 256 x 34816 x 5120)",
+            "kernel": f"gemm_kernel<2,4,2,2,e5m2,3,SWIGLU,{'e2m1' if args.mxfp4 else 'e4m3'},bf16 MFMA,KU=2> (MLP gate/up, 256 x 34816 x 5120)",
             "achieved": round(achieved, 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
