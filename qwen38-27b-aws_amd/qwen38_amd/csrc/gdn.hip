@@ -69,12 +69,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     constexpr int MB = (3 * RS + 31) / 32;   // 32-row MFMA blocks holding them
     __shared__ float mixed[K][3 * D];   // SiLU(conv) of this head's q, k, v channels
     __shared__ float qn[K][D], kn[K][D];
-    __shared__ float wk[D][K];          // committed snapshot keys times their decay weights, input-major
+    constexpr int WKS = K | 1;          // odd row stride of wk: the commit's column reads hit 32 different banks
+    __shared__ float wk[D][WKS];        // committed snapshot keys times their decay weights, input-major
     __shared__ float part[2][2 * K][D]; // reads, one partial per half of the state rows
     // [k_0..k_K-1, q_0..q_K-1] as three bf16 parts (rows r, RS + r, 2 RS + r) whose sum is the float32 value to 2^-27:
     // the A operand of the reads on the bf16 MFMA (products exact, float32 sums). Rows past them are never read out.
     __shared__ __attribute__((aligned(16))) bf16_t kq3[32 * MB][D + 8];
-    __shared__ float kk[K][K], qk[K][K];
+    __shared__ float ck[K][K], cq[K][K], ecum[K];
     __shared__ float ob[K][D];
     __shared__ float rms[K];
 
@@ -82,7 +83,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     const int Hv = a.Hv, Hk = a.Hk, C = a.C;
     const int rep = Hv / Hk, kh = h / rep;
     const bool owner = (h % rep) == 0;  // writes the shared key-head channels
-    const bool on = a.active[b] > 0.5f;
+    const float act = a.active[b];
+    const bool on = act > 0.5f;
     const float keep = (a.position[b] == 0 && on) ? 0.0f : 1.0f;
     const int acc_n = min(max(a.accepted[b], 0), K);
     constexpr int GMAX = 8;  // gate groups, at most
@@ -92,24 +94,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     const int cgrp = (2 * tid) / D, cj = (2 * tid) % D;
     const int cc = cgrp == 0 ? kh * D + cj : cgrp == 1 ? Hk * D + kh * D + cj : 2 * Hk * D + h * D + cj;
 
-    // Every global load of the block is issued here, before the first store: a load placed after a store would wait
-    // for it (the pointers may alias as far as the compiler knows), and each wait is a memory round trip.
+    // Every global load of the block is issued here, before the first store (a load placed after a store would wait
+    // for it: the pointers may alias as far as the compiler knows), and in the order the phases use them, the state
+    // last: the memory counter is in order, so each phase's wait leaves the later loads in flight. All of them are
+    // unconditional, at clamped valid addresses, so that none sits in a branch whose end waits for it.
     float gp[GMAX];
-    if (tid < 2 * K) {
-        const int t = tid % K, which = tid / K, O = 2 * Hv;
+    {
+        const int t = tid % K, which = (tid / K) & 1, O = 2 * Hv;
         const float* p = a.gate_part + ((size_t)b * K + t) * O + (which ? Hv + h : h);
-        // Unconditional loads (group indices clamped to valid ones), so that none waits for another.
 #pragma unroll
         for (int gi = 0; gi < GMAX; ++gi) gp[gi] = p[(size_t)min(gi, a.gate_groups - 1) * a.B * K * O];
     }
+    const bf16_t a_log = a.a_log[h], dt_bias = a.dt_bias[h];
     float dec_in[K];
 #pragma unroll
     for (int s = 0; s < K; ++s) dec_in[s] = a.decay_old[((size_t)b * K + s) * Hv + h];
     // Old conv state (3 bf16 per channel, so 3 words for the pair), last step's and this step's inputs (a word per
-    // token), conv weights (4 bf16 per channel: 16 bytes).
+    // token), conv weights (4 bf16 per channel: 16 bytes). Threads past the conv channels load the v group's.
     uint32_t cv_old[3], cv_prev[K], cv_new[K];
     uint4 cv_w;
-    if (conv_thread) {
+    {
         const uint32_t* po = (const uint32_t*)(a.conv_old + ((size_t)b * C + cc) * 3);
 #pragma unroll
         for (int q = 0; q < 3; ++q) cv_old[q] = po[q];
@@ -124,32 +128,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     float key_in[KPT];
 #pragma unroll
     for (int u = 0; u < KPT; ++u) {
-        const int i = tid + 256 * u;
-        key_in[u] = i < K * D ? a.key_old[(((size_t)b * K + i / D) * Hk + kh) * D + i % D] : 0.0f;
+        const int i = min(tid + 256 * u, K * D - 1);
+        key_in[u] = a.key_old[(((size_t)b * K + i / D) * Hk + kh) * D + i % D];
     }
     // State ownership: wave w holds columns [64 (w & 1), +64) and rows [64 (w >> 1), +64); lane l the two columns jc,
     // jc + 1 and, in each of 4 MFMA K-steps ks, the 8 rows ir + 16 ks + [0, 8), as the bf16 MFMA's B operand wants
     // them (column l % 32, inputs 8 (l / 32) + [0, 8)); even and odd columns go to two MFMAs.
     const int jc = 64 * (wave & 1) + 2 * (lane & 31), ir = 64 * (wave >> 1) + 8 * (lane >> 5);
-    float2 dlt_in[K];
+    // The commit's snapshot deltas, as the f32 MFMA's B operand: lane l holds snapshot 2 mi + l / 32 of columns jc,
+    // jc + 1 (zero past the last snapshot, set after the loads).
+    constexpr int MI = (K + 1) / 2;
+    float2 dlt_in[MI];
 #pragma unroll
-    for (int s = 0; s < K; ++s) dlt_in[s] = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + jc);
+    for (int mi = 0; mi < MI; ++mi) {
+        const int s = min(2 * mi + (lane >> 5), K - 1);
+        dlt_in[mi] = *(const float2*)(a.delta_old + (((size_t)b * K + s) * Hv + h) * D + jc);
+    }
+    constexpr int ZPW = (K + 3) / 4;  // gated-norm rows per wave
+    bf16_t z_in[ZPW][2];
+#pragma unroll
+    for (int u = 0; u < ZPW; ++u) {
+        const int r = min(wave + 4 * u, K - 1);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) z_in[u][half] = a.z[(size_t)(b * K + r) * Hv * D + h * D + lane + half * 64];
+    }
+    const bf16_t nw_lo_b = a.norm_w[lane], nw_hi_b = a.norm_w[lane + 64];
+    // Compiler barriers around the state loads keep every load above in place (rather than sunk into the branch that
+    // uses it, behind the state) and the state loads before the first use of anything.
+    asm volatile("" ::: "memory");
     bf16_t* st = a.state + ((size_t)b * Hv + h) * D * D;
     uint32_t sv[4][8];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int e = 0; e < 8; ++e) sv[ks][e] = *(const uint32_t*)(st + (size_t)(ir + 16 * ks + e) * D + jc);
-    constexpr int ZPW = (K + 3) / 4;  // gated-norm rows per wave
-    bf16_t z_in[ZPW][2];
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int u = 0; u < ZPW; ++u) {
-        const int r = wave + 4 * u;
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-            z_in[u][half] = r < K ? a.z[(size_t)(b * K + r) * Hv * D + h * D + lane + half * 64] : (bf16_t)0;
-    }
-    const float nw_lo = bf2f(a.norm_w[lane]), nw_hi = bf2f(a.norm_w[lane + 64]);
+    for (int mi = 0; mi < MI; ++mi)
+        if (2 * mi + (lane >> 5) >= K) dlt_in[mi] = make_float2(0.0f, 0.0f);
 
     // This step's gates (model.py:145-147): beta = sigmoid(bf16(x . in_proj_b)), g = -exp(A_log) softplus(bf16(x .
     // in_proj_a) + dt_bias), both times the row's active flag; the dot products are the gates kernel's partials, added
@@ -161,29 +177,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
 #pragma unroll
         for (int gi = 0; gi < GMAX; ++gi)
             if (gi < a.gate_groups) sum += gp[gi];
-        const float lin = rbf(sum), act = a.active[b];
+        const float lin = rbf(sum);
         if (which)
-            s_g[t] = -expf(bf2f(a.a_log[h])) * softplusf_(lin + bf2f(a.dt_bias[h])) * act;
+            s_g[t] = -expf(bf2f(a_log)) * softplusf_(lin + bf2f(dt_bias)) * act;
         else
             s_beta[t] = rbf(sigmoidf_(lin)) * act;
     }
 
     // Commit coefficients (model.py:386-398): decays of the taken snapshots, the state's scale and each snapshot's
-    // weight exp(sum of later decays), all float32 in the reference's order.
-    float decays[K], coef[K];
-    float total = 0.0f;
-#pragma unroll
-    for (int s = 0; s < K; ++s) {
-        decays[s] = dec_in[s] * (acc_n > s ? 1.0f : 0.0f);
-        total = total + decays[s];
-    }
-    const float scale = on ? expf(total) * keep : 1.0f;
-    {
-        float rem = total;
+    // weight exp(sum of later decays), all float32 in the reference's order; thread 192 + s of the last wave (which
+    // has no conv channels) computes snapshot s's weight, thread 192 + K the scale.
+    __shared__ float s_coef[K], s_scale;
+    if (tid >= 192 && tid <= 192 + K) {
+        const int s0 = tid - 192;
+        float decays[K];
+        float total = 0.0f;
 #pragma unroll
         for (int s = 0; s < K; ++s) {
-            rem = rem - decays[s];
-            coef[s] = expf(rem) * (acc_n > s ? 1.0f : 0.0f) * keep * (on ? 1.0f : 0.0f);
+            decays[s] = dec_in[s] * (acc_n > s ? 1.0f : 0.0f);
+            total = total + decays[s];
+        }
+        if (s0 == K) {
+            s_scale = on ? expf(total) * keep : 1.0f;
+        } else {
+            float rem = total;
+#pragma unroll
+            for (int s = 0; s < K; ++s)
+                if (s <= s0) rem = rem - decays[s];
+            s_coef[s0] = expf(rem) * (acc_n > s0 ? 1.0f : 0.0f) * keep * (on ? 1.0f : 0.0f);
         }
     }
 
@@ -262,14 +283,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
         const int i = tid + 256 * u;
         if (i >= K * D) break;
         const int s = i / D;
-        float c = 0.0f;
-#pragma unroll
-        for (int r = 0; r < K; ++r) c = s == r ? coef[r] : c;
-        wk[i % D][s] = key_in[u] * c;
+        wk[i % D][s] = key_in[u] * s_coef[s];
     }
     __syncthreads();
 
-    // In-step dot products k_t.k_s and q_t.k_s (model.py:438, 444): 8 lanes per product, 16 inputs each.
+    // In-step couplings (model.py:438, 444): e^(cum_t - cum_s) times k_t.k_s and q_t.k_s, the dot products over 8
+    // lanes of 16 inputs each; and e^cum_t. cum is the running float32 sum of this step's log decays.
+    float cum[K];
+#pragma unroll
+    for (int t = 0; t < K; ++t) cum[t] = t == 0 ? s_g[0] : cum[t - 1] + s_g[t];
+    if (tid < K) {
+        float c = 0.0f;
+#pragma unroll
+        for (int t = 0; t < K; ++t) c = tid == t ? cum[t] : c;
+        ecum[tid] = expf(c);
+    }
     for (int p = tid >> 3; p < 2 * K * K; p += 32) {
         const int isq = p / (K * K), t = (p % (K * K)) / K, s = p % K;
         const float* x = (isq ? qn[t] : kn[t]) + (tid & 7) * 16;
@@ -284,51 +312,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
             v += xv.w * yv.w;
         }
         v = group8_sum(v);
-        if ((tid & 7) == 0) (isq ? qk : kk)[t][s] = v;
+        if ((tid & 7) == 0) {
+            float ct = 0.0f, cs = 0.0f;
+#pragma unroll
+            for (int u = 0; u < K; ++u) {
+                ct = t == u ? cum[u] : ct;
+                cs = s == u ? cum[u] : cs;
+            }
+            (isq ? cq : ck)[t][s] = expf(ct - cs) * v;
+        }
     }
 
-    // State commit and reads (model.py:262-266, 419-429). Commit on the VALU: S' = bf16(S * scale + sum_s wk_s d_s),
-    // stored; reads [k; q] S' on the MFMA, S' (exact in bf16) against the three bf16 parts of [k; q], so every product
-    // is exact and the sums are float32. Each wave sums its 64 rows; the two row halves are added in the solve.
+    // State commit and reads (model.py:262-266, 419-429). Commit S' = bf16(S * scale + U) with the rank-K update
+    // U = sum_s wk_s d_s on the f32 MFMA, stored; reads [k; q] S' on the bf16 MFMA, S' (exact in bf16) against the
+    // three bf16 parts of [k; q], so every product is exact and the sums are float32. Each wave sums its 64 rows; the
+    // two row halves are added in the solve.
+    // U's 32 x 32 blocks (bi, bj) of the wave's quadrant are laid out to match the state registers: MFMA column n is
+    // state column jc + bj of lane n; MFMA row 8 q + 4 hh + t of block bi is state row ir0 + 32 bi + 16 (q / 2) + 8 hh
+    // + 4 (q % 2) + t, so accumulator register 4 q + t of lane l holds U at the row ir + 16 ks + e of sv[ks][e] with
+    // ks = 2 bi + q / 2, e = 4 (q % 2) + t.
     {
-        float d0[K], d1[K];
-#pragma unroll
-        for (int s = 0; s < K; ++s) {
-            d0[s] = dlt_in[s].x;
-            d1[s] = dlt_in[s].y;
-        }
+        const float scale = s_scale;
+        const int m = lane & 31, hl = lane >> 5;
+        const int arow = 64 * (wave >> 1) + 16 * (m >> 4) + 8 * ((m >> 2) & 1) + 4 * ((m >> 3) & 1) + (m & 3);
         v16f acc[MB][2];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[mb][0][q] = acc[mb][1][q] = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int i = ir + 16 * ks;
-            uint32_t pk[8];
+        for (int bi = 0; bi < 2; ++bi) {
+            v16f u0, u1;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float u0 = 0.0f, u1 = 0.0f;
+            for (int q = 0; q < 16; ++q) u0[q] = u1[q] = 0.0f;
 #pragma unroll
-                for (int s = 0; s < K; ++s) {
-                    u0 += wk[i + e][s] * d0[s];
-                    u1 += wk[i + e][s] * d1[s];
+            for (int mi = 0; mi < MI; ++mi) {
+                const int s = 2 * mi + hl;
+                const float av = s < K ? wk[arow + 32 * bi][s] : 0.0f;
+                u0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, dlt_in[mi].x, u0, 0, 0, 0);
+                u1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, dlt_in[mi].y, u1, 0, 0, 0);
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int ks = 2 * bi + half;
+                const int i = ir + 16 * ks;
+                uint32_t pk[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int r = 4 * (2 * half + (e >> 2)) + (e & 3);
+                    pk[e] = pk_bf16(__uint_as_float(sv[ks][e] << 16) * scale + u0[r],
+                                    __uint_as_float(sv[ks][e] & 0xffff0000u) * scale + u1[r]);
+                    *(uint32_t*)(st + (size_t)(i + e) * D + jc) = pk[e];
                 }
-                pk[e] = pk_bf16(__uint_as_float(sv[ks][e] << 16) * scale + u0,
-                                __uint_as_float(sv[ks][e] & 0xffff0000u) * scale + u1);
-                *(uint32_t*)(st + (size_t)(i + e) * D + jc) = pk[e];
-            }
-            v4i be, bo;  // column jc (low halves) and jc + 1 (high halves), rows i .. i + 7
+                v4i be, bo;  // column jc (low halves) and jc + 1 (high halves), rows i .. i + 7
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                be[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x05040100u);
-                bo[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x07060302u);
-            }
+                for (int q = 0; q < 4; ++q) {
+                    be[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x05040100u);
+                    bo[q] = (int)__builtin_amdgcn_perm(pk[2 * q + 1], pk[2 * q], 0x07060302u);
+                }
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-                const v8bf16 av = *(const v8bf16*)&kq3[32 * mb + (lane & 31)][i];
-                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, be), acc[mb][0], 0, 0, 0);
-                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, bo), acc[mb][1], 0, 0, 0);
+                for (int mb = 0; mb < MB; ++mb) {
+                    const v8bf16 av = *(const v8bf16*)&kq3[32 * mb + (lane & 31)][i];
+                    acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, be), acc[mb][0], 0, 0, 0);
+                    acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(v8bf16, bo), acc[mb][1], 0, 0, 0);
+                }
             }
         }
         // Accumulator register 4 q + t of block mb holds row 32 mb + 8 q + 4 (lane / 32) + t; row r of [k; q] is the
@@ -354,35 +401,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
     // In-step solve (model.py:431-448), one column per thread.
     if (tid < D) {
         const int j = tid;
-        float cum[K], beta[K], gl[K], dl[K];
-#pragma unroll
-        for (int t = 0; t < K; ++t) {
-            gl[t] = s_g[t];
-            beta[t] = s_beta[t];
-            cum[t] = t == 0 ? gl[0] : cum[t - 1] + gl[t];
-        }
+        float dl[K];
 #pragma unroll
         for (int t = 0; t < K; ++t) {
             const float ks = part[0][t][j] + part[1][t][j];
             const float qs = part[0][K + t][j] + part[1][K + t][j];
-            float delta = mixed[t][2 * D + j] - expf(cum[t]) * ks;
+            float delta = mixed[t][2 * D + j] - ecum[t] * ks;
 #pragma unroll
-            for (int s = 0; s < t; ++s) delta = delta - (expf(cum[t] - cum[s]) * kk[t][s]) * dl[s];
-            dl[t] = delta * beta[t];
-            float out = expf(cum[t]) * qs;
+            for (int s = 0; s < t; ++s) delta = delta - ck[t][s] * dl[s];
+            dl[t] = delta * s_beta[t];
+            float out = ecum[t] * qs;
 #pragma unroll
-            for (int s = 0; s <= t; ++s) out = out + (expf(cum[t] - cum[s]) * qk[t][s]) * dl[s];
+            for (int s = 0; s <= t; ++s) out = out + cq[t][s] * dl[s];
             ob[t][j] = rbf(out);
             if (a.out_probe) a.out_probe[((size_t)b * K + t) * Hv * D + h * D + j] = f2bf(ob[t][j]);
             a.delta_new[(((size_t)b * K + t) * Hv + h) * D + j] = dl[t];
             if (owner) a.key_new[(((size_t)b * K + t) * Hk + kh) * D + j] = kn[t][j] + 0.0f;
         }
-        if (j < K) {
-            float g = 0.0f;
-#pragma unroll
-            for (int t = 0; t < K; ++t) g = j == t ? gl[t] : g;
-            a.decay_new[((size_t)b * K + j) * Hv + h] = g + 0.0f;
-        }
+        if (j < K) a.decay_new[((size_t)b * K + j) * Hv + h] = s_g[j] + 0.0f;
     }
     __syncthreads();
 
@@ -402,7 +438,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K <= 4 ? 3 
         for (int half = 0; half < 2; ++half) {
             const int j = lane + half * 64;
             float hv = rbf(ob[r][j] * rms[r]);
-            hv = rbf((half ? nw_hi : nw_lo) * hv);
+            hv = rbf(bf2f(half ? nw_hi_b : nw_lo_b) * hv);
             float zf = bf2f(z_in[u][half]);
             float sz = zf * sigmoidf_(zf);
             a.act[act_offset(tok, h * D + j, Hv * D)] = (uint8_t)e5m2_byte(rbf(hv * sz));
