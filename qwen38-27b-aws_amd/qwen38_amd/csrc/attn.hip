@@ -84,92 +84,102 @@ __device__ __forceinline__ void load_keys(const AttnArgs& a, size_t head, int p0
 // q rows normed and rotated (bf16, qb; rows NQ .. QT*32 - 1 zero) and, with `own`, the step's keys normed and rotated
 // (bf16, kb) and values: to kv_own (float32, global) and/or vown (float32, LDS), where given; with KV8 the own keys
 // and values as they read back from the cache. NWV waves; wave w takes rows w, w + NWV, ...; lane l holds dims
-// 4l .. 4l + 3. Loads are issued before any store.
+// 4l .. 4l + 3. load() issues every load, unconditionally (rows past the real ones read row 0, cos/sin past dim 64
+// read dims 0-63), so that a kernel can issue its cache loads behind them and wait for these alone in finish().
 template <int QT, int NWV, bool KV8>
-__device__ __forceinline__ void project_rows(const AttnArgs& a, int b, int kvh, int wave, int lane, bool own,
-                                             bf16_t* qb, bf16_t* kb, float* kv_own, float (*vown)[256]) {
-    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K;
-    constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + NWV - 1) / NWV;
-    const int nrows = QT * 32 + (own ? 2 * K : 0), d0 = lane * 4;
-    uint2 raw[RPW], rc[RPW], rs_[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int r = wave + NWV * i;
-        raw[i] = rc[i] = rs_[i] = make_uint2(0, 0);
-        if (r >= nrows || (r >= NQ && r < QT * 32)) continue;
-        const bf16_t* src;
-        int t;
-        if (r < NQ) {
-            t = r % K;
-            src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)(kvh * G + r / K) * 512;
-        } else if (r < QT * 32 + K) {
-            t = r - QT * 32;
-            src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)a.Hq * 512 + kvh * 256;
-        } else {
-            t = r - QT * 32 - K;
-            src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)a.Hq * 512 + (size_t)a.Hkv * 256 + kvh * 256;
-        }
-        raw[i] = *(const uint2*)(src + d0);
-        if (d0 < 64) {
-            rc[i] = *(const uint2*)(a.cos + ((size_t)b * K + t) * 64 + d0);
-            rs_[i] = *(const uint2*)(a.sin + ((size_t)b * K + t) * 64 + d0);
-        }
-    }
-    float qn_w[4], kn_w[4], ksc = 0.0f, vsc = 0.0f;
-    if (KV8 && own) ksc = bf2f(*a.k_scale), vsc = bf2f(*a.v_scale);
-    unpack4(*(const uint2*)(a.q_norm + d0), qn_w);
-    unpack4(*(const uint2*)(a.k_norm + d0), kn_w);
+struct RowLoads {
+    static constexpr int RPW = (QT * 32 + 2 * ATTN_KMAX + NWV - 1) / NWV;
+    uint2 raw[RPW], rc[RPW], rs_[RPW], qn, kn;
+    bf16_t ksc_b, vsc_b;
 
-    // All rows' sums of squares reduced together (independent shuffle chains), then norm, RoPE and stores.
-    float v[RPW][4], ss[RPW];
+    __device__ __forceinline__ void load(const AttnArgs& a, int b, int kvh, int wave, int lane, bool own) {
+        const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K;
+        const int nrows = QT * 32 + (own ? 2 * K : 0), d0 = lane * 4;
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        unpack4(raw[i], v[i]);
-        ss[i] = v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-        for (int i = 0; i < RPW; ++i) ss[i] += __shfl_xor(ss[i], o);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        const int r = wave + NWV * i;
-        const float* nw = r < QT * 32 ? qn_w : kn_w;
-        const float rsq = 1.0f / sqrtf(ss[i] / 256.0f + a.eps);
-        float hn[4], part[4], cs[4], sn[4], out[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hn[e] = rbf(v[i][e] * rsq * (1.0f + nw[e]));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) part[e] = __shfl_xor(hn[e], 8);
-        unpack4(rc[i], cs);
-        unpack4(rs_[i], sn);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int d = d0 + e;
-            const float rot = d < 32 ? -part[e] : part[e];
-            out[e] = d < 64 ? rbf(rbf(hn[e] * cs[e]) + rbf(rot * sn[e])) : hn[e];
+        for (int i = 0; i < RPW; ++i) {
+            int r = wave + NWV * i;
+            if (r >= nrows || (r >= NQ && r < QT * 32)) r = 0;
+            const bf16_t* src;
+            int t;
+            if (r < NQ) {
+                t = r % K;
+                src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)(kvh * G + r / K) * 512;
+            } else if (r < QT * 32 + K) {
+                t = r - QT * 32;
+                src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)a.Hq * 512 + kvh * 256;
+            } else {
+                t = r - QT * 32 - K;
+                src = a.qkv + ((size_t)b * K + t) * a.ld + (size_t)a.Hq * 512 + (size_t)a.Hkv * 256 + kvh * 256;
+            }
+            raw[i] = *(const uint2*)(src + d0);
+            rc[i] = *(const uint2*)(a.cos + ((size_t)b * K + t) * 64 + (d0 & 63));
+            rs_[i] = *(const uint2*)(a.sin + ((size_t)b * K + t) * 64 + (d0 & 63));
         }
-        if (r < QT * 32) {
-            *(uint2*)(qb + r * QPITCH + d0) = r < NQ ? pack4(out) : make_uint2(0, 0);
-        } else if (r >= nrows) {
-            // rows of own keys and values exist only with `own`
-        } else if (r < QT * 32 + K) {
-            const int t = r - QT * 32;
-            if constexpr (KV8)
+        qn = *(const uint2*)(a.q_norm + d0);
+        kn = *(const uint2*)(a.k_norm + d0);
+        if constexpr (KV8) ksc_b = *a.k_scale, vsc_b = *a.v_scale;
+    }
+
+    __device__ __forceinline__ void finish(const AttnArgs& a, int wave, int lane, bool own, bf16_t* qb, bf16_t* kb,
+                                           float* kv_own, float (*vown)[256]) {
+        const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K;
+        const int nrows = QT * 32 + (own ? 2 * K : 0), d0 = lane * 4;
+        float qn_w[4], kn_w[4], ksc = 0.0f, vsc = 0.0f;
+        if constexpr (KV8) ksc = bf2f(ksc_b), vsc = bf2f(vsc_b);
+        unpack4(qn, qn_w);
+        unpack4(kn, kn_w);
+
+        // All rows' sums of squares reduced together (independent shuffle chains), then norm, RoPE and stores.
+        float v[RPW][4], ss[RPW];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) out[e] = kv_round_trip(out[e], ksc);
-            *(uint2*)(kb + t * QPITCH + d0) = pack4(out);
-            if (kv_own) *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
-        } else {
-            const int t = r - QT * 32 - K;
-            if constexpr (KV8)
+        for (int i = 0; i < RPW; ++i) {
+            unpack4(raw[i], v[i]);
+            ss[i] = v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[i][e] = kv_round_trip(v[i][e], vsc);
-            if (kv_own) *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
-            if (vown) *(v4f*)&vown[t][d0] = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) ss[i] += __shfl_xor(ss[i], o);
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int r = wave + NWV * i;
+            const float* nw = r < QT * 32 ? qn_w : kn_w;
+            const float rsq = 1.0f / sqrtf(ss[i] / 256.0f + a.eps);
+            float hn[4], part[4], cs[4], sn[4], out[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hn[e] = rbf(v[i][e] * rsq * (1.0f + nw[e]));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[e] = __shfl_xor(hn[e], 8);
+            unpack4(rc[i], cs);
+            unpack4(rs_[i], sn);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = d0 + e;
+                const float rot = d < 32 ? -part[e] : part[e];
+                out[e] = d < 64 ? rbf(rbf(hn[e] * cs[e]) + rbf(rot * sn[e])) : hn[e];
+            }
+            if (r < QT * 32) {
+                *(uint2*)(qb + r * QPITCH + d0) = r < NQ ? pack4(out) : make_uint2(0, 0);
+            } else if (r >= nrows) {
+                // rows of own keys and values exist only with `own`
+            } else if (r < QT * 32 + K) {
+                const int t = r - QT * 32;
+                if constexpr (KV8)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) out[e] = kv_round_trip(out[e], ksc);
+                *(uint2*)(kb + t * QPITCH + d0) = pack4(out);
+                if (kv_own) *(v4f*)(kv_own + t * 256 + d0) = (v4f){out[0], out[1], out[2], out[3]};
+            } else {
+                const int t = r - QT * 32 - K;
+                if constexpr (KV8)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[i][e] = kv_round_trip(v[i][e], vsc);
+                if (kv_own) *(v4f*)(kv_own + (ATTN_KMAX + t) * 256 + d0) = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
+                if (vown) *(v4f*)&vown[t][d0] = (v4f){v[i][0], v[i][1], v[i][2], v[i][3]};
+            }
         }
     }
-}
+};
 
 // Scores of 32 keys against the query tiles (lane l: query row l % 32 of each 32-row tile, positions p0 +
 // acc_row(i, l)), as rbf(q.k) / 16, -inf at positions p_hi and beyond; lmax takes their maximum.
@@ -244,17 +254,17 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     auto scored = [&](int nb) { return (nb * SW + wave) * 32 < npos; };
     const int dcol = wave * 16 + (lane & 15);  // output dim of this lane
 
+    // The step's rows first, then this wave's cache keys (the first block also for waves past the visible positions,
+    // whose scores are never formed): the row work waits for its own loads only. The compiler barriers keep that
+    // order.
+    RowLoads<QT, SW, KV8> rows;
+    rows.load(a, b, kvh, wave, lane, true);
+    asm volatile("" ::: "memory");
     v8bf kf[16];
-    if (scored(0)) load_keys<KV8>(a, head, wave * 32, lane, kf);
-    uint32_t gate[RT][4];  // gates of this lane's output rows rt*16 + 4 (l / 16) + i, dim dcol
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = min(rt * 16 + 4 * (lane >> 4) + i, NQ - 1);
-            gate[rt][i] = a.qkv[(size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + dcol];
-        }
-    project_rows<QT, SW, KV8>(a, b, kvh, wave, lane, true, qb, kb, nullptr, vown);
+    load_keys<KV8>(a, head, min(wave * 32, S - 32), lane, kf);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);  // nor may the row arithmetic (and its waits) be scheduled above the key loads
+    rows.finish(a, wave, lane, true, qb, kb, nullptr, vown);
     __syncthreads();
 
     v16f sacc[NB][QT];
@@ -358,7 +368,16 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
         }
     __syncthreads();
 
-    // Weights x V for this wave's 16 dims; then the own part, the gate and the e5m2 activation bytes.
+    // Weights x V for this wave's 16 dims; then the own part, the gate and the e5m2 activation bytes. The gates load
+    // here, where the scores' registers are free, behind the V loads and ahead of the MFMAs that hide them.
+    uint32_t gate[RT][4];  // gates of this lane's output rows rt*16 + 4 (l / 16) + i, dim dcol
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = min(rt * 16 + 4 * (lane >> 4) + i, NQ - 1);
+            gate[rt][i] = a.qkv[(size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + dcol];
+        }
     v4f acc[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
@@ -432,9 +451,16 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     const int blk = (p_lo >> 5) + wave;  // this wave's 32 positions
     const bool scored = blk * 32 < p_hi;
 
+    // The step's rows first, then the cache keys (clamped into the cache for waves past the chunk's positions, whose
+    // scores are never formed), so that the row work waits for its own loads only.
+    RowLoads<QT, SW, KV8> rows;
+    rows.load(a, b, kvh, wave, lane, first);
+    asm volatile("" ::: "memory");
     v8bf kf[16];
-    if (scored) load_keys<KV8>(a, head, blk * 32, lane, kf);
-    project_rows<QT, SW, KV8>(a, b, kvh, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
+    load_keys<KV8>(a, head, min(blk * 32, S - 32), lane, kf);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);  // nor may the row arithmetic (and its waits) be scheduled above the key loads
+    rows.finish(a, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
     __syncthreads();
 
     // The wave's block of scores, kept in registers; chunk 0's last wave also scores the own keys.
@@ -716,6 +742,7 @@ hipError_t launch_attn(AttnArgs a, hipStream_t stream) {
 hipError_t q38_attn_verify(const AttnArgs& a, hipStream_t stream) {
     const int NQ = a.Hq / a.Hkv * a.K;
     if (NQ > ATTN_QMAX || a.K > ATTN_KMAX || (long)a.nchunks * ATTN_CHUNK < a.S) return hipErrorInvalidValue;
+    if (a.S < 32 || a.S % 32) return hipErrorInvalidValue;  // whole blocks of 32 positions (every wave loads one)
     // Two position blocks per wave need 66 KB of bf16 weights in LDS at 32 query rows; 64 rows keep one.
     if (a.kv8) {
         if (!a.k_scale || !a.v_scale) return hipErrorInvalidValue;
