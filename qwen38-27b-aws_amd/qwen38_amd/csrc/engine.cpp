@@ -109,6 +109,10 @@ struct q38_handle {
         const void* args[8] = {};
     } graphs[2];
     hipStream_t capture_stream = nullptr;
+    // A second stream for work that can run beside the main chain (a gated-delta layer's gate projections beside its
+    // qkvz GEMM), forked and joined with the two events; made when the workspace is bound.
+    hipStream_t side_stream = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 
     uint8_t* ws(size_t off) const { return (uint8_t*)global.at("workspace").p + off; }
     void drop_graphs() {
@@ -342,12 +346,8 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         // A verify step's qkv output is also its pending input snapshot; a decode step's or a prefill chunk's goes to
         // scratch.
         uint16_t* qkv_out = io.decode || io.slot ? (uint16_t*)h->ws(h->off_qkv) : pin + wr * BKC;
-        if (gemm(h, li, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
-            return 1;
-        if (probe && !io.decode && !io.slot) {
-            HIP_TRY(hipMemcpyAsync(probe, h->ws(h->off_hbf), (size_t)h->T * H * 2, hipMemcpyDeviceToDevice, stream));
-            HIP_TRY(hipMemcpyAsync(probe + (size_t)h->T * H, z, (size_t)h->T * h->Hv * h->dk * 2, hipMemcpyDeviceToDevice, stream));
-        }
+        // The gate projections (x . in_proj_b, x . in_proj_a) read only the normed input: they run on the side stream
+        // beside the qkvz GEMM, whose persistent workgroups leave room for theirs on every CU.
         GatesArgs ga{};
         ga.x = (const bf16_t*)h->ws(h->off_hbf);
         ga.wb = wb;
@@ -357,7 +357,22 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         ga.Hv = h->Hv;
         ga.groups = h->gate_groups;
         ga.part = (float*)h->ws(h->off_gates);
-        HIP_TRY(q38_gdn_gates(ga, stream));
+        const bool fork = h->side_stream != nullptr;
+        if (fork) {
+            HIP_TRY(hipEventRecord(h->fork_ev, stream));
+            HIP_TRY(hipStreamWaitEvent(h->side_stream, h->fork_ev, 0));
+            HIP_TRY(q38_gdn_gates(ga, h->side_stream));
+            HIP_TRY(hipEventRecord(h->join_ev, h->side_stream));
+        } else {
+            HIP_TRY(q38_gdn_gates(ga, stream));
+        }
+        if (gemm(h, li, qkvz_t, qkvz_s, act_h, H, h->C + h->Hv * h->dk, EPI_BF16, qkv_out, h->C, h->C, z, h->Hv * h->dk, stream))
+            return 1;
+        if (fork) HIP_TRY(hipStreamWaitEvent(stream, h->join_ev, 0));
+        if (probe && !io.decode && !io.slot) {
+            HIP_TRY(hipMemcpyAsync(probe, h->ws(h->off_hbf), (size_t)h->T * H * 2, hipMemcpyDeviceToDevice, stream));
+            HIP_TRY(hipMemcpyAsync(probe + (size_t)h->T * H, z, (size_t)h->T * h->Hv * h->dk * 2, hipMemcpyDeviceToDevice, stream));
+        }
         if (io.slot) {
             PrefillGdnArgs p{};
             p.L = h->T;
@@ -712,6 +727,9 @@ void q38_destroy(q38_handle* h) {
     for (hipEvent_t e : h->timer_events) (void)hipEventDestroy(e);
     h->drop_graphs();
     if (h->capture_stream) (void)hipStreamDestroy(h->capture_stream);
+    if (h->side_stream) (void)hipStreamDestroy(h->side_stream);
+    if (h->fork_ev) (void)hipEventDestroy(h->fork_ev);
+    if (h->join_ev) (void)hipEventDestroy(h->join_ev);
     delete h;
 }
 
@@ -759,6 +777,11 @@ int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t n
         // The GEMMs' arrival counters and the step status word start at zero.
         HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_gemm, 0, (size_t)GEMM_COUNTERS * 8));
         HIP_TRY(hipMemset((uint8_t*)dev_ptr + h->off_status, 0, 16));
+        if (!h->side_stream) {
+            HIP_TRY(hipStreamCreateWithFlags(&h->side_stream, hipStreamNonBlocking));
+            HIP_TRY(hipEventCreateWithFlags(&h->fork_ev, hipEventDisableTiming));
+            HIP_TRY(hipEventCreateWithFlags(&h->join_ev, hipEventDisableTiming));
+        }
     }
     Buf b;
     b.p = dev_ptr;
