@@ -3,10 +3,11 @@
 layer through two verify steps, a decode step and a prefill chunk (tests/golden/kv8_tiny.*, written from the
 reference's own CPU path; the oracle is pinned to it bit for bit on the CPU).
 
-* Hidden states after each call against the reference's, per token (test_gpu_prefill.check_tokens): the bulk at the
-  float32 level, every token within 0.15, at most one in sixteen above the north-star 2e-2. A token above it has an
-  e5m2 tie at an activation, or one of its own key or value bytes on the neighbouring e4m3 code, decided the other
-  way by a float32-ulp difference upstream; the step grows to a few percent of that token's row through the MLP.
+* Hidden states after each call against the oracle's, teacher-forced: the oracle runs the call from the cache the GPU
+  left (the GPU's bytes at every position written so far) and with the GPU's bytes for the call's own keys and values,
+  so the one rounding that reaches other tokens (e4m3 of a key or value) is the GPU's; then per token within the
+  north-star 2e-2, each token above it explained by one e5m2 rounding tie after its mixer (`ties.check_tokens`). The
+  bytes themselves are held below. (The oracle's own path, unforced, is printed against the reference's outputs.)
 * Cache bytes after each call against the oracle's: the GPU's keys and values come out of its own GEMM and norm, a
   float32 ulp or so from the oracle's, and e4m3 rounds them to 1/16 of a value: so a few bytes may land on the
   neighbouring code. Held to: at most 1% of the bytes differ, each by one code step, and positions no call writes
@@ -27,7 +28,7 @@ from qwen38_amd.generate import batch_step_inputs, prefill_inputs, verify_inputs
 from qwen38_amd.steps import Engine, StepGraph, VerifyStep
 from safetensors.torch import load_file
 from scenario import GOLDEN, oracle_weights
-from test_gpu_prefill import check_tokens
+import ties
 
 
 def row_rel(got: torch.Tensor, want: torch.Tensor) -> float:
@@ -63,46 +64,99 @@ def test_fp8_kv_cache_steps_like_the_reference(gpu):
     engine.load((n, v) for n, v in values.items() if not n.startswith("mtp."))
     engine.set_kv_scales(0, ks, vs)
     engine.set_kv(0, kc, vc)
+    engine.enable_probe(0)  # verify calls leave the layer's GEMM inputs for the tie proofs
     verify, step = VerifyStep(engine), StepGraph(engine)
     verify_ids, decode_ids, prefill_ids, positions_2, decode_positions = g8.scenario(cfg)
     embed, kind = values["embed_tokens"], "full_attention"
 
-    def check(name, got, want):
+    w = layers[0]
+    o_w = w["self_attn.o_proj"]
+
+    def written(cache: torch.Tensor, where: torch.Tensor) -> torch.Tensor:
+        """The GPU cache bytes ``[B, Hkv, n, hd]`` at per-row positions ``where`` ``[B, n]``."""
+        at = where.long().reshape(b, 1, -1, 1).expand(-1, cache.shape[1], -1, cache.shape[3])
+        return cache.cpu().gather(2, at)
+
+    def oracle(gpu_kv, x, *args, **kw):
+        """The oracle's layer on x from ``st``, teacher-forced with the GPU's bytes for the step's own keys and values
+        (``gpu_kv``: as the oracle's kv_store would give them; its calls alternate key, value). Updates ``st``; returns
+        the output and the out projection's input it rounded (for `ties`)."""
+        calls = []
+
+        def forced(t, scale):
+            calls.append(t)
+            return gpu_kv[(len(calls) - 1) % 2].reshape(t.shape)
+
+        plain = om.kv_store
+        om.kv_store = forced
+        try:
+            with ties.Recorder() as rec:
+                want = om.decoder_layer(cfg, kind, w, st, x, *args, **kw)
+        finally:
+            om.kv_store = plain
+        return want, rec.inputs[id(o_w)]
+
+    def check(name, got, want, x, o_in, plain, o_gpu=None):
         torch.cuda.synchronize()
-        gk, gv = engine.get_kv(0)
-        check_codes(gk, st["k_cache"], f"{name} k_cache")
-        check_codes(gv, st["v_cache"], f"{name} v_cache")
         h = gold[name].shape[-1]
         rows = [r for r in range(b) if meta["active"][r]]  # an inactive row's output is not used
-        print(f"{name}: CPU builds apart {row_rel(want, gold[name]):.3g}", flush=True)
-        check_tokens(got[rows].reshape(-1, h), gold[name][rows].reshape(-1, h))
+        print(f"{name}: CPU builds apart {row_rel(plain, gold[name]):.3g}", flush=True)
+        o_in = o_in.reshape(b, -1, o_in.shape[-1])
+        if o_gpu is not None:
+            o_gpu = o_gpu.reshape(b, -1, o_gpu.shape[-1])[rows].reshape(-1, o_gpu.shape[-1])
+        ties.check_tokens(got[rows].reshape(-1, h), want[rows].reshape(-1, h), w, cfg.rms_norm_eps,
+                          x[rows].reshape(-1, h), o_in[rows].reshape(-1, o_in.shape[-1]), o_gpu)
+
+    def plain_oracle(name, x, *args, **kw):
+        """The oracle's own layer (no forcing) from a copy of ``st``: the reference's path. Its output is compared with
+        the reference's, its cache bytes with the GPU's."""
+        mine = {n: v.clone() for n, v in st.items()}
+        out = om.decoder_layer(cfg, kind, w, mine, x, *args, **kw)
+        gk, gv = engine.get_kv(0)
+        check_codes(gk, mine["k_cache"], f"{name} k_cache")
+        check_codes(gv, mine["v_cache"], f"{name} v_cache")
+        return out
 
     for n, (pos, acc) in enumerate(((meta["positions_1"], [0] * b), (positions_2, meta["accepted_2"]))):
         print(f"verify {n + 1}", flush=True)
         vi = verify_inputs(cfg, pos, k, s, torch.bfloat16, meta["active"], acc)
-        got = verify(inputs_embeds=embed[verify_ids[n]], **vi)
-        want = om.decoder_layer(cfg, kind, layers[0], st, embed[verify_ids[n]], vi["cos"], vi["sin"], vi["position"],
-                                vi["active"], accepted=vi["accepted"])
-        check(f"verify{n + 1}", got, want)
+        x = embed[verify_ids[n]]
+        got = verify(inputs_embeds=x, **vi)
+        torch.cuda.synchronize()
+        args = (vi["cos"], vi["sin"], vi["position"], vi["active"])
+        plain = plain_oracle(f"verify{n + 1}", x, *args, accepted=vi["accepted"])
+        where = torch.where(vi["active"].unsqueeze(-1) > 0.5, vi["position"].long().unsqueeze(-1) + torch.arange(k),
+                            s - k + torch.arange(k))
+        gk, gv = engine.get_kv(0)
+        want, o_in = oracle((written(gk, where), written(gv, where)), x, *args, accepted=vi["accepted"])
+        check(f"verify{n + 1}", got, want, x, o_in, plain, engine.probe(0)["mid"].cpu())
     print("decode", flush=True)
     di = batch_step_inputs(cfg, decode_positions, s, torch.bfloat16, meta["active"])
-    got = step(inputs_embeds=embed[decode_ids].unsqueeze(1), **di)
-    want = om.decoder_layer(cfg, kind, layers[0], st, embed[decode_ids].unsqueeze(1), di["cos"], di["sin"], di["position"],
-                            di["active"])
-    check("decode", got, want)
+    x = embed[decode_ids].unsqueeze(1)
+    got = step(inputs_embeds=x, **di)
+    torch.cuda.synchronize()
+    args = (di["cos"], di["sin"], di["position"], di["active"])
+    plain = plain_oracle("decode", x, *args)
+    where = torch.where(di["active"] > 0.5, di["position"].long(), s - 1).unsqueeze(-1)
+    gk, gv = engine.get_kv(0)
+    want, o_in = oracle((written(gk, where), written(gv, where)), x, *args)
+    check("decode", got, want, x, o_in, plain)
     print("prefill", flush=True)
     p = meta["prefill"]
     pi = prefill_inputs(cfg, p["slot"], p["start"], p["n_valid"], p["chunk"], torch.bfloat16)
     x = embed[prefill_ids].unsqueeze(0)
     got = step(inputs_embeds=x, **pi)
-    want = om.decoder_layer(cfg, kind, layers[0], st, x, pi["cos"], pi["sin"], None, None, slot=pi["slot"],
-                            start=pi["start"], n_valid=pi["n_valid"])
+    torch.cuda.synchronize()
+    kw = dict(slot=pi["slot"], start=pi["start"], n_valid=pi["n_valid"])
+    span = slice(p["start"], p["start"] + p["chunk"])
+    mine = {n: v.clone() for n, v in st.items()}
+    plain = om.decoder_layer(cfg, kind, w, mine, x, pi["cos"], pi["sin"], None, None, **kw)
+    gk, gv = engine.get_kv(0)
+    check_codes(gk[p["slot"], :, span], mine["k_cache"][p["slot"], :, span], "prefill k_cache")
+    check_codes(gv[p["slot"], :, span], mine["v_cache"][p["slot"], :, span], "prefill v_cache")
+    want, o_in = oracle((gk[p["slot"], :, span].cpu(), gv[p["slot"], :, span].cpu()), x, pi["cos"], pi["sin"], None, None, **kw)
     # Only row `slot`'s prefill positions are compared: the reference also writes junk at every other row's last
     # positions, which this build leaves alone (nothing reads them before a later step overwrites them).
-    torch.cuda.synchronize()
     n = p["n_valid"]
-    check_tokens(got[0, :n], gold["prefill"][0, :n])
-    gk, gv = engine.get_kv(0)
-    span = slice(p["start"], p["start"] + p["chunk"])
-    check_codes(gk[p["slot"], :, span], st["k_cache"][p["slot"], :, span], "prefill k_cache")
-    check_codes(gv[p["slot"], :, span], st["v_cache"][p["slot"], :, span], "prefill v_cache")
+    print(f"prefill: CPU builds apart {row_rel(plain[0, :n], gold['prefill'][0, :n]):.3g}", flush=True)
+    ties.check_tokens(got[0, :n], want[0, :n], w, cfg.rms_norm_eps, x[0, :n], o_in.reshape(-1, o_in.shape[-1])[:n])
