@@ -24,11 +24,3 @@ def gpu():
 
     return ext.library()
 
-
-@pytest.fixture(scope="session")
-def references():
-    """The oracle on the golden scenario here (AVX512 kernels where the host has them) and the scalar build of it
-    (tests/floor.py), computed once per session."""
-    import floor
-
-    return floor.run_scenario(), floor.scalar_build()

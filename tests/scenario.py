@@ -111,3 +111,14 @@ def spec_states(cfg, spec=SPEC):
             states.append(synth.kv_states(cfg, b, s, context, seed, f"spec.layers.{i}"))
     mtp = synth.kv_states(cfg, b, s, [max(n - 1, 0) for n in context], seed, "spec.mtp")
     return states, mtp
+
+
+def row_rel(got: torch.Tensor, want: torch.Tensor) -> float:
+    """Largest per-row relative distance ||got - want|| / ||want|| over the leading dimension."""
+    got, want = got.float().cpu(), want.float().cpu()
+    worst = 0.0
+    for r in range(want.shape[0]):
+        n = float(want[r].norm())
+        if n > 0:
+            worst = max(worst, float((got[r] - want[r]).norm()) / n)
+    return worst

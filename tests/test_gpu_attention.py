@@ -4,7 +4,7 @@ The golden scenario's contexts are short; these cases spread each (row, KV head)
 2048 positions, with 4 tokens per row and with 1 as in decode), take the one-launch path with one and with two blocks
 of 512 positions per wave, take the 64-query-row path (16 query heads over 2 KV heads, 8 tokens), and include an
 empty cache and an inactive row (which writes the cache tail), each with a bf16 cache and with an FP8 one (e4m3 bytes with the layer's scales). Checked: the
-MTP output (one layer, so the north-star 2e-2 per-row bound without a floor factor), the positions the step writes in
+MTP output (one layer, held to the north-star 2e-2 per row), the positions the step writes in
 both caches (1e-2 on the values they read back: the keys are normed and rotated in bf16 by both sides), and every
 other cache position unchanged.
 """

@@ -20,7 +20,6 @@ from __future__ import annotations
 import pytest
 import torch
 
-import floor
 import layerwise
 import ties
 from qwen38_amd import synth
@@ -28,7 +27,9 @@ from oracle import model as om
 from qwen38_amd.config import tiny_config, with_layers
 from qwen38_amd.generate import batch_step_inputs, verify_inputs
 from qwen38_amd.steps import Engine, StepGraph
-from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, tiny_states
+from scenario import clone_states, golden_meta, golden_tensors, oracle_weights, row_rel, tiny_states
+
+DECODE_STEPS = 3
 
 
 def set_states(engine, cfg, states):
@@ -94,13 +95,13 @@ def test_one_layer_decodes_like_the_oracle_step_by_step(gpu, kind):
         torch.cuda.synchronize()
         before = clone_states(states)
         want = om.step_decode(cfg, layers, states, x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"])
-        err = floor.row_rel(got, want)
+        err = row_rel(got, want)
         print(f"  hidden {err:.3g}", flush=True)
         assert err <= 2e-2
         if kind == "linear_attention":
             mine = engine.gdn_state(0)
             for key in ("recurrent_state", "conv_state"):
-                err = floor.row_rel(mine[key], states[0][key])
+                err = row_rel(mine[key], states[0][key])
                 print(f"  {key} {err:.3g}", flush=True)
                 assert err <= 1e-2, key
                 assert torch.equal(mine[key][3].cpu(), before[0][key][3]), key
@@ -109,7 +110,7 @@ def test_one_layer_decodes_like_the_oracle_step_by_step(gpu, kind):
             for name, cache in (("k_cache", kc), ("v_cache", vc)):
                 for row in range(meta["batch"]):
                     at = pos[row] if active[row] else s - 1
-                    assert floor.row_rel(cache[row, :, at], states[0][name][row, :, at]) <= 1e-2, (name, row)
+                    assert row_rel(cache[row, :, at], states[0][name][row, :, at]) <= 1e-2, (name, row)
                     keep = torch.ones(s, dtype=torch.bool)
                     keep[at] = False
                     assert torch.equal(cache[row, :, keep].cpu(), before[0][name][row, :, keep]), (name, row)
@@ -158,7 +159,7 @@ def test_decode_steps_then_verify_layer_by_layer(scenario):
                 assert torch.equal(mine[key], full[key]), (i, key)
 
     pos = list(meta["positions_1"])
-    for t in range(floor.DECODE_STEPS):
+    for t in range(DECODE_STEPS):
         print(f"decode step {t}", flush=True)
         inputs = batch_step_inputs(cfg, pos, s, torch.bfloat16, active)
         run(embed[ids[0][:, t]].unsqueeze(1),

@@ -24,7 +24,6 @@ import pytest
 import torch
 from safetensors.torch import load_file
 
-import floor
 import layerwise
 import ties
 from oracle import model as om
@@ -32,7 +31,7 @@ from qwen38_amd import synth
 from qwen38_amd.config import tiny_config, with_layers
 from qwen38_amd.generate import mtp_prefill_inputs, prefill_inputs
 from qwen38_amd.steps import Engine, MTPStep, StepGraph
-from scenario import GOLDEN, clone_states, golden_meta, oracle_weights, tiny_states
+from scenario import GOLDEN, clone_states, golden_meta, oracle_weights, row_rel, tiny_states
 
 
 def prefill_meta():
@@ -109,7 +108,7 @@ def test_one_layer_prefills_like_the_oracle_chunk_by_chunk(gpu, kind):
             for name, cache in (("k_cache", kc), ("v_cache", vc)):
                 cache = cache.cpu()
                 written = slice(start, start + chunk)
-                assert floor.row_rel(cache[slot, :, written].transpose(0, 1), states[0][name][slot, :, written].transpose(0, 1)) <= 1e-2, name
+                assert row_rel(cache[slot, :, written].transpose(0, 1), states[0][name][slot, :, written].transpose(0, 1)) <= 1e-2, name
                 keep = torch.ones(s, dtype=torch.bool)
                 keep[written] = False
                 assert torch.equal(cache[slot, :, keep], before[0][name][slot, :, keep]), name
@@ -153,7 +152,7 @@ def test_two_prefill_chunks_layer_by_layer(gpu):
             for key, value in before.items():  # the oracle's state after the chunk
                 if key in ("k_cache", "v_cache"):
                     written = slice(start, start + chunk)
-                    err = floor.row_rel(mine[key][slot, :, written].transpose(0, 1), value[slot, :, written].transpose(0, 1))
+                    err = row_rel(mine[key][slot, :, written].transpose(0, 1), value[slot, :, written].transpose(0, 1))
                 else:
                     err = rel_all(mine[key][slot], value[slot])
                 print(f"    {key} {err:.3g}", flush=True)
@@ -196,10 +195,10 @@ def test_mtp_prefill_writes_the_layers_cache_like_the_oracle(gpu):
     got = MTPStep(engine)(hidden=hidden, inputs_embeds=embeds, **mi)
     torch.cuda.synchronize()
     want = om.mtp_prefill(cfg, mtp_w, mst, hidden, embeds, mi["cos"], mi["sin"], mi["slot"], mi["start"], mi["n_valid"])
-    assert floor.row_rel(got[0], want[0]) <= 2e-2
+    assert row_rel(got[0], want[0]) <= 2e-2
     kc, vc = engine.get_kv(engine.mtp_layer)
     others = [r for r in range(meta["batch"]) if r != slot]
     for name, cache in (("k_cache", kc.cpu()), ("v_cache", vc.cpu())):
-        assert floor.row_rel(cache[slot, :, :chunk].transpose(0, 1), mst[name][slot, :, :chunk].transpose(0, 1)) <= 1e-2, name
+        assert row_rel(cache[slot, :, :chunk].transpose(0, 1), mst[name][slot, :, :chunk].transpose(0, 1)) <= 1e-2, name
         assert torch.equal(cache[slot, :, chunk:], before[name][slot, :, chunk:]), name
         assert torch.equal(cache[others], before[name][others]), name
