@@ -53,9 +53,10 @@ __device__ __forceinline__ void wait_and_barrier() {
 // Direct global -> LDS load of BYTES per lane: lane l's bytes land at LDS address dst + l * BYTES (dst wave-uniform).
 // Issued as inline assembly, so the compiler neither waits for it before unrelated LDS reads (it cannot tell ring
 // stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the compiler's waits for its own loads only
-// get longer. NT marks the load non-temporal (the weight and scale streams, read once): L2 then keeps the activation
-// tiles every workgroup rereads (the 256-row head's L2 misses fall from 2.2 GB to 1.43 GB per launch for 1.31 GB of
-// weights).
+// get longer. NT marks the load non-temporal. The head's weight and scale streams (1.31 GB, read once per launch) use
+// it: L2 then keeps the activation tiles every workgroup rereads (the 256-row head's HBM reads fall from 2.2 GB to
+// 1.43 GB per launch). The decoder projections do not: there it changed no GEMM's time, and the attention kernel that
+// follows them ran 55 instead of 46 us.
 template <int BYTES, bool NT = false>
 __device__ __forceinline__ void lds_load(const void* src, uint32_t dst) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst);
@@ -186,10 +187,10 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             for (int i = 0; i < N_W; ++i) {
                 const int off = (i * NW + wave) * (64 * W_DMA);
                 const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS64 + k64) * WTB + off % WTB;
-                lds_load<W_DMA, true>(g + lane * W_DMA, sb + ACT_B + off);
+                lds_load<W_DMA, EPI == EPI_GROUPMAX>(g + lane * W_DMA, sb + ACT_B + off);
             }
             const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS64 + k64) * 64;
-            lds_load<4, true>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
+            lds_load<4, EPI == EPI_GROUPMAX>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
         }
     };
 
