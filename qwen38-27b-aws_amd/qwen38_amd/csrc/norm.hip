@@ -9,52 +9,60 @@
 #include "kernels.h"
 
 // One workgroup of max(64, H / 8) threads per row (H <= 8192, H % 256 == 0, checked by the host); thread tid owns
-// columns 4 tid + [0, 4) and H / 2 + 4 tid + [0, 4). All of a thread's global loads (every split's partials, the
-// residual, the norm weights) are issued before any arithmetic or store: the partials come from HBM, and a CU reaches
-// its share of HBM bandwidth only with its whole working set in flight.
+// columns 8 tid + [0, 8): 32 contiguous bytes of each split's partials, 16 of the residual, and its e5m2 activation
+// bytes are one 8-byte store (8 consecutive inputs of one tile lane). All of a thread's global loads (every split's
+// partials, the residual, the norm weights) are issued before any arithmetic or store: the partials come from HBM,
+// and a CU reaches its share of HBM bandwidth only with its whole working set in flight.
 __global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
     __shared__ float red[16];
     const int t = blockIdx.x, tid = threadIdx.x, H = a.H;
-    const bool on = tid * 4 < H / 2;
-    const int col[2] = {tid * 4, H / 2 + tid * 4};
+    const bool on = tid * 8 < H;
+    const int c0 = tid * 8;
     v4f p[GEMM_SPLIT_MAX][2];
-    uint2 rr[2], ww[2], dd[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        rr[h] = ww[h] = dd[h] = make_uint2(0, 0);
-        if (!on) continue;
+    uint4 rr = make_uint4(0, 0, 0, 0), ww = rr, dd = rr;
+    if (on) {
         if (!a.part)
-            rr[h] = *(const uint2*)(a.xin + (size_t)t * H + col[h]);
+            rr = *(const uint4*)(a.xin + (size_t)t * H + c0);
         else if (a.resid)
-            rr[h] = *(const uint2*)(a.resid + (size_t)t * H + col[h]);
-        if (a.w) ww[h] = *(const uint2*)(a.w + col[h]);
-        if (a.div_w) dd[h] = *(const uint2*)(a.div_w + col[h]);
+            rr = *(const uint4*)(a.resid + (size_t)t * H + c0);
+        if (a.w) ww = *(const uint4*)(a.w + c0);
+        if (a.div_w) dd = *(const uint4*)(a.div_w + c0);
 #pragma unroll
         for (int s = 0; s < GEMM_SPLIT_MAX; ++s)
-            if (a.part && s < a.splits) p[s][h] = *(const v4f*)(a.part + ((size_t)s * a.Tpad + t) * H + col[h]);
+            if (a.part && s < a.splits) {
+                const float* src = a.part + ((size_t)s * a.Tpad + t) * H + c0;
+                p[s][0] = *(const v4f*)src;
+                p[s][1] = *(const v4f*)(src + 4);
+            }
     }
-    float v[2][4];
+    auto unpack8 = [](uint4 r, float* f) {
+        const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bf2f((bf16_t)(w4[i] & 0xffff));
+            f[2 * i + 1] = bf2f((bf16_t)(w4[i] >> 16));
+        }
+    };
+    float v[8], rb[8];
+    unpack8(rr, rb);
     float ss = 0.0f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const bf16_t rb[4] = {(bf16_t)(rr[h].x & 0xffff), (bf16_t)(rr[h].x >> 16), (bf16_t)(rr[h].y & 0xffff), (bf16_t)(rr[h].y >> 16)};
+    for (int e = 0; e < 8; ++e) {
+        if (a.part) {
+            float sum = 0.0f;  // split order
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (a.part) {
-                float sum = 0.0f;  // split order
-#pragma unroll
-                for (int s = 0; s < GEMM_SPLIT_MAX; ++s)
-                    if (s < a.splits) sum += p[s][h][e];
-                v[h][e] = a.resid ? rbf(bf2f(rb[e]) + rbf(sum)) : rbf(sum);
-            } else {
-                v[h][e] = bf2f(rb[e]);
-            }
-            ss += on ? v[h][e] * v[h][e] : 0.0f;
+            for (int s = 0; s < GEMM_SPLIT_MAX; ++s)
+                if (s < a.splits) sum += p[s][e >> 2][e & 3];
+            v[e] = a.resid ? rbf(rb[e] + rbf(sum)) : rbf(sum);
+        } else {
+            v[e] = rb[e];
         }
-        if (on && a.xout)
-            *(uint2*)(a.xout + (size_t)t * H + col[h]) =
-                make_uint2(pk_bf16(v[h][0], v[h][1]), pk_bf16(v[h][2], v[h][3]));
+        ss += on ? v[e] * v[e] : 0.0f;
     }
+    auto pack8 = [](const float* f) {
+        return make_uint4(pk_bf16(f[0], f[1]), pk_bf16(f[2], f[3]), pk_bf16(f[4], f[5]), pk_bf16(f[6], f[7]));
+    };
+    if (on && a.xout) *(uint4*)(a.xout + (size_t)t * H + c0) = pack8(v);
     if (!a.act && !a.hout) return;  // residual only (the last layer)
     ss = warp_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -63,23 +71,18 @@ __global__ __launch_bounds__(1024) void residual_norm_kernel(const NormArgs a) {
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
     const float r = 1.0f / sqrtf(tot / (float)H + a.eps);
     if (!on) return;
+    float wf[8], df[8], o[8];
+    unpack8(ww, wf);
+    unpack8(dd, df);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const bf16_t wb[4] = {(bf16_t)(ww[h].x & 0xffff), (bf16_t)(ww[h].x >> 16), (bf16_t)(ww[h].y & 0xffff), (bf16_t)(ww[h].y >> 16)};
-        const bf16_t db[4] = {(bf16_t)(dd[h].x & 0xffff), (bf16_t)(dd[h].x >> 16), (bf16_t)(dd[h].y & 0xffff), (bf16_t)(dd[h].y >> 16)};
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            o[e] = rbf(v[h][e] * r * (1.0f + bf2f(wb[e])));
-            if (a.div_w) o[e] = rbf(o[e] / (1.0f + bf2f(db[e])));
-        }
-        if (a.hout)
-            *(uint2*)(a.hout + (size_t)t * H + col[h]) =
-                make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
-        if (a.act)
-            *(uint32_t*)(a.act + act_offset(t, a.act_col0 + col[h], a.Kact)) =
-                pk_e5m2(o[0], o[1], o[2], o[3]);
+    for (int e = 0; e < 8; ++e) {
+        o[e] = rbf(v[e] * r * (1.0f + wf[e]));
+        if (a.div_w) o[e] = rbf(o[e] / (1.0f + df[e]));
     }
+    if (a.hout) *(uint4*)(a.hout + (size_t)t * H + c0) = pack8(o);
+    if (a.act)
+        *(uint2*)(a.act + act_offset(t, a.act_col0 + c0, a.Kact)) =
+            make_uint2(pk_e5m2(o[0], o[1], o[2], o[3]), pk_e5m2(o[4], o[5], o[6], o[7]));
 }
 
 hipError_t q38_residual_norm(const NormArgs& a, hipStream_t stream) {
