@@ -155,6 +155,14 @@ int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles
  * is exact. Same scratch. */
 int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                      uint8_t* scratch, uint16_t* out, void* stream);
+/* The reference's `FP4Linear.forward` (model.py:198-208, the weight_format "fp4" numerics): bf16 x [rows][k] against an
+ * MXFP4 weight from q38_pack_weight_fp4, out = bf16(bf16(x_even . W_even) + bf16(x_odd . W_odd)) [rows][n] with the
+ * inputs split by parity (fp4.decode_planes, fp4.py:93-100) and float32 sums. scratch holds q38_fp4_linear_scratch(rows,
+ * k) bytes, zero-filled before its first use (bf16 input tiles, then the GEMM's counters and partial sums); calls that
+ * share it must not overlap. */
+int q38_fp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                   uint8_t* scratch, uint16_t* out, void* stream);
+size_t q38_fp4_linear_scratch(int rows, int k);
 /* q38_fp8_linear for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops):
  * the same outputs, with the scratch in the library's own static device array (66.5 MiB, held by each GPU the call
  * runs on until the process ends) instead of an argument. 1 to 64 rows, K <= 32768, n % 256 == 0; other sizes are

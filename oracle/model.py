@@ -19,6 +19,9 @@ Pinning of each function (what fixes it besides this text):
   `attention_verify`, `attention_decode` and `attention_prefill` bit for bit (hidden states and cache bytes after two
   verify steps, a decode step and a prefill chunk of one attention layer); tests/test_oracle.py also holds the e4m3
   codec against its bit fields over every bf16 value.
+* `decode_planes` and `linear_fp4` (the weight_format "fp4" numerics): the planes against the reference's FP4 decode
+  known-answer file (tests/golden/fp4_decode_kat), each plane's product against its float64 sum (one of the two bf16
+  neighbours) and the sum of the planes in bf16, in tests/test_oracle.py.
 * invariants in tests/test_oracle.py: prefill then decode equals decoding every token (float32, reference
   tests/test_prefill.py:143-166); the chunked rule equals the recurrence in float64 with correlated keys and padding;
   `unit_lower_inverse` equals a dense inverse; blocked attention equals one softmax;
@@ -137,6 +140,30 @@ def linear_fp8(x: torch.Tensor, weight: FP8Weight) -> torch.Tensor:
     """`FP8Linear.forward` on CPU (model.py:221-225): e5m2 input, weights in x's dtype, x's dtype out."""
     x = fp8_round(x)
     return F.linear(x, weight.dense_t().T.to(x.dtype))
+
+
+# E2M1 magnitudes of nibble codes 0-7 (codes 8-15 are their negatives), fp4.py:31.
+E2M1_MAGNITUDES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def decode_planes(packed: torch.Tensor, scale_bytes: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The checkpoint's MXFP4 weight (``packed`` uint8 ``[out, in / 2]``, the even input in the low nibble; E8M0
+    ``scale_bytes`` ``[out, in / 32]``) as its even and odd input columns in bf16 (fp4.py:93-100 on the sign-free form,
+    which `to_sign_free` makes from these bytes, fp4.py:75-84; every value exact in bf16, fp4.py:20-22)."""
+    lut = torch.tensor(E2M1_MAGNITUDES, dtype=torch.float32)
+    lut = torch.cat((lut, -lut))
+    scale = torch.pow(2.0, scale_bytes.float() - 127.0).repeat_interleave(16, dim=-1)  # 16 of each plane per group
+    even = lut[(packed & 15).long()] * scale
+    odd = lut[(packed >> 4).long()] * scale
+    # The sign-free codes have one zero: a negative zero decodes as +0 (fp4.py:78).
+    return (torch.where(even == 0, 0.0, even).to(torch.bfloat16), torch.where(odd == 0, 0.0, odd).to(torch.bfloat16))
+
+
+def linear_fp4(x: torch.Tensor, packed: torch.Tensor, scale_bytes: torch.Tensor) -> torch.Tensor:
+    """`FP4Linear.forward` (model.py:205-208): x's even and odd inputs through the two planes, each a matmul in x's
+    dtype, the results added in x's dtype."""
+    even, odd = decode_planes(packed, scale_bytes)
+    return F.linear(x[..., ::2], even.to(x.dtype)) + F.linear(x[..., 1::2], odd.to(x.dtype))
 
 
 def mlp(w: dict, x: torch.Tensor) -> torch.Tensor:

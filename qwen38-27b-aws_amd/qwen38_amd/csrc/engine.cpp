@@ -849,6 +849,41 @@ int q38_fp8_linear_mfma(const uint16_t* x, int rows, int k, const uint8_t* tiles
                       (hipStream_t)stream, 0, kind == Q38_MFMA_FP8, (mfma & Q38_GEMM_RECOMPUTE) != 0);
 }
 
+size_t q38_fp4_linear_scratch(int rows, int k) {
+    return align256((size_t)pad_tokens(rows) * k * 2) + gemm_scratch_bytes(device_cus());
+}
+
+// FP4Linear.forward (model.py:206-208): each parity plane of x through the whole weight (the other plane's inputs are
+// zero in the tiles, so the sum is the plane's), the first plane's sums stored as bf16, the second's added to them.
+int q38_fp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
+                   uint8_t* scratch, uint16_t* out, void* stream_) {
+    if (!x || !tiles || !tile_scales || !scratch || !out) return fail("null argument");
+    if (rows < 1 || n % 256 || k % 256) return fail("fp4_linear needs rows >= 1, N % 256 == 0 and K % 256 == 0");
+    const hipStream_t stream = (hipStream_t)stream_;
+    bf16_t* act = (bf16_t*)scratch;
+    uint8_t* gemm_base = scratch + align256((size_t)pad_tokens(rows) * k * 2);
+    for (int plane = 0; plane < 2; ++plane) {
+        HIP_TRY(q38_act_tiles_bf16((const bf16_t*)x, rows, k, plane, act, stream));
+        GemmArgs a{};
+        a.w = tiles;
+        a.ws = tile_scales;
+        a.act = act;
+        a.K = k;
+        a.N = n;
+        a.T = rows;
+        a.Tpad = pad_tokens(rows);
+        a.w4 = 1;
+        a.bf16_act = 1;
+        a.accumulate = plane;
+        a.out0 = out;
+        a.ld0 = n;
+        a.n0 = n;
+        gemm_scratch(a, gemm_base, device_cus());
+        HIP_TRY(q38_gemm(a, EPI_BF16, nullptr, stream));
+    }
+    return 0;
+}
+
 int q38_mxfp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                      uint8_t* scratch, uint16_t* out, void* stream) {
     return standalone(x, rows, k, tiles, tile_scales, n, EPI_BF16, scratch, out, 0, (hipStream_t)stream, 1);

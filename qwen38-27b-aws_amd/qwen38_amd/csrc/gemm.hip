@@ -304,11 +304,17 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int col = (ft0 + f) * 32 + g * 8 + rowq;
-                        uint32_t lo = pk_bf16(acc[f][t][g * 4 + 0], acc[f][t][g * 4 + 1]);
-                        uint32_t hi = pk_bf16(acc[f][t][g * 4 + 2], acc[f][t][g * 4 + 3]);
                         bf16_t* dst = col < a.n0 ? (bf16_t*)a.out0 + (size_t)tok * a.ld0 + col
                                                  : (bf16_t*)a.out1 + (size_t)tok * a.ld1 + (col - a.n0);
-                        *(uint2*)dst = make_uint2(lo, hi);
+                        float v[4] = {acc[f][t][g * 4 + 0], acc[f][t][g * 4 + 1], acc[f][t][g * 4 + 2], acc[f][t][g * 4 + 3]};
+                        if (a.accumulate) {  // bf16(out + bf16(sum)), the reference's sum of two bf16 products
+                            const uint2 old = *(const uint2*)dst;
+                            v[0] = lo_bf(old.x) + rbf(v[0]);
+                            v[1] = hi_bf(old.x) + rbf(v[1]);
+                            v[2] = lo_bf(old.y) + rbf(v[2]);
+                            v[3] = hi_bf(old.y) + rbf(v[3]);
+                        }
+                        *(uint2*)dst = make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
                     }
                 }
             } else if constexpr (EPI == EPI_SWIGLU) {
@@ -604,6 +610,11 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
 }  // namespace
 
 hipError_t q38_gemm(const GemmArgs& a, int epi, int* splits_out, hipStream_t stream) {
+    if (a.w4 && a.bf16_act) {
+        // bf16 activation tiles against MXFP4 weights (the reference's FP4Linear numerics, one plane per launch)
+        if (epi != EPI_BF16) return hipErrorInvalidValue;
+        return dispatch<false, EPI_BF16, true, false>(a, splits_out, stream);
+    }
     if (a.w4) {
         switch (epi) {
             case EPI_BF16: return dispatch<true, EPI_BF16, true, false>(a, splits_out, stream);

@@ -30,6 +30,8 @@ struct GemmArgs {
     int splits;          // EPI_PARTIAL split count (set by the launcher)
     int w4;              // weight tiles hold MXFP4 (q38_pack_fp4) rather than e4m3
     int f8;              // e4m3 weights x e5m2 activations on the FP8 MFMA (else widened to bf16 for the bf16 MFMA)
+    int bf16_act;        // with w4 and EPI_BF16: bf16 activation tiles (q38_act_tiles_bf16) instead of e5m2 ones
+    int accumulate;      // EPI_BF16: out = bf16(out + bf16(sum)) instead of bf16(sum)
 };
 
 struct NormArgs {
@@ -212,6 +214,8 @@ hipError_t q38_pack(const uint8_t* coded, const uint8_t* scales, int N, int K, u
 hipError_t q38_pack_fp4(const uint8_t* packed, const uint8_t* scales, int N, int K, uint8_t* tiles, uint8_t* tile_scales,
                         hipStream_t stream);
 hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_t stream);
+// bf16 activation tiles (the same element order) of x's inputs k with k % 2 == plane; the other inputs zero.
+hipError_t q38_act_tiles_bf16(const bf16_t* x, int T, int K, int plane, bf16_t* act, hipStream_t stream);
 
 // Host helpers of the C ABI (engine.cpp): the thread's q38_last_error message (returns 1), the device's CUs, and one
 // projection outside a handle (input tiles into act, GEMM counters then fix_floats floats of partial slots at gemm).

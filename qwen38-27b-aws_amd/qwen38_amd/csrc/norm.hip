@@ -147,3 +147,21 @@ hipError_t q38_act_tiles(const bf16_t* x, int T, int K, uint8_t* act, hipStream_
     hipLaunchKernelGGL(act_tiles_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream, x, T, K, act);
     return hipGetLastError();
 }
+
+// bf16 activation tiles of one input plane (FP4Linear's x[..., ::2] or x[..., 1::2], model.py:206-208): inputs of the
+// other parity are zero, so a GEMM over all K inputs sums exactly the plane's products.
+__global__ __launch_bounds__(256) void act_tiles_bf16_kernel(const bf16_t* x, int T, int K, int plane, bf16_t* act) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // group of 4 elements
+    if (i >= (size_t)T * K / 4) return;
+    const int t = (int)(i / (K / 4)), c = (int)(i % (K / 4)) * 4;
+    const uint2 r = *(const uint2*)(x + (size_t)t * K + c);
+    const uint32_t keep = plane ? 0xffff0000u : 0x0000ffffu;  // inputs c + 1, c + 3 (odd) or c, c + 2 (even)
+    *(uint2*)(act + act_offset(t, c, K)) = make_uint2(r.x & keep, r.y & keep);
+}
+
+hipError_t q38_act_tiles_bf16(const bf16_t* x, int T, int K, int plane, bf16_t* act, hipStream_t stream) {
+    size_t groups = (size_t)T * K / 4;
+    hipLaunchKernelGGL(act_tiles_bf16_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream, x, T, K,
+                       plane, act);
+    return hipGetLastError();
+}

@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph", "q38_step_status",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp4_linear", "q38_fp4_linear_scratch", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph", "q38_step_status",
     "q38_kernel_timer",
 )
 
@@ -68,6 +68,8 @@ def library() -> ctypes.CDLL:
     lib.q38_pack_weight_fp4.argtypes = [p, p, i, i, p, p, p]
     lib.q38_fp8_linear.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_mxfp4_linear.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_fp4_linear.argtypes = [p, i, i, p, p, i, p, p, p]
+    lib.q38_fp4_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_scratch.argtypes = [i, i]
     lib.q38_fp8_linear_f32.argtypes = [p, i, i, p, p, i, p, p, p]
     lib.q38_fp8_linear_mfma.argtypes = [p, i, i, p, p, i, i, i, p, p, p]
@@ -90,7 +92,7 @@ def library() -> ctypes.CDLL:
     lib.q38_step_status.argtypes = [p, ctypes.POINTER(i), i, p]
     for name in EXPORTS:
         if name not in ("q38_last_error", "q38_destroy"):
-            getattr(lib, name).restype = ctypes.c_size_t if name in ("q38_fp8_linear_scratch", "q38_tiles_size") else ctypes.c_int
+            getattr(lib, name).restype = ctypes.c_size_t if name in ("q38_fp8_linear_scratch", "q38_fp4_linear_scratch", "q38_tiles_size") else ctypes.c_int
     _lib = lib
     return lib
 
@@ -299,6 +301,17 @@ def mxfp4_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: 
     scratch = linear_scratch(rows, k, x.device) if scratch is None else scratch
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
     check(library().q38_mxfp4_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
+    return out
+
+
+def fp4_linear(x: torch.Tensor, tiles: torch.Tensor, scales: torch.Tensor, n: int, scratch=None) -> torch.Tensor:
+    """`FP4Linear.forward` on the GPU (the weight_format "fp4" numerics): bf16 x [rows, k] -> bf16 [rows, n] through a
+    packed MXFP4 weight (`pack_weight_fp4`), the even and odd inputs summed apart and their bf16 results added."""
+    rows, k = x.shape
+    if scratch is None:
+        scratch = torch.zeros(library().q38_fp4_linear_scratch(rows, k), dtype=torch.uint8, device=x.device)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
+    check(library().q38_fp4_linear(ptr(x.contiguous()), rows, k, ptr(tiles), ptr(scales), n, ptr(scratch), ptr(out), stream()))
     return out
 
 

@@ -26,6 +26,42 @@ def same(a: torch.Tensor, b: torch.Tensor) -> bool:
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("rows,k,n", [(256, 5120, 1024), (64, 2048, 512), (3, 1024, 256), (300, 768, 512)])
+def test_fp4_linear_matches_the_references_fp4_numerics(gpu, rows, k, n):
+    """`q38_fp4_linear` (FP4Linear.forward, model.py:205-208: bf16 inputs, even and odd inputs through their weight
+    planes apart, each product rounded to bf16, then added) against the oracle's `linear_fp4`: equal, except at an
+    output where a plane's float64 sum lies within 2^-20 of its sum |x w| of a point halfway between two bf16 values
+    (there the GPU's and torch's float32 sums, in different orders, may round to different neighbours); at most 1% of
+    the outputs are such."""
+    from oracle import model as om
+
+    print(f"fp4 linear rows={rows} k={k} n={n}", flush=True)
+    g = torch.Generator().manual_seed(rows + k + n)
+    w = torch.randn(n, k, generator=g) * 0.02
+    w[:, 64:96] *= 1e-6  # a group whose scale is far below the others
+    packed, scales = quantize_mxfp4(w)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    tiles, words = ext.pack_weight_fp4(packed.cuda(), scales.cuda())
+    got = ext.fp4_linear(x.cuda(), tiles, words, n).cpu()
+    again = ext.fp4_linear(x.cuda(), tiles, words, n).cpu()
+    want = om.linear_fp4(x, packed, scales)
+    assert same(got, again)
+    differ = got != want
+    print(f"  outputs differing from the oracle: {int(differ.sum())} of {differ.numel()}", flush=True)
+    assert float(differ.float().mean()) <= 0.01
+    if differ.any():
+        even, odd = om.decode_planes(packed, scales)
+        near = torch.zeros_like(differ)
+        for p, wp in ((0, even), (1, odd)):
+            xp, wd = x[:, p::2].double(), wp.double()
+            exact, abs_sum = xp @ wd.T, xp.abs() @ wd.abs().T
+            step = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0**-126))) - 7)
+            mid = torch.floor(exact / step) * step + step / 2  # the halfway point inside exact's bf16 interval
+            near |= (exact - mid).abs() <= 2.0**-20 * abs_sum
+        assert bool(near[differ].all())
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("rows", [3, 64, 128, 256, 300])
 def test_mxfp4_projection_equals_the_e4m3_projection_of_the_same_values(gpu, rows):
     print(f"mxfp4 linear rows={rows}", flush=True)

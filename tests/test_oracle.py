@@ -455,6 +455,36 @@ def test_mxfp4_codec_matches_the_references_decode_kat_and_converts_exactly_to_e
     assert torch.equal(dequantize_e4m3(coded, s8), values)
 
 
+def bf16_spacing(x: torch.Tensor) -> torch.Tensor:
+    """The distance between the two bf16 values around each of x (float64)."""
+    return torch.pow(2.0, torch.floor(torch.log2(x.abs().clamp_min(2.0**-126))) - 7)
+
+
+def test_fp4_planes_match_the_decode_kat_and_fp4_linear_sums_its_planes_apart():
+    """`decode_planes` against the reference's FP4 decode known-answer file (its even and odd columns); `linear_fp4`
+    (FP4Linear.forward, model.py:205-208): each plane's bf16 product within one bf16 spacing of its float64 sum (a
+    plane with the other parity's inputs, a plausible slip, misses it by far), and the output the two planes' bf16 sum."""
+    kat = load_file(GOLDEN / "fp4_decode_kat.safetensors")
+    _, exp = torch.frexp(kat["weight_scale"].float())
+    even, odd = om.decode_planes(kat["weight_packed"], (exp - 1 + 127).to(torch.uint8))
+    assert torch.equal(even, kat["expected"][:, ::2]) and torch.equal(odd, kat["expected"][:, 1::2])
+    assert not bool((even.view(torch.int16) == -32768).any())  # no negative zeros (sign-free codes)
+
+    g = torch.Generator().manual_seed(7)
+    n, k, rows = 64, 512, 16
+    packed = torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.uint8)
+    scale_bytes = torch.randint(118, 128, (n, k // 32), generator=g, dtype=torch.uint8)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    even, odd = om.decode_planes(packed, scale_bytes)
+    planes = [F.linear(x[:, p::2], w) for p, w in ((0, even), (1, odd))]
+    for p, w in ((0, even), (1, odd)):
+        exact = x[:, p::2].double() @ w.double().T
+        assert bool(((planes[p].double() - exact).abs() <= bf16_spacing(exact)).all())
+        wrong = x[:, 1 - p :: 2].double() @ w.double().T
+        assert not bool(((wrong - exact).abs() <= bf16_spacing(exact)).all())
+    assert torch.equal(om.linear_fp4(x, packed, scale_bytes), (planes[0].float() + planes[1].float()).to(torch.bfloat16))
+
+
 def _kv8_layer():
     """The FP8 KV golden scenario's single attention layer: config, weights, oracle state (cache bytes + scales)."""
     import make_golden_kv8 as g8
