@@ -53,6 +53,16 @@ def test_unsupported_shapes_and_names_are_refused():
     lib = ext.library()
     assert lib.q38_bind(h.h, b"linear_attn.recurrent_state", 0, ctypes.c_void_p(4096), 3) != 0
     assert b"needs" in lib.q38_last_error()
+    # The FP4Linear operator checks its shapes before any device work; its scratch holds bf16 input tiles (twice the
+    # e5m2 tiles of the FP8 projection's scratch) before the same GEMM counters and partial slots.
+    p = ctypes.c_void_p(4096)
+    assert lib.q38_fp4_linear(p, 4, 256, p, p, 100, p, p, None) != 0
+    assert b"N % 256" in lib.q38_last_error()
+    assert lib.q38_fp4_linear(None, 4, 256, p, p, 256, p, p, None) != 0
+    assert b"null" in lib.q38_last_error()
+    for rows, k in ((3, 256), (64, 5120), (256, 17408)):
+        extra = lib.q38_fp4_linear_scratch(rows, k) - lib.q38_fp8_linear_scratch(rows, k)
+        assert extra == lib.q38_tiles_size(rows, k)
 
 
 def test_weight_and_kv_cache_formats_size_their_buffers():
