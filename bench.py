@@ -345,7 +345,6 @@ def decode_main(args, cfg, engine, batch: int, context: int, max_seq_len: int) -
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
-        "ms_per_step_launches": round(ms_launches, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
