@@ -55,7 +55,8 @@ __device__ __forceinline__ void wait_and_barrier() {
 // stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the compiler's waits for its own loads only
 // get longer. NT marks the load non-temporal. The head's weight and scale streams (1.31 GB, read once per launch) use
 // it: L2 then keeps the activation tiles every workgroup rereads (the 256-row head's HBM reads fall from 2.2 GB to
-// 1.43 GB per launch). The decoder projections do not: there it changed no GEMM's time, and the attention kernel that
+// 1.43 GB per launch). So does the SwiGLU pair at 64 tokens (the decode step: 45.4 against 50.1 us). The other
+// decoder projections do not: at 256 tokens it changed no GEMM's time or slowed it, and the attention kernel that
 // follows them ran 55 instead of 46 us.
 template <int BYTES, bool NT = false>
 __device__ __forceinline__ void lds_load(const void* src, uint32_t dst) {
@@ -121,6 +122,7 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     static_assert(EPI != EPI_SWIGLU || FR % 2 == 0, "gate and up tiles pair up");
     static_assert(!F8 || (A8 && !W4), "the FP8 MFMA takes e4m3 weight tiles and e5m2 activation tiles");
     constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
+    constexpr bool NT_W = EPI == EPI_GROUPMAX || (EPI == EPI_SWIGLU && TT == 2);  // non-temporal weight streams
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
     __shared__ unsigned long long s_arrived;
 
@@ -187,10 +189,10 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             for (int i = 0; i < N_W; ++i) {
                 const int off = (i * NW + wave) * (64 * W_DMA);
                 const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS64 + k64) * WTB + off % WTB;
-                lds_load<W_DMA, EPI == EPI_GROUPMAX>(g + lane * W_DMA, sb + ACT_B + off);
+                lds_load<W_DMA, NT_W>(g + lane * W_DMA, sb + ACT_B + off);
             }
             const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS64 + k64) * 64;
-            lds_load<4, EPI == EPI_GROUPMAX>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
+            lds_load<4, NT_W>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
         }
     };
 
