@@ -598,7 +598,12 @@ hipError_t dispatch(const GemmArgs& a, int* splits_out, hipStream_t stream) {
                 if (EPI == EPI_PARTIAL && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4, F8>(a, splits_out, stream);
                 if (!balanced(512) && !balanced(256) && balanced(128)) return launch<2, 2, 2, 1, true, 5, EPI, W4, F8>(a, splits_out, stream);
             }
-            if constexpr (!A8) return launch<4, 2, 2, 1, false, 6, EPI, W4, F8>(a, splits_out, stream);
+            // bf16 activations at 64 tokens (the draft heads' group maxima): 512 x 64 tiles, 64 x 64 per wave, when N
+            // allows (248.3 against 261.5 us as 256 x 64 with 64 x 32 per wave, per 1.31 GB launch).
+            if constexpr (!A8) {
+                if (a.N % 512 == 0) return launch<8, 1, 2, 2, false, 3, EPI, W4, F8>(a, splits_out, stream);
+                return launch<4, 2, 2, 1, false, 6, EPI, W4, F8>(a, splits_out, stream);
+            }
             return wide ? launch<8, 1, 2, 2, A8, (A8 ? 4 : 3), EPI, W4, F8>(a, splits_out, stream)
                         : launch<4, 2, 2, 1, A8, 4, EPI, W4, F8>(a, splits_out, stream);
         case 32:
