@@ -28,6 +28,9 @@ typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
 
 #define Q38_HOST_DEVICE __host__ __device__ __forceinline__
 
+// A __shared__ object as an LDS address (its 32-bit value is the LDS byte offset the direct global -> LDS copies take).
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
 // The bf16 in the low / high half of a word, widened.

@@ -39,8 +39,6 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-
 namespace {
 
 // Wait until at most N vector-memory operations of this wave are outstanding, then meet the other waves. The memory

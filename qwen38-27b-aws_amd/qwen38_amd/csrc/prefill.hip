@@ -16,7 +16,8 @@
 //   attn_prefill_prep  (token): q and k RMS norms and RoPE in bf16 (model.py:565-577), q times 1/16 (exact) to scratch;
 //                      the chunk's keys and values into row slot's cache at start .. start + L - 1 (model.py:791-799;
 //                      the other rows' junk writes at the cache's end are left out: nothing reads them)
-//   attn_prefill       (32 tokens, query head), one wave: blocked_attention (model.py:170-191) over the row's cached
+//   attn_prefill       (128 tokens, query head), four waves of 32 tokens sharing each 32-position K/V sub-block through
+//                      LDS: blocked_attention (model.py:170-191) over the row's cached
 //                      positions before `start` and the chunk's own tokens causally, in the reference's blocks of 2048
 //                      positions of [cache, chunk]: per block the running max, e^(s - max) summed in float32, the
 //                      weights in bf16 times V on the MFMA (float32 sums, rounded to bf16 once per block, as the
@@ -194,6 +195,51 @@ constexpr int QP = 256;  // bf16 per scaled query row in the scratch
 __device__ __forceinline__ v8bf16 load8p(const bf16_t* p) { return *(const v8bf16*)p; }
 __device__ __forceinline__ int drow(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
+// Direct global -> LDS copy of one dword per lane from base + off (base wave-uniform, in scalar registers): lane l's 4
+// bytes land at LDS address dst + 4 l (dst wave-uniform). Inline assembly, so the compiler neither counts it nor waits
+// for it; the ring's own vmcnt waits below cover it.
+__device__ __forceinline__ void lds_dword(const void* base, uint32_t off, uint32_t dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst);
+    asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding (its copies into the stage about to be
+// read have landed), then meet the other waves. The memory clobber keeps LDS reads after it.
+template <int N>
+__device__ __forceinline__ void ring_ready() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Every LDS read of this wave has returned; then meet the other waves, so the stage just read can be refilled.
+__device__ __forceinline__ void ring_release() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS layout of one 32-position sub-block (E bytes per element), swizzled at the granularity the MFMA operand reads use
+// so that they are free of bank conflicts, and filled by coalesced dword copies (each copy instruction of a wave takes
+// 256 contiguous bytes of the cache, permuted within rows). The maps are their own inverses.
+//   K [32 positions][256 dims]: bf16 16-byte chunk c of row r at chunk c ^ (r & 15); e4m3 8-byte chunk c at c ^ r.
+//   V [256 dims][32 positions]: bf16 8-byte chunk c of row d at c ^ ((d >> 2) & 7); e4m3 4-byte chunk c at
+//   c ^ (((d >> 3) & 3) << 1).
+template <int E>
+__device__ __forceinline__ uint32_t k_swz(uint32_t byte) {  // byte offset in the sub-block, either direction
+    if constexpr (E == 2) {
+        const uint32_t r = byte >> 9;
+        return byte ^ ((r & 15) << 4);
+    } else {
+        const uint32_t r = byte >> 8;
+        return byte ^ ((r & 31) << 3);
+    }
+}
+template <int E>
+__device__ __forceinline__ uint32_t v_swz(uint32_t byte) {
+    if constexpr (E == 2) {
+        const uint32_t d = byte >> 6;
+        return byte ^ (((d >> 2) & 7) << 3);
+    } else {
+        const uint32_t d = byte >> 5;
+        return byte ^ (((d >> 3) & 3) << 3);
+    }
+}
+
 }  // namespace
 
 // Grid (token): wave w normalises and rotates rows w, w + 4, ...: query heads (scaled by 1/16 into qs), then the KV
@@ -261,75 +307,144 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAtt
     }
 }
 
-// Grid (tiles of 32 tokens, query head), one wave. Scores by v_mfma_f32_32x32x16_bf16 with the keys as A (32 positions)
-// and the queries as B (32 tokens): lane l holds token t0 + l % 32 and positions drow(i, l). The weights go straight
-// from those registers into the A operand of weights x V (two MFMA steps of 16 positions: rows drow(0..7) and
-// drow(8..15) of the lane), with V's B operand loaded in the same position order from the transposed cache. With KV8
-// the cached bytes (the chunk's own included, written by the prep kernel) widen to bf16(e4m3 x scale) as they load.
+// Grid (query head, tiles of 128 tokens), four waves: wave w takes tokens T0 + 32 w .. + 31. The four waves see the
+// same cached positions, so each sub-block of 32 positions is copied into LDS once per workgroup (double-buffered: the
+// next sub-block's copies are in flight while the current one is used) and read by all four.
+// Scores by v_mfma_f32_32x32x16_bf16 with the keys as A (32 positions) and the queries as B (32 tokens): lane l holds
+// token t0 + l % 32 and positions drow(i, l); MFMA step m takes dims 8 m .. 8 m + 7 in lanes 0-31 and 128 + 8 m .. in
+// lanes 32-63 (the queries in the same order). The weights go straight from those registers into the A operand of
+// weights x V (two MFMA steps of 16 positions: rows drow(0..7) and drow(8..15) of the lane), with V's B operand read in
+// the same position order from the transposed sub-block. With KV8 the cached bytes (the chunk's own included, written by
+// the prep kernel) widen to bf16(e4m3 x scale) as they are read from LDS. A wave skips the sub-blocks none of its tokens
+// sees (as if it ran alone) but still copies its share and meets the barriers; the output so far stays in registers.
 template <bool KV8>
-__global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs a) {
-    __shared__ float so[32][256 + 4];  // output so far, [token][dim]
-    __shared__ float s_scale[32];
-    const int tile = blockIdx.x, hq = blockIdx.y, lane = threadIdx.x;
-    const int L = a.L, S = a.S, G = a.Hq / a.Hkv, kvh = hq / G, t0 = tile * 32;
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs a) {
+    constexpr int E = KV8 ? 1 : 2;        // bytes per cached element
+    constexpr int SUB = 32 * 256 * E;     // bytes of one K (or V) sub-block
+    constexpr int NCP = SUB / 1024;       // dword copies per wave per sub-block of one array
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[2][2][SUB];  // [stage][K, V]
+    __shared__ float s_row[4][32];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Workgroups start in the order of their linear id, x fastest, and go to the XCDs in turn: the last (heaviest,
+    // causally) tiles start first, and with 8 | Hq the query heads of one XCD are consecutive (one KV head's, when
+    // G >= Hq / 8), so its L2 holds few KV heads' keys and values.
+    const int T0 = (gridDim.y - 1 - blockIdx.y) * 128;
+    const int hq = a.Hq % 8 ? blockIdx.x : (blockIdx.x % 8) * (a.Hq / 8) + blockIdx.x / 8;
+    const int L = a.L, S = a.S, G = a.Hq / a.Hkv, kvh = hq / G, t0 = T0 + 32 * wv;
     const int slot = *a.slot, start = *a.start;
     if (start < 0 || start + L > S || slot < 0 || slot >= a.rows) return;  // the host checks these too
+    const bool live = t0 < L;         // wave-uniform: the wave has tokens
     const int tq = t0 + (lane & 31);  // this lane's token (query)
     const size_t head = (size_t)slot * a.Hkv + kvh;
     const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f, vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
+    const uint8_t* kg = (const uint8_t*)a.k_cache + head * S * 256 * E;
+    const uint8_t* vg = (const uint8_t*)a.v_cache + head * S * 256 * E;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)LDS_PTR(&ring[0][0][0]);
 
     v8bf16 qf[16];
-    {
+    if (live) {
         const bf16_t* qp = a.qs + ((size_t)hq * L + tq) * QP + (lane >> 5) * 128;
 #pragma unroll
         for (int m = 0; m < 16; ++m) qf[m] = load8p(qp + m * 8);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[m][e] = (__bf16)0.0f;
     }
-    for (int e = lane; e < 32 * 256; e += 64) so[e / 256][e % 256] = 0.0f;
+    v16f so[8];  // output so far: so[db][i] is token drow(i, l), dim 32 db + l % 32
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) so[db][i] = 0.0f;
     float best = 2.0f * -1e4f, total = 0.0f;
 
-    // Scores of the 32 cached positions from p0 against the 32 tokens; visible(pos_index) decides the mask.
-    auto score = [&](int p0, v16f& acc) {
-        const size_t ko = (head * S + p0 + (lane & 31)) * 256 + (lane >> 5) * 128;
-        v8bf16 kf[16];
-        if constexpr (KV8) {
-            uint2 r[16];
+    // This wave's dword copies of the sub-block at p0 into stage st: copy j of lane l fills LDS byte at + 4 l of the
+    // stage, at = 256 (4 j + w), from the cache byte the swizzle maps there. A wave's 256 bytes lie in rows that share
+    // one swizzle (K rows hold 256 or 512 bytes; V rows 64 or 32 bytes, in groups of 4 or 8 with one pattern), so that
+    // byte is at + (4 l ^ X) with X = swz(at) ^ at uniform over the wave.
+    auto copy = [&](int p0, int st, bool with_v) {
+        const uint32_t dst = lds0 + (uint32_t)st * 2 * SUB;
+        const uint8_t* ks = kg + (size_t)p0 * 256 * E;
 #pragma unroll
-            for (int m = 0; m < 16; ++m) r[m] = *(const uint2*)((const uint8_t*)a.k_cache + ko + m * 8);
-#pragma unroll
-            for (int m = 0; m < 16; ++m) kf[m] = kv_widen8(r[m].x, r[m].y, ksc);
-        } else {
-#pragma unroll
-            for (int m = 0; m < 16; ++m) kf[m] = load8p(a.k_cache + ko + m * 8);
+        for (int j = 0; j < NCP; ++j) {
+            const uint32_t at = (j * 4 + wv) * 256;
+            lds_dword(ks + at, (uint32_t)(lane * 4) ^ (k_swz<E>(at) ^ at), dst + at);
         }
+        if (with_v) {
+            const uint8_t* vs = vg + (size_t)(p0 >> 5) * SUB;
+#pragma unroll
+            for (int j = 0; j < NCP; ++j) {
+                const uint32_t at = (j * 4 + wv) * 256;
+                lds_dword(vs + at, (uint32_t)(lane * 4) ^ (v_swz<E>(at) ^ at), dst + SUB + at);
+            }
+        }
+    };
+    // Scores of the sub-block in stage st against the wave's 32 tokens.
+    auto score = [&](int st, v16f& acc) {
+        const uint8_t* kl = &ring[st][0][0];
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 16; ++m) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[m], qf[m], acc, 0, 0, 0);
+        for (int m = 0; m < 16; ++m) {
+            v8bf16 kf;
+            if constexpr (KV8) {
+                const uint2 r = *(const uint2*)(kl + k_swz<1>((lane & 31) * 256 + (lane >> 5) * 128 + m * 8));
+                kf = kv_widen8(r.x, r.y, ksc);
+            } else {
+                kf = *(const v8bf16*)(kl + k_swz<2>((lane & 31) * 512 + (lane >> 5) * 256 + m * 16));
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[m], acc, 0, 0, 0);
+        }
     };
-    const int t_max = min(t0 + 31, L - 1);
+    const int t_max = min(t0 + 31, L - 1), t_top = min(T0 + 127, L - 1);  // the wave's and the workgroup's last token
     const int nblocks = (S + L + 2047) / 2048;
     for (int b = 0; b < nblocks; ++b) {
         // Sub-blocks of 32 cache positions (aligned, as the transposed V cache is): the cached positions [c_lo, c_hi),
-        // then the positions [p_lo, p_hi) the chunk's own tokens o_lo .. o_hi - 1 were written to.
+        // then the positions [p_lo, p_hi) the chunk's own tokens o_lo .. o_hi - 1 were written to. n counts the
+        // workgroup's sub-blocks, nw this wave's (a prefix of them: the same positions in the same order).
         const int c_lo = 2048 * b, c_hi = min(min(2048 * (b + 1), S), start);
-        const int o_lo = max(0, 2048 * b - S), o_hi = min(min(2048 * (b + 1) - S, L), t_max + 1);
+        const int o_lo = max(0, 2048 * b - S), o_end = min(2048 * (b + 1) - S, L);
+        const int o_hi = min(o_end, t_max + 1), o_top = min(o_end, t_top + 1);
         const int p_lo = start + o_lo, p_hi = start + o_hi, p_al = p_lo & ~31;
-        const int n_c = c_hi > c_lo ? (c_hi - c_lo + 31) / 32 : 0, n_o = o_hi > o_lo ? (p_hi - p_al + 31) / 32 : 0;
-        if (n_c + n_o == 0) continue;
+        const int n_c = c_hi > c_lo ? (c_hi - c_lo + 31) / 32 : 0;
+        const int n = n_c + (o_top > o_lo ? (start + o_top - p_al + 31) / 32 : 0);
+        const int nw = live ? n_c + (o_hi > o_lo ? (p_hi - p_al + 31) / 32 : 0) : 0;
+        if (n == 0) continue;
         auto base = [&](int sb) { return sb < n_c ? c_lo + 32 * sb : p_al + 32 * (sb - n_c); };
         auto visible = [&](int sb, int i) {  // sub-block sb, accumulator row i
             const int pos = base(sb) + drow(i, lane);
             if (sb < n_c) return pos < c_hi;
             return pos >= p_lo && pos < p_hi && pos - start <= tq;
         };
+        auto whole = [&](int sb) {  // wave-uniform: every position of sub-block sb is visible to every token of the wave
+            const int p0 = base(sb);
+            if (sb < n_c) return p0 + 32 <= c_hi;
+            return p0 >= p_lo && p0 + 32 <= p_hi && p0 + 31 - start <= t0;
+        };
         // Pass 1: the block's maximum per token.
         float mx = -INFINITY;
-        for (int sb = 0; sb < n_c + n_o; ++sb) {
-            v16f acc;
-            score(base(sb), acc);
+        copy(base(0), 0, false);
+        for (int sb = 0; sb < n; ++sb) {
+            if (sb + 1 < n) {
+                copy(base(sb + 1), (sb + 1) & 1, false);
+                ring_ready<NCP>();
+            } else {
+                ring_ready<0>();
+            }
+            if (sb < nw) {
+                v16f acc;
+                score(sb & 1, acc);
+                if (whole(sb)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (visible(sb, i)) mx = fmaxf(mx, rbf(acc[i]));
+                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, rbf(acc[i]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (visible(sb, i)) mx = fmaxf(mx, rbf(acc[i]));
+                }
+            }
+            ring_release();
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float nb = fmaxf(best, mx);  // a token with nothing visible here keeps its maximum
@@ -341,64 +456,81 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const PrefillAttnArgs 
 #pragma unroll
             for (int i = 0; i < 16; ++i) pv[db][i] = 0.0f;
         float wsum = 0.0f;
-        for (int sb = 0; sb < n_c + n_o; ++sb) {
-            v16f acc;
-            const int p0 = base(sb);
-            score(p0, acc);
-            float w[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                w[i] = visible(sb, i) ? expf(rbf(acc[i]) - nb) : 0.0f;
-                wsum += w[i];
+        copy(base(0), 0, true);
+        for (int sb = 0; sb < n; ++sb) {
+            if (sb + 1 < n) {
+                copy(base(sb + 1), (sb + 1) & 1, true);
+                ring_ready<2 * NCP>();
+            } else {
+                ring_ready<0>();
             }
-            typedef unsigned u4_ __attribute__((ext_vector_type(4)));
+            if (sb < nw) {
+                v16f acc;
+                score(sb & 1, acc);
+                float w[16];
+                if (whole(sb)) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u4_ pw = {pk_bf16(w[8 * ks + 0], w[8 * ks + 1]), pk_bf16(w[8 * ks + 2], w[8 * ks + 3]),
-                                pk_bf16(w[8 * ks + 4], w[8 * ks + 5]), pk_bf16(w[8 * ks + 6], w[8 * ks + 7])};
-                const v8bf16 pa = __builtin_bit_cast(v8bf16, pw);
-                // Positions of this step in this lane: 16 ks + 4 (l / 32) + [0, 4) and 16 ks + 8 + 4 (l / 32) + [0, 4).
-                const int q0 = p0 + 16 * ks + 4 * (lane >> 5);
-                const size_t vb = (head * S + (q0 & ~31)) * 256 + (q0 & 31);
+                    for (int i = 0; i < 16; ++i) w[i] = expf(rbf(acc[i]) - nb);
+                } else {
 #pragma unroll
-                for (int db = 0; db < 8; ++db) {
-                    const size_t vo = vb + (size_t)(db * 32 + (lane & 31)) * 32;
-                    v8bf16 vw;
-                    if constexpr (KV8) {
-                        const uint8_t* vp = (const uint8_t*)a.v_cache + vo;
-                        vw = kv_widen8(*(const uint32_t*)vp, *(const uint32_t*)(vp + 8), vsc);
-                    } else {
-                        const uint2 lo = *(const uint2*)(a.v_cache + vo), hi = *(const uint2*)(a.v_cache + vo + 8);
-                        vw = __builtin_bit_cast(v8bf16, (u4_){lo.x, lo.y, hi.x, hi.y});
+                    for (int i = 0; i < 16; ++i) w[i] = visible(sb, i) ? expf(rbf(acc[i]) - nb) : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) wsum += w[i];
+                const uint8_t* vl = &ring[sb & 1][1][0];
+                typedef unsigned u4_ __attribute__((ext_vector_type(4)));
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const u4_ pw = {pk_bf16(w[8 * ks + 0], w[8 * ks + 1]), pk_bf16(w[8 * ks + 2], w[8 * ks + 3]),
+                                    pk_bf16(w[8 * ks + 4], w[8 * ks + 5]), pk_bf16(w[8 * ks + 6], w[8 * ks + 7])};
+                    const v8bf16 pa = __builtin_bit_cast(v8bf16, pw);
+                    // Positions of this step in this lane: 16 ks + 4 (l / 32) + [0, 4) and 16 ks + 8 + 4 (l / 32) + [0, 4).
+                    const int q0 = 16 * ks + 4 * (lane >> 5);
+#pragma unroll
+                    for (int db = 0; db < 8; ++db) {
+                        const int d = db * 32 + (lane & 31);
+                        v8bf16 vw;
+                        if constexpr (KV8) {
+                            const uint32_t lo = *(const uint32_t*)(vl + v_swz<1>(d * 32 + q0));
+                            const uint32_t hi = *(const uint32_t*)(vl + v_swz<1>(d * 32 + q0 + 8));
+                            vw = kv_widen8(lo, hi, vsc);
+                        } else {
+                            const uint2 lo = *(const uint2*)(vl + v_swz<2>(d * 64 + q0 * 2));
+                            const uint2 hi = *(const uint2*)(vl + v_swz<2>(d * 64 + q0 * 2 + 16));
+                            vw = __builtin_bit_cast(v8bf16, (u4_){lo.x, lo.y, hi.x, hi.y});
+                        }
+                        pv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, vw, pv[db], 0, 0, 0);
                     }
-                    pv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, vw, pv[db], 0, 0, 0);
                 }
             }
+            ring_release();
         }
+        if (nw == 0) continue;  // nothing of this block is visible to the wave: it keeps its state
         wsum += __shfl_xor(wsum, 32);
         total = total * scale + wsum;
         best = nb;
-        if (lane < 32) s_scale[lane] = scale;
+        if (lane < 32) s_row[wv][lane] = scale;
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land before its reads
 #pragma unroll
         for (int db = 0; db < 8; ++db)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = drow(i, lane), col = db * 32 + (lane & 31);
-                so[row][col] = so[row][col] * s_scale[row] + rbf(pv[db][i]);
-            }
+            for (int i = 0; i < 16; ++i) so[db][i] = so[db][i] * s_row[wv][drow(i, lane)] + rbf(pv[db][i]);
     }
     // out / total in bf16, times bf16 sigmoid(gate), e5m2 tiles for o_proj.
-    if (lane < 32) s_scale[lane] = total;
+    if (!live) return;
+    if (lane < 32) s_row[wv][lane] = total;
     __builtin_amdgcn_s_waitcnt(0xc07f);
     const int act_k = a.Hq * 256;
-    for (int e = lane; e < 32 * 256; e += 64) {
-        const int row = e / 256, d = e % 256, t = t0 + row;
-        if (t >= L) continue;
-        const float o = rbf(so[row][d] / s_scale[row]);
-        const float gt = bf2f(a.qkv[(size_t)t * a.ld + (size_t)hq * 512 + 256 + d]);
-        a.act[act_offset(t, hq * 256 + d, act_k)] = (uint8_t)e5m2_byte(rbf(o * rbf(sigmoidf_(gt))));
-    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = drow(i, lane), d = db * 32 + (lane & 31), t = t0 + row;
+            if (t >= L) continue;
+            const float o = rbf(so[db][i] / s_row[wv][row]);
+            const float gt = bf2f(a.qkv[(size_t)t * a.ld + (size_t)hq * 512 + 256 + d]);
+            a.act[act_offset(t, hq * 256 + d, act_k)] = (uint8_t)e5m2_byte(rbf(o * rbf(sigmoidf_(gt))));
+        }
 }
 
 hipError_t q38_attn_prefill(const PrefillAttnArgs& a, hipStream_t stream) {
@@ -406,10 +538,10 @@ hipError_t q38_attn_prefill(const PrefillAttnArgs& a, hipStream_t stream) {
     if (a.kv8) {
         if (!a.k_scale || !a.v_scale) return hipErrorInvalidValue;
         hipLaunchKernelGGL(attn_prefill_prep_kernel<true>, dim3(a.L), dim3(256), 0, stream, a);
-        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(a.L / 32, a.Hq), dim3(64), 0, stream, a);
+        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(a.Hq, (a.L + 127) / 128), dim3(256), 0, stream, a);
     } else {
         hipLaunchKernelGGL(attn_prefill_prep_kernel<false>, dim3(a.L), dim3(256), 0, stream, a);
-        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(a.L / 32, a.Hq), dim3(64), 0, stream, a);
+        if (!a.keys_only) hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(a.Hq, (a.L + 127) / 128), dim3(256), 0, stream, a);
     }
     return hipGetLastError();
 }
