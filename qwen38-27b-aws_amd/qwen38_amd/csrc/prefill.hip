@@ -204,10 +204,11 @@ __device__ __forceinline__ void lds_dword(const void* base, uint32_t off, uint32
 }
 
 // Wait until at most N of this wave's vector-memory operations are outstanding (its copies into the stage about to be
-// read have landed), then meet the other waves. The memory clobber keeps LDS reads after it.
+// read have landed) and its LDS reads have returned, then meet the other waves: after it the stage read one step
+// before is free. The memory clobber keeps LDS reads after it.
 template <int N>
 __device__ __forceinline__ void ring_ready() {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Every LDS read of this wave has returned; then meet the other waves, so the stage just read can be refilled.
@@ -308,21 +309,25 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const PrefillAtt
 }
 
 // Grid (query head, tiles of 128 tokens), four waves: wave w takes tokens T0 + 32 w .. + 31. The four waves see the
-// same cached positions, so each sub-block of 32 positions is copied into LDS once per workgroup (double-buffered: the
-// next sub-block's copies are in flight while the current one is used) and read by all four.
+// same cached positions, so each sub-block of 32 positions is copied into LDS once per workgroup (a ring of three
+// stages: the next two sub-blocks' copies are in flight while the current one is used, one barrier per sub-block) and
+// read by all four.
 // Scores by v_mfma_f32_32x32x16_bf16 with the keys as A (32 positions) and the queries as B (32 tokens): lane l holds
 // token t0 + l % 32 and positions drow(i, l); MFMA step m takes dims 8 m .. 8 m + 7 in lanes 0-31 and 128 + 8 m .. in
 // lanes 32-63 (the queries in the same order). The weights go straight from those registers into the A operand of
 // weights x V (two MFMA steps of 16 positions: rows drow(0..7) and drow(8..15) of the lane), with V's B operand read in
 // the same position order from the transposed sub-block. With KV8 the cached bytes (the chunk's own included, written by
-// the prep kernel) widen to bf16(e4m3 x scale) as they are read from LDS. A wave skips the sub-blocks none of its tokens
-// sees (as if it ran alone) but still copies its share and meets the barriers; the output so far stays in registers.
+// the prep kernel) widen to bf16(e4m3 x scale) as they are read from LDS. Every wave runs all of the workgroup's
+// sub-blocks: those past its own tokens (at most three, on the diagonal, where the workgroup waits for its last wave
+// anyway) hold chunk positions the prep kernel wrote, so they add weights of exactly zero times finite values, which
+// leaves the sums as they were (none of them is -0: they start at +0). A block none of a wave's tokens sees leaves
+// its state alone. The output so far stays in registers.
 template <bool KV8>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs a) {
     constexpr int E = KV8 ? 1 : 2;        // bytes per cached element
     constexpr int SUB = 32 * 256 * E;     // bytes of one K (or V) sub-block
     constexpr int NCP = SUB / 1024;       // dword copies per wave per sub-block of one array
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[2][2][SUB];  // [stage][K, V]
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[3][2][SUB];  // [stage][K, V]
     __shared__ float s_row[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Workgroups start in the order of their linear id, x fastest, and go to the XCDs in turn: the last (heaviest,
@@ -412,40 +417,34 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs
         const int nw = live ? n_c + (o_hi > o_lo ? (p_hi - p_al + 31) / 32 : 0) : 0;
         if (n == 0) continue;
         auto base = [&](int sb) { return sb < n_c ? c_lo + 32 * sb : p_al + 32 * (sb - n_c); };
-        auto visible = [&](int sb, int i) {  // sub-block sb, accumulator row i
-            const int pos = base(sb) + drow(i, lane);
-            if (sb < n_c) return pos < c_hi;
-            return pos >= p_lo && pos < p_hi && pos - start <= tq;
-        };
-        auto whole = [&](int sb) {  // wave-uniform: every position of sub-block sb is visible to every token of the wave
+        // The rows r (positions base(sb) + r) of sub-block sb this lane's token sees: rlo <= r < rhi. Cached
+        // positions below c_hi; the chunk's from p_lo, below p_hi and up to the token's own.
+        auto window = [&](int sb, int& rlo, int& rhi) {
             const int p0 = base(sb);
-            if (sb < n_c) return p0 + 32 <= c_hi;
-            return p0 >= p_lo && p0 + 32 <= p_hi && p0 + 31 - start <= t0;
+            rlo = sb < n_c ? 0 : p_lo - p0;
+            rhi = (sb < n_c ? c_hi : min(p_hi, start + tq + 1)) - p0;
         };
         // Pass 1: the block's maximum per token.
         float mx = -INFINITY;
         copy(base(0), 0, false);
-        for (int sb = 0; sb < n; ++sb) {
-            if (sb + 1 < n) {
-                copy(base(sb + 1), (sb + 1) & 1, false);
+        if (n > 1) copy(base(1), 1, false);
+        for (int sb = 0, st = 0; sb < n; ++sb, st = st == 2 ? 0 : st + 1) {
+            if (sb + 1 < n)
                 ring_ready<NCP>();
-            } else {
+            else
                 ring_ready<0>();
-            }
-            if (sb < nw) {
-                v16f acc;
-                score(sb & 1, acc);
-                if (whole(sb)) {
+            if (sb + 2 < n) copy(base(sb + 2), st == 0 ? 2 : st - 1, false);
+            v16f acc;
+            score(st, acc);
+            int rlo, rhi;
+            window(sb, rlo, rhi);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, rbf(acc[i]));
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (visible(sb, i)) mx = fmaxf(mx, rbf(acc[i]));
-                }
+            for (int i = 0; i < 16; ++i) {
+                const int r = drow(i, lane);
+                mx = (r >= rlo) & (r < rhi) ? fmaxf(mx, rbf(acc[i])) : mx;
             }
-            ring_release();
         }
+        ring_release();
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float nb = fmaxf(best, mx);  // a token with nothing visible here keeps its maximum
         const float scale = expf(best - nb);
@@ -457,27 +456,28 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs
             for (int i = 0; i < 16; ++i) pv[db][i] = 0.0f;
         float wsum = 0.0f;
         copy(base(0), 0, true);
-        for (int sb = 0; sb < n; ++sb) {
-            if (sb + 1 < n) {
-                copy(base(sb + 1), (sb + 1) & 1, true);
+        if (n > 1) copy(base(1), 1, true);
+        for (int sb = 0, st = 0; sb < n; ++sb, st = st == 2 ? 0 : st + 1) {
+            if (sb + 1 < n)
                 ring_ready<2 * NCP>();
-            } else {
+            else
                 ring_ready<0>();
-            }
-            if (sb < nw) {
+            if (sb + 2 < n) copy(base(sb + 2), st == 0 ? 2 : st - 1, true);
+            {
                 v16f acc;
-                score(sb & 1, acc);
+                score(st, acc);
+                int rlo, rhi;
+                window(sb, rlo, rhi);
                 float w[16];
-                if (whole(sb)) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) w[i] = expf(rbf(acc[i]) - nb);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) w[i] = visible(sb, i) ? expf(rbf(acc[i]) - nb) : 0.0f;
+                for (int i = 0; i < 16; ++i) {
+                    const int r = drow(i, lane);
+                    const float e = expf(rbf(acc[i]) - nb);
+                    w[i] = (r >= rlo) & (r < rhi) ? e : 0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) wsum += w[i];
-                const uint8_t* vl = &ring[sb & 1][1][0];
+                const uint8_t* vl = &ring[st][1][0];
                 typedef unsigned u4_ __attribute__((ext_vector_type(4)));
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
@@ -503,8 +503,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs
                     }
                 }
             }
-            ring_release();
         }
+        ring_release();
         if (nw == 0) continue;  // nothing of this block is visible to the wave: it keeps its state
         wsum += __shfl_xor(wsum, 32);
         total = total * scale + wsum;
