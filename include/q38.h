@@ -112,8 +112,9 @@ void q38_destroy(q38_handle* h);
  *   bf16 [B*K][.], the layer's normed input (gated-delta layers), the mixer's projection output (the gated-delta
  *   in_proj_z part, Hv*128 wide; or the attention q|gate|k|v projection) and the residual stream after the mixer; then
  *   the e5m2 activation tiles of the out_proj/o_proj input, the MLP input and the down projection's input, for the
- *   first B*K tokens rounded up to 32. For stage-by-stage comparison with another implementation; unbound, nothing is
- *   copied. */
+ *   first B*K tokens rounded up to 32; last, bf16 [B*K][H], the residual stream entering the layer. For
+ *   stage-by-stage comparison with another implementation; unbound, nothing is copied. The MTP layer (index
+ *   num_layers) takes one too, filled by q38_mtp_step (its layer input is the fc output). */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
 int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
 
@@ -249,6 +250,14 @@ int q38_accept(q38_handle* h, const int32_t* picks, const int32_t* drafts, const
  * embeddings and a bound "rope_table" (bf16 [max_seq_len][2][rotary_dim]: cos then sin of each position). */
 int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
                   uint16_t* hidden, int32_t* picks, int32_t* drafts, void* stream);
+/* The verify half of q38_spec_step for drafts the host made: the reference's Scheduler._verify_step without an MTP
+ * drafter (scheduler.py:269-301), whose drafts come from the row's own history (`Drafter.draft`, drafting.py:44-51,
+ * padded with the row's last token, scheduler.py:276-282). drafts int32 [B][K-1] is read; position, index, match,
+ * accepted, hidden and picks are read and updated as by q38_spec_step: [picks[match], drafts] per row is embedded and
+ * verified, the head picks K tokens per row over all B*K rows (top-4 recheck) and acceptance sets match and accepted.
+ * The emitted tokens of row b are picks[b][0..match[b]]. Needs the head, the embeddings and the bound "rope_table". */
+int q38_verify_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
+                    uint16_t* hidden, int32_t* picks, const int32_t* drafts, void* stream);
 /* q38_spec_step as one HIP graph: the step is captured on first use for the current gated-delta parity and these
  * argument pointers (at most one graph per parity is kept; other pointers, or any q38_bind, capture again) and
  * replayed with hipGraphLaunch on `stream`, the host's parity flipping as after q38_spec_step. The same kernels with

@@ -6,7 +6,10 @@ What it restates, from /root/reference/qwen38_inf2:
 * `Scheduler._mtp_drafts` (scheduler.py:160-193): K - 1 drafts per running row from the MTP layer, the first call over
   the row's last K positions, each later one on the previous call's output and the token it drafted;
 * `Scheduler._verify_step` (scheduler.py:269-301): ``[last token] + drafts`` per row, one verify call, the head over
-  every row's K tokens, longest-prefix acceptance, the next step's MTP seed;
+  every row's K tokens, longest-prefix acceptance, the next step's MTP seed; without an MTP drafter the drafts come
+  from the row's own history by prompt lookup, padded with the row's last token (scheduler.py:276-282);
+* `lookup_draft` (drafting.py:11-24), the history scan that `Drafter.draft` (drafting.py:44-51) equals (reference
+  tests/test_scheduler.py:177-185), which the restated step calls on the row's tokens;
 * the parts of `Scheduler.run_sessions`, `_prefill` and `_mtp_prefill` (scheduler.py:110-158, 201-267) a speculative
   run needs, for single-turn prompts without prefix reuse, so the reference's invariants can run on it;
 * graph adapters with the reference's call forms over `oracle.model`: `Step` (`Qwen38Step.forward`, model.py:983-995),
@@ -20,6 +23,9 @@ Pinning:
 * tests/golden/spec_tiny.safetensors, written by tests/golden/make_golden_spec.py from the reference's own
   `Scheduler._verify_step` (which calls `_mtp_drafts`) over three speculative steps on config 0 shapes in bf16: drafts,
   picks, matches, emitted tokens, hidden states and state digests bit for bit;
+* tests/golden/lookup_tiny.safetensors, written by tests/golden/make_golden_lookup.py from the reference's own
+  `Scheduler._verify_step` with no MTP drafter (its `Drafter` drafts) over five steps on config 0 shapes: drafts,
+  picks, matches, hidden states and state digests bit for bit;
 * tests/test_oracle_spec.py holds the reference's invariants on it: speculation with MTP drafts gives the tokens plain
   greedy decoding gives, and each step's first draft is what the MTP layer gives over the sequence's true history
   (reference tests/test_prefill.py:267-289, 380-448); and a fake-device contract in the style of reference
@@ -96,6 +102,23 @@ def mtp_prefill_inputs(cfg, slot: int, start: int, n_valid: int, chunk: int, dty
     cos, sin = rotary(cfg, start + 1 + torch.arange(chunk), dtype)
     out["cos"], out["sin"] = cos.unsqueeze(0), sin.unsqueeze(0)
     return out
+
+
+# ----------------------------------------------------------------------------------------------- prompt lookup
+
+
+def lookup_draft(history: Sequence[int], count: int, max_match: int = 4, min_match: int = 1) -> list[int]:
+    """drafting.py:11-24: for n from ``max_match`` (at most len - 1) down to ``min_match``, the latest earlier start
+    of the history's last n tokens; the first n with such a start drafts the up to ``count`` tokens after it. Empty
+    when no length matches."""
+    tokens = list(history)
+    size = len(tokens)
+    for n in range(min(max_match, size - 1), min_match - 1, -1):
+        tail = tokens[size - n :]
+        for start in range(size - n - 1, -1, -1):
+            if tokens[start : start + n] == tail:
+                return tokens[start + n : start + n + count]
+    return []
 
 
 # ----------------------------------------------------------------------------------------------- graph adapters
@@ -229,10 +252,19 @@ class Scheduler:
         return drafts
 
     def verify_step(self, slots: Sequence[Row | None], positions, active, ready) -> list[list[int]]:
-        """scheduler.py:269-301, with MTP drafts. Returns each ready slot's new tokens (the matching drafts, then the
-        model's own next pick) and leaves each ready row's next seed ``(hidden [K, H], picks, position, match)``."""
+        """scheduler.py:269-301. Drafts from the MTP layer when there is one, else from each row's own history
+        (`lookup_draft`, padded to K - 1 with the row's last token). Returns each ready slot's new tokens (the matching
+        drafts, then the model's own next pick); with MTP it leaves each ready row's next seed ``(hidden [K, H], picks,
+        position, match)``. ``last`` keeps the step's drafts, hidden states, picks and matches."""
         k = self.k
-        drafts = self.mtp_drafts(slots)
+        if self.mtp:
+            drafts = self.mtp_drafts(slots)
+        else:
+            drafts = {}
+            for slot, row in enumerate(slots):
+                if row is not None:
+                    found = lookup_draft(row.ids, k - 1)
+                    drafts[slot] = found + [row.ids[-1]] * (k - 1 - len(found))
         tokens = []
         for slot, row in enumerate(slots):
             tokens += [row.ids[-1]] + drafts[slot] if row is not None else [0] * k
@@ -241,7 +273,7 @@ class Scheduler:
         hidden = self.verify(inputs_embeds=embeds,
                              **verify_inputs(self.cfg, positions, k, self.max_seq_len, self.dtype, active, accepted))
         chosen = self.head.next_tokens(hidden[ready].reshape(len(ready) * k, 1, -1))
-        emitted = []
+        emitted, picked, matched = [], {}, {}
         for i, slot in enumerate(ready):
             picks, draft = chosen[i * k : (i + 1) * k], drafts[slot]
             match = 0
@@ -250,8 +282,10 @@ class Scheduler:
             self.accepted[slot] = match + 1
             self.drafted_tokens += match
             emitted.append(picks[: match + 1])
-            slots[slot].seed = (hidden[slot], picks, positions[slot], match)
-        self.last = {"drafts": drafts, "hidden": hidden, "chosen": chosen}
+            picked[slot], matched[slot] = picks, match
+            if self.mtp:
+                slots[slot].seed = (hidden[slot], picks, positions[slot], match)
+        self.last = {"drafts": drafts, "hidden": hidden, "chosen": chosen, "picks": picked, "match": matched}
         return emitted
 
     # -------------------------------------------------------------------------------------- prompts and the run loop

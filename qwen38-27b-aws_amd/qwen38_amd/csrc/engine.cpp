@@ -140,7 +140,8 @@ bool fp4_layer(const q38_handle* h, int layer) {
 // after the mixer [T][H]; then, as the e5m2 activation tiles the GEMMs read (for the first T32 = T rounded up to 32
 // tokens), the out_proj input (M = Hv*dk or Hq*hd inputs), the MLP input (H) and the down projection's input (I). For
 // comparing the layer stage by stage against another implementation; a verify call with no probe bound does no extra
-// work.
+// work. Last, as bf16 [T][H], the residual stream entering the layer (its input). The MTP layer (index num_layers)
+// takes a probe too, filled by q38_mtp_step: its layer input is the fc output.
 size_t probe_width(const q38_handle* h, int layer) {
     return is_linear(h, layer) ? (size_t)h->Hv * h->dk : (size_t)h->Hq * h->hd * 2 + 2 * (size_t)h->Hkv * h->hd;
 }
@@ -154,10 +155,17 @@ size_t probe_tiles_at(const q38_handle* h, int layer) {
     return T * (2 * (size_t)h->H + probe_width(h, layer) + probe_inner(h, layer)) * 2;
 }
 
-size_t probe_bytes(const q38_handle* h, int layer) {
+size_t probe_input_at(const q38_handle* h, int layer) {
     const size_t T32 = ((size_t)h->cfg.batch_size * h->cfg.verify_tokens + 31) / 32 * 32;
     return probe_tiles_at(h, layer) + T32 * (probe_mid(h, layer) + h->H + h->I);
 }
+
+size_t probe_bytes(const q38_handle* h, int layer) {
+    return probe_input_at(h, layer) + (size_t)h->cfg.batch_size * h->cfg.verify_tokens * h->H * 2;
+}
+
+// Layers that take a probe: the decoder layers and, when present, the MTP layer.
+bool probed_layer(const q38_handle* h, int layer) { return layer < h->cfg.num_layers || (h->cfg.mtp && layer == h->cfg.num_layers); }
 
 uint16_t* probe_of(q38_handle* h, int layer) {
     auto it = h->layer[layer].find("probe");
@@ -186,7 +194,7 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
     if (layer < 0 || layer > h->cfg.num_layers) return 0;
     if (layer == h->cfg.num_layers && !h->cfg.mtp) return 0;
     if (name == "input_layernorm" || name == "post_attention_layernorm") return H * 2;
-    if (name == "probe" && layer < h->cfg.num_layers) return probe_bytes(h, layer);
+    if (name == "probe") return probe_bytes(h, layer);
     if ((r = fp8("mlp.gate_up", 2 * I, H))) return r;
     if ((r = fp8("mlp.down", H, I))) return r;
     if (is_linear(h, layer)) {
@@ -316,11 +324,13 @@ struct TokensScope {
 int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream_t stream) {
     bool ok = true;
     const int H = h->H;
-    uint16_t* probe = li < h->cfg.num_layers ? probe_of(h, li) : nullptr;
+    uint16_t* probe = probed_layer(h, li) ? probe_of(h, li) : nullptr;
     uint8_t* act_h = h->ws(h->off_act_h);
     uint8_t* act_mid = h->ws(h->off_act_mid);
     uint16_t* x = (uint16_t*)h->ws(h->off_x);
     int splits, kmid;
+    if (probe && !io.decode && !io.slot)
+        HIP_TRY(hipMemcpyAsync((uint8_t*)probe + probe_input_at(h, li), x, (size_t)h->T * H * 2, hipMemcpyDeviceToDevice, stream));
     const uint8_t* otiles;
     const uint8_t* oscales;
     if (is_linear(h, li)) {
@@ -548,7 +558,7 @@ int run_mlp(q38_handle* h, int li, int next, uint16_t* final_out, bool mtp_tail,
     if (timed) HIP_TRY(hipEventRecord(timed[0], stream));
     if (gemm(h, li, gu_t, gu_s, act_h, H, 2 * I, EPI_SWIGLU, act_ffn, 0, 0, nullptr, 0, stream)) return 1;
     if (timed) HIP_TRY(hipEventRecord(timed[1], stream));
-    uint8_t* probe = li < h->cfg.num_layers && h->T == h->cfg.batch_size * h->cfg.verify_tokens ? (uint8_t*)probe_of(h, li) : nullptr;
+    uint8_t* probe = probed_layer(h, li) && h->T == h->cfg.batch_size * h->cfg.verify_tokens ? (uint8_t*)probe_of(h, li) : nullptr;
     if (probe) {
         const size_t t32 = (size_t)(h->T + 31) / 32 * 32, at = probe_tiles_at(h, li) + t32 * probe_mid(h, li);
         HIP_TRY(hipMemcpyAsync(probe + at, act_h, t32 * H, hipMemcpyDeviceToDevice, stream));
@@ -1196,6 +1206,25 @@ int q38_spec_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* mat
         if (q38_mtp_step(h, states, embeds, cos, sin, at, active, out, stream_)) return 1;
         HIP_TRY(q38_select_rows(out, nullptr, B, K, H, current, stream));
     }
+    return q38_verify_step(h, position, index, match, accepted, active, hidden, picks, drafts, stream_);
+}
+
+int q38_verify_step(q38_handle* h, int32_t* position, int32_t* index, int32_t* match, int32_t* accepted, const float* active,
+                    uint16_t* hidden, int32_t* picks, const int32_t* drafts, void* stream_) {
+    if (!h || !position || !index || !match || !accepted || !active || !hidden || !picks || !drafts)
+        return fail("null argument");
+    if (h->K < 2) return fail("the verify step needs at least 2 verify tokens");
+    hipStream_t stream = (hipStream_t)stream_;
+    bool ok = true;
+    get<uint8_t>(h, "workspace", -1, &ok);
+    auto rope = get<uint16_t>(h, "rope_table", -1, &ok);
+    if (!ok) return 1;
+    const int B = h->B, K = h->K, S = h->S;
+    uint16_t* embeds = (uint16_t*)h->ws(h->off_sp_embeds);
+    uint16_t* cos = (uint16_t*)h->ws(h->off_sp_cos);
+    uint16_t* sin = (uint16_t*)h->ws(h->off_sp_sin);
+    int32_t* ids = (int32_t*)h->ws(h->off_sp_ids);
+    int* status = (int*)h->ws(h->off_status);
     // Verify (scheduler.py:276-301): [last emitted token, drafts] per row, the head over all B*K rows, acceptance.
     HIP_TRY(q38_verify_tokens(picks, match, drafts, B, K, ids, stream));
     if (q38_embed(h, ids, B * K, embeds, stream_)) return 1;

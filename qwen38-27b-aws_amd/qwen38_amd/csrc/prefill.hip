@@ -441,7 +441,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int r = drow(i, lane);
-                mx = (r >= rlo) & (r < rhi) ? fmaxf(mx, rbf(acc[i])) : mx;
+                mx = ((r >= rlo) & (r < rhi)) ? fmaxf(mx, rbf(acc[i])) : mx;
             }
         }
         ring_release();
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const PrefillAttnArgs
                 for (int i = 0; i < 16; ++i) {
                     const int r = drow(i, lane);
                     const float e = expf(rbf(acc[i]) - nb);
-                    w[i] = (r >= rlo) & (r < rhi) ? e : 0.0f;
+                    w[i] = ((r >= rlo) & (r < rhi)) ? e : 0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) wsum += w[i];

@@ -18,7 +18,7 @@ MAX_LAYERS = 128
 
 EXPORTS = (
     "q38_last_error", "q38_create", "q38_destroy", "q38_buffer_size", "q38_bind", "q38_parity", "q38_set_parity",
-    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp4_linear", "q38_fp4_linear_scratch", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph", "q38_step_status",
+    "q38_pack_weight", "q38_pack_weight_fp4", "q38_mxfp4_linear", "q38_fp4_linear", "q38_fp4_linear_scratch", "q38_fp8_linear", "q38_fp8_linear_scratch", "q38_fp8_linear_f32", "q38_fp8_linear_mfma", "q38_fp8_linear_noalloc", "q38_mlp_up", "q38_tiles_size", "q38_verify", "q38_decode", "q38_copy_states", "q38_prefill", "q38_mtp_prefill", "q38_mtp_step", "q38_head_groupmax", "q38_head_pick", "q38_embed", "q38_accept", "q38_spec_step", "q38_spec_step_graph", "q38_verify_step", "q38_step_status",
     "q38_kernel_timer",
 )
 
@@ -89,6 +89,7 @@ def library() -> ctypes.CDLL:
     lib.q38_accept.argtypes = [p, p, p, p, p, p, p]
     lib.q38_spec_step.argtypes = [p] * 10
     lib.q38_spec_step_graph.argtypes = [p] * 10
+    lib.q38_verify_step.argtypes = [p] * 10
     lib.q38_step_status.argtypes = [p, ctypes.POINTER(i), i, p]
     for name in EXPORTS:
         if name not in ("q38_last_error", "q38_destroy"):
@@ -210,6 +211,12 @@ class Handle:
         """One speculative step on the device (`q38_spec_step`), or its captured HIP graph (`q38_spec_step_graph`)."""
         fn = self.lib.q38_spec_step_graph if graph else self.lib.q38_spec_step
         check(fn(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)), stream()))
+
+    def verify_step(self, position, index, match, accepted, active, hidden, picks, drafts) -> None:
+        """The verify half of the speculative step for host-made drafts (`q38_verify_step`): the prompt-lookup
+        branch of the reference's `Scheduler._verify_step` (scheduler.py:269-301)."""
+        check(self.lib.q38_verify_step(self.h, *map(ptr, (position, index, match, accepted, active, hidden, picks, drafts)),
+                                       stream()))
 
     def step_status(self, clear: bool = True) -> int:
         """The device's step status word (`q38_step_status`: STATUS_NONFINITE, STATUS_POSITION), then reset."""

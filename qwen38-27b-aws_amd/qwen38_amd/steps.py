@@ -204,14 +204,15 @@ class Engine:
         self._bind_zeros("probe", layer, torch.uint8)
 
     def probe(self, layer: int) -> dict:
-        """The last verify call's intermediates of layer ``layer``, for ``T = B*K`` tokens: ``normed`` [T, H] (gated-delta
-        layers), ``projection`` [T, P] (in_proj_z, or the attention q|gate|k|v projection), ``inner`` [T, Hv*128] (the
-        gated-delta in-step output before its gated norm; empty for attention), ``mixed`` [T, H] (the residual after
-        the mixer), all bf16; and the e5m2 GEMM inputs as bf16 values: ``mid`` (out_proj/o_proj input),
-        ``mlp_in`` [T, H], ``ffn`` [T, I]."""
+        """The last verify call's intermediates of layer ``layer`` (or the last MTP call's, for ``mtp_layer``), for
+        ``T = B*K`` tokens: ``normed`` [T, H] (gated-delta layers), ``projection`` [T, P] (in_proj_z, or the attention
+        q|gate|k|v projection), ``inner`` [T, Hv*128] (the gated-delta in-step output before its gated norm; empty for
+        attention), ``mixed`` [T, H] (the residual after the mixer), all bf16; the e5m2 GEMM inputs as bf16 values:
+        ``mid`` (out_proj/o_proj input), ``mlp_in`` [T, H], ``ffn`` [T, I]; and ``input`` [T, H] bf16, the residual
+        stream entering the layer (for the MTP layer, its fc output)."""
         cfg = self.cfg
         t, hsz = self.batch_size * self.verify_tokens, cfg.hidden_size
-        linear = cfg.layer_types[layer] == LINEAR
+        linear = layer < cfg.num_hidden_layers and cfg.layer_types[layer] == LINEAR
         width = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim * 2 + 2 * cfg.num_key_value_heads * cfg.head_dim
         mid = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim
         inner = cfg.linear_value_dim if linear else 0
@@ -224,6 +225,7 @@ class Engine:
         for name, k in (("mid", mid), ("mlp_in", hsz), ("ffn", cfg.intermediate_size)):
             out[name] = act_tiles_to_rows(flat[at : at + t32 * k], t32, k)[:t]
             at += t32 * k
+        out["input"] = flat[at : at + t * hsz * 2].view(DTYPE).view(t, hsz)
         return out
 
     def kv_cache(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -448,4 +450,65 @@ class HeadGraph:
         out = torch.empty(len(ids), e.cfg.hidden_size, dtype=DTYPE, device=e.device)
         if len(ids):
             e.handle.embed(ids.to(e.device), len(ids), out)
+        return out
+
+
+class LookupStep:
+    """Speculative verify steps with prompt-lookup drafts: the reference's `Scheduler._verify_step` without an MTP
+    drafter (scheduler.py:269-301) for the engine's B slots. Each slot's `drafting.Drafter` runs on the host over the
+    row's tokens; the step itself (embedding of ``[last token] + drafts``, the K-token verify with the accepted-prefix
+    commit, the head's picks over every row's K tokens, acceptance, position advance) is one `q38_verify_step` call
+    on the device. The picks and matches come back to the host once per step, as the drafter needs them.
+
+    ``rows[b]`` is slot b's token ids so far (prompt and the tokens chosen after it), or None for an empty slot;
+    ``written[b]`` how many of them are in the slot's cache and states (after a prefill: the prompt length)."""
+
+    def __init__(self, engine: Engine, rows: Sequence[Sequence[int] | None], written: Sequence[int]):
+        from .drafting import Drafter
+
+        e = self.engine = engine
+        b, k = e.batch_size, e.verify_tokens
+        if len(rows) != b or len(written) != b:
+            raise ValueError(f"LookupStep needs one row and one written count per slot ({b})")
+        if k < 2:
+            raise ValueError("speculative steps need at least 2 verify tokens")
+        dev = e.device
+        self.drafters = [Drafter(ids) if ids is not None else None for ids in rows]
+        picks = torch.zeros(b, k, dtype=torch.int32)
+        for slot, ids in enumerate(rows):
+            if ids is not None:
+                picks[slot, 0] = ids[-1]
+        self.position = torch.tensor(list(written), dtype=torch.int32, device=dev)
+        self.index = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.match = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.accepted = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.active = torch.tensor([float(ids is not None) for ids in rows], device=dev)
+        self.hidden = torch.zeros(b, k, e.cfg.hidden_size, dtype=DTYPE, device=dev)
+        self.picks = picks.to(dev)
+        self.drafts = torch.zeros(b, k - 1, dtype=torch.int32, device=dev)
+
+    def __call__(self) -> list[list[int] | None]:
+        """One step for every running slot; returns each slot's new tokens (the drafts the model chose too, then its
+        own next pick), or None for an empty slot."""
+        from .drafting import padded_draft
+
+        e = self.engine
+        k = e.verify_tokens
+        host = torch.zeros(e.batch_size, k - 1, dtype=torch.int32)
+        for slot, drafter in enumerate(self.drafters):
+            if drafter is not None:
+                host[slot] = torch.tensor(padded_draft(drafter, drafter.tokens[-1], k - 1), dtype=torch.int32)
+        self.drafts.copy_(host)
+        e.handle.verify_step(self.position, self.index, self.match, self.accepted, self.active, self.hidden, self.picks,
+                             self.drafts)
+        picks, match = self.picks.cpu(), self.match.cpu()
+        e.handle.raise_step_errors()
+        out: list[list[int] | None] = []
+        for slot, drafter in enumerate(self.drafters):
+            if drafter is None:
+                out.append(None)
+                continue
+            tokens = picks[slot, : int(match[slot]) + 1].tolist()
+            drafter.extend(tokens)
+            out.append(tokens)
         return out

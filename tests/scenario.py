@@ -122,3 +122,26 @@ def row_rel(got: torch.Tensor, want: torch.Tensor) -> float:
         if n > 0:
             worst = max(worst, float((got[r] - want[r]).norm()) / n)
     return worst
+
+
+# The prompt-lookup scenario (tests/golden/make_golden_lookup.py, tests/test_oracle_spec.py, tests/test_gpu_lookup.py):
+# the speculative scenario's shapes, slots and states with no MTP drafter, so drafts come from each row's own history.
+# Each prompt ends in a run of the two steered tokens, which the steered head mostly picks, so prompt lookup finds
+# drafts that the model's picks match about half the time.
+LOOKUP = dict(SPEC)
+
+
+def lookup_start(cfg, spec=LOOKUP):
+    """The starting rows: prompt ids (a random prefix, then a seeded run of the steered tokens) plus the first new
+    token, per running slot (None for an empty slot)."""
+    g = torch.Generator().manual_seed(8765)
+    rows = []
+    for n in spec["prompt_lens"]:
+        if n is None:
+            rows.append(None)
+            continue
+        tail = (n + 1) // 2
+        prefix = torch.randint(0, cfg.vocab_size, (n + 1 - tail,), generator=g).tolist()
+        run = [STEER_TOKENS[int(c)] for c in torch.randint(0, 2, (tail,), generator=g)]
+        rows.append({"ids": prefix + run, "prompt_len": n})
+    return rows

@@ -85,6 +85,98 @@ def test_oracle_speculative_steps_match_the_references_scheduler_bit_for_bit():
         assert _digest(mtp_kv[key]) == meta["state_sha256"][f"mtp.layer.self_attn.{key}"], key
 
 
+def test_oracle_lookup_steps_match_the_references_scheduler_bit_for_bit():
+    """The prompt-lookup branch of `Scheduler._verify_step` (scheduler.py:276-282, no MTP drafter): five steps of the
+    restated scheduler over the oracle equal the reference's own (tests/golden/lookup_tiny.*, every accepted count 1..4
+    among them): positions, committed counts, padded drafts, picks, matches, verify hidden states, final state digests."""
+    from safetensors.torch import load_file
+
+    from scenario import LOOKUP, lookup_start
+
+    cfg = tiny_config(1)
+    meta = json.loads((GOLDEN / "lookup_tiny.json").read_text())
+    gold = load_file(GOLDEN / "lookup_tiny.safetensors")
+    assert {k: meta[k] for k in LOOKUP} == LOOKUP
+    b, k, s = LOOKUP["batch"], LOOKUP["tokens"], LOOKUP["max_seq_len"]
+    values = steer_head(dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg), LOOKUP["seed"])), cfg, LOOKUP["seed"])
+    states, mtp_kv = spec_states(cfg, LOOKUP)
+    step, _, head = build_oracle(cfg, values, states, mtp_kv, b, k)
+    sched = osch.Scheduler(None, None, head, cfg, b, s, LOOKUP["chunk"], verify=step, verify_tokens=k)
+    slots = []
+    for slot, row in enumerate(lookup_start(cfg)):
+        slots.append(None if row is None else osch.Row(0, list(row["ids"]), row["prompt_len"], written=row["prompt_len"]))
+        if row is not None:
+            assert gold[f"start.ids.{slot}"].tolist() == row["ids"]
+    counts = set()
+    with torch.no_grad():
+        for n in range(LOOKUP["steps"]):
+            positions = [row.written if row else 0 for row in slots]
+            active = [row is not None for row in slots]
+            ready = [slot for slot, row in enumerate(slots) if row]
+            assert positions == gold[f"step{n}.positions"].tolist()
+            assert [sched.accepted[i] if slots[i] else 0 for i in range(b)] == gold[f"step{n}.accepted_in"].tolist()
+            emitted = sched.verify_step(slots, positions, active, ready)
+            for slot, tokens in zip(ready, emitted):
+                assert sched.last["drafts"][slot] == gold[f"step{n}.drafts"][slot].tolist(), (n, slot)
+                assert sched.last["picks"][slot] == gold[f"step{n}.picks"][slot].tolist(), (n, slot)
+                assert sched.last["match"][slot] == int(gold[f"step{n}.match"][slot]), (n, slot)
+                counts.add(len(tokens))
+                slots[slot].ids += tokens
+                slots[slot].written += len(tokens)
+            assert torch.equal(sched.last["hidden"], gold[f"step{n}.hidden"]), n
+    assert counts == {1, 2, 3, 4} == set(meta["accepted_counts"])
+    for i, st in enumerate(states):
+        for key, value in st.items():
+            assert _digest(value) == meta["state_sha256"][f"layers.{i}.{'linear_attn' if 'k_cache' not in st else 'self_attn'}.{key}"], (i, key)
+
+
+def test_the_drafter_drafts_what_a_scan_of_the_history_drafts():
+    """The reference's own check of its `Drafter` (tests/test_scheduler.py:177-185), on this build's
+    `drafting.Drafter` against the oracle's restated scan and the build's own `lookup_draft`, over histories of 3 and 6
+    symbols, with max_match 4 and 2; plus closed cases: nothing to match, a draft running into the history's end, the
+    longest match winning over a later shorter one, and `padded_draft`'s padding."""
+    from qwen38_amd import drafting
+
+    for seed, symbols, max_match in ((0, 6, 4), (1, 3, 4), (2, 6, 2)):
+        rng = torch.Generator().manual_seed(seed)
+        history = torch.randint(0, symbols, (400,), generator=rng).tolist()
+        drafter = drafting.Drafter(history[:50], max_match=max_match)
+        for end in range(50, 400):
+            want = osch.lookup_draft(history[:end], 3, max_match=max_match)
+            assert drafter.draft(3) == want == drafting.lookup_draft(history[:end], 3, max_match=max_match), (seed, end)
+            drafter.extend([history[end]])
+    assert drafting.Drafter([1, 2, 3]).draft(3) == [] == osch.lookup_draft([1, 2, 3], 3)
+    assert drafting.Drafter([5, 6, 7, 5]).draft(3) == [6, 7, 5]
+    assert drafting.Drafter([5, 6, 5]).draft(3) == [6, 5]  # runs into the end of the history
+    # [1, 2] occurred followed by 9; the later [2] alone was followed by 8: the longer match wins.
+    assert drafting.Drafter([1, 2, 9, 2, 8, 1, 2]).draft(2) == [9, 2]
+    assert drafting.padded_draft(drafting.Drafter([4, 4]), 4, 3) == [4, 4, 4]
+    assert drafting.padded_draft(drafting.Drafter([1, 2, 3]), 3, 3) == [3, 3, 3]
+
+
+def test_accepted_per_step_counts_what_each_lookup_step_emits():
+    """`drafting.accepted_per_step` (reference drafting.py:54-74) against the restated verify loop driven by a fake
+    model that emits ``output``: the same per-step counts, and they sum to the output's length."""
+    from qwen38_amd import drafting
+
+    rng = torch.Generator().manual_seed(5)
+    for trial in range(20):
+        history = torch.randint(0, 4, (30,), generator=rng).tolist()
+        output = torch.randint(0, 4, (25,), generator=rng).tolist()
+        steps, seen, done = [], list(history), 0
+        while done < len(output):
+            draft = osch.lookup_draft(seen, 3)
+            match = 0
+            while match < len(draft) and done + match < len(output) and draft[match] == output[done + match]:
+                match += 1
+            take = min(match + 1, len(output) - done)
+            steps.append(take)
+            seen += output[done : done + take]
+            done += take
+        got = drafting.accepted_per_step(history, output, 3)
+        assert got == steps and sum(got) == len(output), trial
+
+
 def test_input_builders_keep_the_references_bounds():
     cfg = tiny_config(1)
     with pytest.raises(ValueError):
@@ -160,6 +252,27 @@ def invariant_runs():
     finally:
         om.ROUND_E5M2 = old
     return cfg, values, runs
+
+
+def test_speculation_with_lookup_drafts_gives_the_tokens_plain_greedy_decoding_gives(invariant_runs):
+    """The reference's invariant (tests/test_prefill.py:267-289) for the prompt-lookup branch: speculation with
+    drafts from each row's history (K = 4, no MTP drafter) emits exactly plain greedy decoding's tokens, some drafts
+    match, and it never takes more steps."""
+    cfg, values, runs = invariant_runs
+    old = om.ROUND_E5M2
+    om.ROUND_E5M2 = False
+    try:
+        with torch.no_grad():
+            step, _, head, _ = float32_model(cfg, values, 2, 4)
+            sched = osch.Scheduler(step, step, head, cfg, 2, INV_MAX_SEQ_LEN, INV_CHUNK, (), torch.float32, verify=step,
+                                   verify_tokens=4)
+            out = [[] for _ in INV_PROMPTS]
+            for index, token in sched.run(INV_PROMPTS, 12):
+                out[index].append(token)
+    finally:
+        om.ROUND_E5M2 = old
+    assert out == runs[1][0]
+    assert sched.drafted_tokens > 0 and sched.decode_calls <= runs[1][1]
 
 
 def test_speculation_with_mtp_drafts_gives_the_tokens_plain_greedy_decoding_gives(invariant_runs):
