@@ -114,7 +114,9 @@ void q38_destroy(q38_handle* h);
  *   the e5m2 activation tiles of the out_proj/o_proj input, the MLP input and the down projection's input, for the
  *   first B*K tokens rounded up to 32; last, bf16 [B*K][H], the residual stream entering the layer. For
  *   stage-by-stage comparison with another implementation; unbound, nothing is copied. The MTP layer (index
- *   num_layers) takes one too, filled by q38_mtp_step (its layer input is the fc output). */
+ *   num_layers) takes one too, filled by q38_mtp_step (its layer input is the fc output).
+ * Optional, model-wide: head.probe, which q38_head_groupmax (and q38_head_pick) fills when bound: the head's normed
+ *   rows as bf16 activation tiles (the e5m2 tiles' element order, two bytes each) of whole 32-row blocks. */
 int q38_buffer_size(q38_handle* h, const char* name, int layer, size_t* nbytes);
 int q38_bind(q38_handle* h, const char* name, int layer, void* dev_ptr, size_t nbytes);
 

@@ -114,11 +114,29 @@ def e4m3_to_float(coded: torch.Tensor) -> torch.Tensor:
 
 
 class FP8Weight:
-    """One projection's weight: e4m3 bytes ``[out, in]`` and E8M0 bytes ``[out, in/32]``."""
+    """One projection's weight: e4m3 bytes ``[out, in]`` and E8M0 bytes ``[out, in/32]``. ``dense_t`` may be given
+    when the caller already holds the exact float32 values ``[in, out]`` (tests dequantize large weights on the GPU,
+    where the same exact arithmetic is faster, and spot-check them against `dense_t`'s own decoding)."""
 
-    def __init__(self, coded: torch.Tensor, scales: torch.Tensor):
+    def __init__(self, coded: torch.Tensor, scales: torch.Tensor, dense_t: torch.Tensor | None = None):
         self.coded, self.scales = coded, scales
-        self._dense_t = None
+        self._dense_t = dense_t
+        self._cast: dict = {}
+
+    def decoded_t(self, rows: slice) -> torch.Tensor:
+        """float32 ``[in, rows]`` of the given output rows, decoded from the bytes (never from a given ``dense_t``)."""
+        coded, scales = self.coded[rows], self.scales[rows]
+        n, k = coded.shape
+        values = e4m3_to_float(coded).reshape(n, k // 32, 32)
+        return (values * torch.pow(2.0, scales.float() - 127.0).unsqueeze(-1)).reshape(n, k).T
+
+    def dense_t_as(self, dtype: torch.dtype) -> torch.Tensor:
+        """`dense_t` converted to ``dtype`` (exact for bf16 and wider), kept for later calls."""
+        if dtype == torch.float32:
+            return self.dense_t()
+        if dtype not in self._cast:
+            self._cast[dtype] = self.dense_t().to(dtype)
+        return self._cast[dtype]
 
     def dense_t(self) -> torch.Tensor:
         """float32 ``[in, out]``, contiguous, the layout the reference's weights have (``weight_fp8`` is
@@ -139,7 +157,7 @@ class FP8Weight:
 def linear_fp8(x: torch.Tensor, weight: FP8Weight) -> torch.Tensor:
     """`FP8Linear.forward` on CPU (model.py:221-225): e5m2 input, weights in x's dtype, x's dtype out."""
     x = fp8_round(x)
-    return F.linear(x, weight.dense_t().T.to(x.dtype))
+    return F.linear(x, weight.dense_t_as(x.dtype).T)
 
 
 # E2M1 magnitudes of nibble codes 0-7 (codes 8-15 are their negatives), fp4.py:31.
@@ -226,7 +244,8 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted, force=None
     ``committed`` (the committed state
     ``[B, Hv, d, d]``), ``log_decay`` (``[B, K, Hv]``) or ``delta`` (``[B, K, Hv, d]``), used in place of this function's
     own values from that point on. ``trace``, a dict, receives the in-step quantities (``query``, ``key``, ``value``,
-    ``cumulative`` ``[B, K, Hv]``, ``query_state`` = q·S', ``key_state`` = k·S', ``beta``, ``delta``, ``out``).
+    ``cumulative`` ``[B, K, Hv]``, ``query_state`` = q·S', ``key_state`` = k·S', ``beta``, ``delta``, ``out``) and the
+    in_proj_z output ``z`` ``[B*K, Hv, d]``.
     """
     force = force or {}
     dtype = x.dtype
@@ -299,7 +318,7 @@ def gdn_verify(cfg, w: dict, st: dict, x, position, active, accepted, force=None
     delta, out = torch.stack(deltas, dim=1), torch.stack(outs, dim=1)
     if trace is not None:
         trace.update(query=query, key=key, value=value, cumulative=torch.stack(cumulative, dim=1), query_state=query_state,
-                     key_state=key_state, beta=beta, delta=delta, out=out)
+                     key_state=key_state, beta=beta, delta=delta, out=out, z=z)
     # The reference adds the commit kernel's zero output to order these writes after its reads (model.py:449-452);
     # adding 0.0 also turns -0.0 into +0.0, which the stored bits show.
     st["pending_key_state"] = key.float() + 0.0

@@ -186,6 +186,7 @@ size_t expected_size(const q38_handle* h, const std::string& name, int layer) {
         if (name == "head.norm") return H * 2;
         if ((r = fp8("head.lm_head", V, H))) return r;
         if (name == "head.lm_head.rows") return V * H * 2;
+        if (name == "head.probe") return (B * K + 31) / 32 * 32 * H * 2;
         if (name == "embed_tokens") return V * H * 2;
         if (name == "rope_table") return S * 2 * 64 * 2;
         if (name == "workspace") return h->workspace_bytes;
@@ -1126,6 +1127,11 @@ int q38_head_groupmax(q38_handle* h, const uint16_t* hidden, int rows, float* ma
     if (!ok) return 1;
     HIP_TRY(q38_head_norm(hidden, nw, h->cfg.rms_norm_eps, h->H, rows, (bf16_t*)h->ws(h->off_htiles),
                           (float*)h->ws(h->off_x32), stream));
+    // The optional head probe: the normed rows as the GEMM reads them (bf16 activation tiles of whole 32-row blocks).
+    auto hp = h->global.find("head.probe");
+    if (hp != h->global.end())
+        HIP_TRY(hipMemcpyAsync(hp->second.p, h->ws(h->off_htiles), (size_t)(rows + 31) / 32 * 32 * h->H * 2,
+                               hipMemcpyDeviceToDevice, stream));
     GemmArgs a{};
     a.w = wt;
     a.ws = wsc;

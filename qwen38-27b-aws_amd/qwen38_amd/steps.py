@@ -74,7 +74,8 @@ class Engine:
         if mtp:
             self._bind_zeros("self_attn.k_cache", self.mtp_layer, kv_dtype)
             self._bind_zeros("self_attn.v_cache", self.mtp_layer, kv_dtype)
-            # cos/sin of every position, which the on-device speculative step gathers by the positions it computes.
+        if verify_tokens >= 2:
+            # cos/sin of every position, which the on-device speculative steps gather by the positions they compute.
             from .generate import rope_table
 
             self.bind("rope_table", -1, rope_table(cfg, max_seq_len))
@@ -203,20 +204,21 @@ class Engine:
         (include/q38.h), read back with `probe`."""
         self._bind_zeros("probe", layer, torch.uint8)
 
-    def probe(self, layer: int) -> dict:
+    def probe(self, layer: int, flat: torch.Tensor | None = None) -> dict:
         """The last verify call's intermediates of layer ``layer`` (or the last MTP call's, for ``mtp_layer``), for
         ``T = B*K`` tokens: ``normed`` [T, H] (gated-delta layers), ``projection`` [T, P] (in_proj_z, or the attention
         q|gate|k|v projection), ``inner`` [T, Hv*128] (the gated-delta in-step output before its gated norm; empty for
         attention), ``mixed`` [T, H] (the residual after the mixer), all bf16; the e5m2 GEMM inputs as bf16 values:
         ``mid`` (out_proj/o_proj input), ``mlp_in`` [T, H], ``ffn`` [T, I]; and ``input`` [T, H] bf16, the residual
-        stream entering the layer (for the MTP layer, its fc output)."""
+        stream entering the layer (for the MTP layer, its fc output). ``flat`` parses a saved copy of the probe buffer
+        instead of the bound one."""
         cfg = self.cfg
         t, hsz = self.batch_size * self.verify_tokens, cfg.hidden_size
         linear = layer < cfg.num_hidden_layers and cfg.layer_types[layer] == LINEAR
         width = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim * 2 + 2 * cfg.num_key_value_heads * cfg.head_dim
         mid = cfg.linear_value_dim if linear else cfg.num_attention_heads * cfg.head_dim
         inner = cfg.linear_value_dim if linear else 0
-        flat = self.buffer("probe", layer)
+        flat = self.buffer("probe", layer) if flat is None else flat
         bf = flat[: t * (2 * hsz + width + inner) * 2].view(DTYPE)
         out = {"normed": bf[: t * hsz].view(t, hsz), "projection": bf[t * hsz : t * (hsz + width)].view(t, width),
                "inner": bf[t * (hsz + width) : t * (hsz + width + inner)].view(t, inner),
@@ -227,6 +229,18 @@ class Engine:
             at += t32 * k
         out["input"] = flat[at : at + t * hsz * 2].view(DTYPE).view(t, hsz)
         return out
+
+    def enable_head_probe(self) -> None:
+        """Bind the head's optional probe: later head calls copy their normed rows into it, read back with
+        `head_probe`."""
+        self._bind_zeros("head.probe", -1, DTYPE)
+
+    def head_probe(self, rows: int) -> torch.Tensor:
+        """The last head call's normed rows ``[rows, H]`` bf16 (the final norm's output the group-max GEMM reads)."""
+        h = self.cfg.hidden_size
+        t32 = (rows + 31) // 32 * 32
+        tiles = self.buffer("head.probe", -1)[: t32 * h]
+        return tiles[tile_offsets(t32, h, tiles.device)].reshape(t32, h)[:rows]
 
     def kv_cache(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
         """(k_cache [B,Hkv,S,hd], v_cache stored transposed [B,Hkv,S/32,hd,32])."""
@@ -265,16 +279,20 @@ class Engine:
             mine[key].copy_(value)
 
 
-def act_tiles_to_rows(tiles: torch.Tensor, tokens: int, k: int) -> torch.Tensor:
-    """e5m2 activation tiles (the GEMMs' input layout: tiles of 32 tokens x 64 inputs, token-block major; inside a
-    tile ``[m][lane][8]`` with lane = t % 32 + 32 * ((k % 32) // 16) and byte e = 16 * ((k % 64) // 32) + k % 16,
-    m = e // 8) as bf16 values ``[tokens, k]``."""
-    t = torch.arange(tokens, device=tiles.device).unsqueeze(1)
-    c = torch.arange(k, device=tiles.device).unsqueeze(0)
+def tile_offsets(tokens: int, k: int, device) -> torch.Tensor:
+    """Element index of each (token, input) in the GEMMs' activation tile layout (tiles of 32 tokens x 64 inputs,
+    token-block major; inside a tile ``[m][lane][8]`` with lane = t % 32 + 32 * ((k % 32) // 16) and element
+    e = 16 * ((k % 64) // 32) + k % 16, m = e // 8), flat over ``[tokens, k]``."""
+    t = torch.arange(tokens, device=device).unsqueeze(1)
+    c = torch.arange(k, device=device).unsqueeze(0)
     e = ((c % 64) // 32) * 16 + (c % 16)
     lane = t % 32 + 32 * ((c % 32) // 16)
-    offset = ((t // 32) * (k // 64) + c // 64) * 2048 + (e // 8) * 512 + lane * 8 + e % 8
-    return tiles[offset.reshape(-1)].view(torch.float8_e5m2).to(DTYPE).reshape(tokens, k)
+    return (((t // 32) * (k // 64) + c // 64) * 2048 + (e // 8) * 512 + lane * 8 + e % 8).reshape(-1)
+
+
+def act_tiles_to_rows(tiles: torch.Tensor, tokens: int, k: int) -> torch.Tensor:
+    """e5m2 activation tiles (`tile_offsets`' layout, one byte per element) as bf16 values ``[tokens, k]``."""
+    return tiles[tile_offsets(tokens, k, tiles.device)].view(torch.float8_e5m2).to(DTYPE).reshape(tokens, k)
 
 
 def _dev(t: torch.Tensor, dtype: torch.dtype, device) -> torch.Tensor:

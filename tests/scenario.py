@@ -69,7 +69,7 @@ def steer_head(values: dict, cfg, seed: int) -> dict:
     u = torch.randn(cfg.hidden_size, generator=g)
     u = u / u.norm()
     coded, scales = (t.clone() for t in values["head.lm_head"])
-    rc, rs = quantize_e4m3(torch.stack((STEER_SCALE * u, -STEER_SCALE * u)))
+    rc, rs = (t.to(coded.device) for t in quantize_e4m3(torch.stack((STEER_SCALE * u, -STEER_SCALE * u))))
     for i, token in enumerate(STEER_TOKENS):
         coded[token], scales[token] = rc[i], rs[i]
     out = dict(values)
