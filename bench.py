@@ -9,7 +9,7 @@ as a HIP graph and replayed), on torch's current HIP stream; `ms_per_step_launch
 launches (`q38_spec_step`). Inputs and state are resident in HBM. Weights are seeded random-init FP8 e4m3 (+E8M0 per 32) of the Qwen3.8-27B shapes; there is no
 checkpoint.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill] [--mxfp4] [--kv-fp8]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--decode | --prefill | --config 3|4] [--mxfp4] [--kv-fp8]
 
 prints one JSON line. `value` is accepted tokens per second (the sum of every row's accepted count, which advances
 its position, over the timed steps). `roofline` is the dominant kernel, the MLP gate/up projection (gemm_kernel with
@@ -31,6 +31,11 @@ two chunks of 2048 (the second one attending to the first's 2048 cached position
 prefill of each chunk: `value` is prompt tokens per second, `roofline` the projections' bf16 MFMA work (2 x tokens x
 every projection weight; attention's own products left out) over the time against the dense bf16 peak, and `cpu_baseline` the CPU oracle's prefill of one block
 on a 512-token chunk, x16.
+
+`--config 3` / `--config 4` measure BASELINE configs 3 and 4 at block level (one 27B block of 3 gated-delta + 1
+attention layer, `q38_verify`): B=16, K=4 from 32768 cached positions (HBM-bound: `roofline` in GB/s), or B=256, K=8
+from 4096 (near the MFMA balance: `roofline` in TFLOP/s of the block's matrix work); `value` is verify tokens per
+second through the block, `cpu_baseline` the CPU oracle's verify of the same block.
 
 `--mxfp4` binds the 64 decoder layers' projections as MXFP4 (the checkpoint's E2M1 nibbles + E8M0 scales, read by the
 GEMMs directly: half the weight bytes of e4m3), the seeded e4m3 weights requantized; the MTP layer and the head stay
@@ -479,6 +484,149 @@ def prefill_main(args) -> dict:
     }
 
 
+def block_main(args, index: int) -> dict:
+    """BASELINE config 3 or 4 at block level: verify steps of one 27B block (3 gated-delta + 1 attention layer,
+    `q38_verify`) over B rows of K tokens from a long context, each committing the step before's accepted prefixes.
+    Config 3 (B=16, K=4, 32768 cached positions) is bound by HBM (the KV stream): `roofline` is the block's algorithmic
+    bytes over its time. Config 4 (B=256, K=8, 4096 cached positions) is near the MFMA balance: `roofline` is the
+    block's matrix work (the projections' 2 x T x weights, attention's 4 x T x Hq x context x 256, the gated-delta
+    commit and reads) over its time, against the dense bf16 peak."""
+    import torch
+
+    from qwen38_amd import synth
+    from qwen38_amd.config import verify_configs
+    from qwen38_amd.generate import verify_inputs
+    from qwen38_amd.steps import Engine
+
+    w = verify_configs()[index]
+    cfg, batch, tokens, context, max_seq_len = w.cfg, w.batch, w.tokens, w.context, w.max_seq_len
+    engine = Engine(cfg, batch, tokens, max_seq_len, mtp=False, weight_format="mxfp4" if args.mxfp4 else "e4m3",
+                    kv_cache_format="fp8" if args.kv_fp8 else "bf16")
+    started = time.time()
+    weights = ((spec.name, synth.make(spec, args.seed, "cuda")) for spec in synth.model_specs(cfg, mtp=False, head=False))
+    engine.load(synth.to_mxfp4(weights) if args.mxfp4 else weights)
+    from qwen38_amd.quant import encode_kv
+
+    for i, kind in enumerate(cfg.layer_types):
+        if kind == "linear_attention":
+            engine.set_gdn(i, synth.gdn_states(cfg, batch, tokens, args.seed, f"state.{i}", "cuda"))
+        else:
+            kv = synth.kv_states(cfg, batch, max_seq_len, [context] * batch, args.seed, f"kv.{i}", "cuda")
+            if args.kv_fp8:
+                ks, vs = synth.kv_scales(cfg, args.seed, f"kv.{i}", "cuda")
+                engine.set_kv_scales(i, ks, vs)
+                kv = {"k_cache": encode_kv(kv["k_cache"], ks), "v_cache": encode_kv(kv["v_cache"], vs)}
+            engine.set_kv(i, kv["k_cache"], kv["v_cache"])
+            del kv
+    torch.cuda.synchronize()
+    log(f"config {index} block ready in {time.time() - started:.0f}s")
+    x = (synth.hidden_states((batch, tokens, cfg.hidden_size), args.seed, "bench.block", "cuda").float() * 0.02).to(torch.bfloat16)
+    accepted = [1 + b % tokens for b in range(batch)]  # every accepted count, as corrupted or steered drafts give
+    inputs = {k: v.cuda() for k, v in verify_inputs(cfg, [context] * batch, tokens, max_seq_len, torch.bfloat16,
+                                                     [True] * batch, accepted).items()}
+    out = torch.empty(batch, tokens, cfg.hidden_size, dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        engine.handle.verify(x, inputs["cos"], inputs["sin"], inputs["position"], inputs["active"], inputs["accepted"], out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    assert bool(torch.isfinite(out.float()).all()), "the block's output is not finite"
+    t = batch * tokens
+    alg = algorithmic_bytes(cfg, batch, tokens, context, args.mxfp4, args.kv_fp8)
+    block_bytes = alg["weights"] + alg["state"] + alg["kv"] + alg["io"]
+    h, inter = cfg.hidden_size, cfg.intermediate_size
+    hv, d, c = cfg.linear_num_value_heads, cfg.linear_key_head_dim, cfg.linear_conv_dim
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    n_gdn = sum(1 for k in cfg.layer_types if k == "linear_attention")
+    n_attn = cfg.num_hidden_layers - n_gdn
+    gemm = n_gdn * ((c + hv * d) * h + h * hv * d + 3 * inter * h) + n_attn * ((hq * hd * 2 + 2 * hkv * hd) * h + h * hq * hd + 3 * inter * h)
+    flops = 2.0 * t * gemm + n_attn * 4.0 * t * hq * context * hd + n_gdn * 2.0 * batch * hv * d * d * 3 * tokens
+    log(f"config {index}: {ms:.3f} ms per block step ({t} tokens)")
+    if index == 3:
+        gbs = block_bytes / (ms / 1000.0) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes_per_step": block_bytes}
+    else:
+        tf = flops / (ms / 1000.0) / 1e12
+        roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops_per_step": flops}
+    return {
+        "metric": f"verify tokens/s/GPU through one 27B block (3 gated-delta + 1 attention layer), batch {batch}, "
+                  f"{tokens} tokens, context {context}",
+        "value": round(t / (ms / 1000.0), 1),
+        "unit": "verify tokens/s per block",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": weight_dtype(args),
+        "data": "synthetic: seeded random-init weights of the 27B shapes, unit-RMS states and KV",
+        "config": {"workload": f"{w.name} (BASELINE config {index})" + variant(args), "global_batch": batch,
+                   "tokens_per_row": tokens, "context": context, "parallelism": "none (one GPU)"},
+        "roofline": roof,
+        "block_hbm": {"algorithmic_bytes_per_step": block_bytes, "achieved": round(block_bytes / (ms / 1000.0) / 1e9, 1),
+                      "unit": "GB/s"},
+        "block_flops_per_step": flops,
+        "_engine": engine,
+        "_shape": (cfg, batch, tokens, max_seq_len, context),
+    }
+
+
+def cpu_block_baseline(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int) -> dict:
+    """The CPU oracle's verify step of the same block (bf16, all host threads), timed once after one warm-up."""
+    import torch
+
+    from oracle import model as om
+    from qwen38_amd import synth
+    from qwen38_amd.generate import verify_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    layers = []
+    for i in range(cfg.num_hidden_layers):
+        prefix = f"layers.{i}."
+        w = {}
+        for spec in synth.layer_specs(cfg, i):
+            v = synth.make(spec, seed, "cuda")
+            w[spec.name[len(prefix):]] = om.FP8Weight(*(x.cpu() for x in v)) if isinstance(v, tuple) else v.cpu()
+        layers.append(w)
+    states = []
+    for i, kind in enumerate(cfg.layer_types):
+        if kind == "linear_attention":
+            states.append({k: v.cpu() for k, v in synth.gdn_states(cfg, batch, tokens, seed, f"cpu.{i}", "cuda").items()})
+        else:
+            states.append({k: v.cpu() for k, v in synth.kv_states(cfg, batch, max_seq_len, [context] * batch, seed, f"cpu.{i}", "cuda").items()})
+    x = (synth.hidden_states((batch, tokens, cfg.hidden_size), seed, "cpu.block.x").float() * 0.02).to(torch.bfloat16)
+    inp = verify_inputs(cfg, [context] * batch, tokens, max_seq_len, torch.bfloat16, [True] * batch,
+                        [1 + b % tokens for b in range(batch)])
+    times = []
+    for _ in range(2):
+        started = time.perf_counter()
+        om.step_verify(cfg, layers, states, x, inp["cos"], inp["sin"], inp["position"], inp["active"], inp["accepted"])
+        times.append(time.perf_counter() - started)
+        log(f"cpu block {times[-1]:.2f}s")
+    return {
+        "value": batch * tokens / times[-1],
+        "unit": "verify tokens/s per block",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"the same block's verify step (B={batch}, K={tokens}, context {context}) on the CPU oracle in bf16, "
+        f"{times[-1]:.2f} s after one warm-up",
+    }
+
+
 def weight_dtype(args) -> str:
     kv = ", fp8 e4m3 KV cache" if args.kv_fp8 else ""
     if args.mxfp4:
@@ -504,6 +652,8 @@ def main() -> int:
     ap.add_argument("--context", type=int, default=512,
                     help="cached positions per row before the timed steps (BASELINE's configs use 512)")
     ap.add_argument("--kv-fp8", action="store_true", help="KV caches as e4m3 bytes with per-layer scales")
+    ap.add_argument("--config", type=int, choices=(3, 4), default=None,
+                    help="time BASELINE config 3 (long context) or 4 (high batch, 8 tokens) at block level instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -529,6 +679,15 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy probe: {args.copy_probe} MiB read and written by one bitwise_not kernel")
         del src, dst
+    if args.config is not None:
+        result = block_main(args, args.config)
+        engine, shape = result.pop("_engine"), result.pop("_shape")
+        if not args.no_cpu_baseline:
+            del engine
+            torch.cuda.empty_cache()
+            result["cpu_baseline"] = cpu_block_baseline(shape[0], shape[1], shape[2], shape[3], shape[4], seed)
+        print(json.dumps(result), flush=True)
+        return 0
     if args.prefill:
         result = prefill_main(args)
         engine = result.pop("_engine")
@@ -587,6 +746,10 @@ def main() -> int:
         step()
     launches, total_ms = engine.handle.kernel_timer(False)
     kernel_ms = total_ms / max(launches, 1)
+    # Every step above records a non-finite head row or a row past its last usable position in the device's status
+    # word instead of stopping; a run that hit either measures nothing, so it fails here.
+    engine.handle.raise_step_errors()
+    log("step status word clear after every step")
     log(f"gate/up GEMM inside the steps: {launches} launches, {kernel_ms * 1000:.1f} us each")
     flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
     achieved = flops / (kernel_ms / 1000.0) / 1e12

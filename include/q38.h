@@ -167,8 +167,9 @@ int q38_fp4_linear(const uint16_t* x, int rows, int k, const uint8_t* tiles, con
                    uint8_t* scratch, uint16_t* out, void* stream);
 size_t q38_fp4_linear_scratch(int rows, int k);
 /* q38_fp8_linear for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops):
- * the same outputs, with the scratch in the library's own static device array (66.5 MiB, held by each GPU the call
- * runs on until the process ends) instead of an argument. 1 to 64 rows, K <= 32768, n % 256 == 0; other sizes are
+ * the same outputs, with the scratch in the library's own static device array (66.5 MiB in the library's code object:
+ * resident on every GPU where any libq38 kernel is loaded, from then until the process ends, whether or not this entry
+ * point is called) instead of an argument. 1 to 64 rows, K <= 32768, n % 256 == 0; other sizes are
  * refused. Calls share their GPU's array, so calls that overlap on one GPU race. No counterpart in the reference. */
 int q38_fp8_linear_noalloc(const uint16_t* x, int rows, int k, const uint8_t* tiles, const uint8_t* tile_scales, int n,
                            uint16_t* out, void* stream);

@@ -202,3 +202,79 @@ def test_mtp_prefill_writes_the_layers_cache_like_the_oracle(gpu):
         assert row_rel(cache[slot, :, :chunk].transpose(0, 1), mst[name][slot, :, :chunk].transpose(0, 1)) <= 1e-2, name
         assert torch.equal(cache[slot, :, chunk:], before[name][slot, :, chunk:]), name
         assert torch.equal(cache[others], before[name][others]), name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("heads", [8, 16])
+def test_prefill_attention_over_several_tiles_and_blocks(gpu, heads, kv):
+    """One attention layer, one chunk of 288 tokens (270 real) of row 1 from position 1601 of a 1984-position cache:
+    three 128-token tiles (the last one partly live, part of it padding), the chunk's tokens 64 and on in the second
+    2048-position block of [cache, chunk] (the reference's blocked softmax, model.py:760-781), so a block boundary cuts
+    the chunk and some waves of a tile hold no token of a block; 8 and 16 query heads over 2 KV heads (4 and 8 query
+    heads per KV head on an XCD). The real tokens within 2e-2 of the oracle or explained by a rounding tie
+    (`ties.check_tokens`); the written cache positions within 1e-2 (bf16) or at most 1% of the bytes one e4m3 code
+    apart (FP8, the oracle then forced onto the GPU's bytes for the chunk's own keys and values, as
+    tests/test_gpu_kv8.py does); every other position unchanged."""
+    from dataclasses import replace
+
+    from qwen38_amd.quant import encode_kv
+
+    cfg = replace(with_layers(tiny_config(1), ("full_attention",)), num_attention_heads=heads)
+    rows, s, chunk, slot, start, n_valid, seed = 2, 1984, 288, 1, 1601, 270, 41
+    values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg, mtp=False, head=False), seed))
+    layers, _, _ = oracle_weights(values, cfg)
+    w = layers[0]
+    st = synth.kv_states(cfg, rows, s, [700, start], seed, "pf.kv")
+    engine = Engine(cfg, rows, 4, s, mtp=False, prefill_chunk=chunk, kv_cache_format=kv)
+    engine.load(values.items())
+    if kv == "fp8":
+        ks, vs = synth.kv_scales(cfg, seed, "pf.kv")
+        st = {"k_cache": encode_kv(st["k_cache"], ks), "v_cache": encode_kv(st["v_cache"], vs), "k_scale": ks, "v_scale": vs}
+        engine.set_kv_scales(0, ks, vs)
+    engine.set_kv(0, st["k_cache"], st["v_cache"])
+    before = {k: v.clone() for k, v in st.items()}
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, cfg.vocab_size, (chunk,), generator=g)
+    ids[n_valid:] = 0
+    x = synth.hidden_states((1, chunk, cfg.hidden_size), seed, "pf.x")
+    pi = prefill_inputs(cfg, slot, start, n_valid, chunk, torch.bfloat16)
+    got = StepGraph(engine)(inputs_embeds=x, **pi)
+    torch.cuda.synchronize()
+    kc, vc = (t.cpu() for t in engine.get_kv(0))
+    written = slice(start, start + chunk)
+    plain = om.kv_store
+    oracle_bytes = None
+    if kv == "fp8":
+        # The oracle's own bytes for the chunk, from an unforced run on a copy of the cache.
+        unforced = {k: v.clone() for k, v in st.items()}
+        oracle_layer(cfg, w, unforced, x, pi)
+        oracle_bytes = unforced
+        own = (kc[slot, :, written], vc[slot, :, written])
+        calls = []
+
+        def forced(t, scale):
+            calls.append(t)
+            return own[(len(calls) - 1) % 2].reshape(t.shape)
+
+        om.kv_store = forced
+    try:
+        want, o_in = oracle_layer(cfg, w, st, x, pi)
+    finally:
+        om.kv_store = plain
+    check_layer(got, want, w, cfg, x, o_in, n_valid)
+    keep = torch.ones(s, dtype=torch.bool)
+    keep[written] = False
+    for name, cache in (("k_cache", kc), ("v_cache", vc)):
+        if kv == "fp8":
+            want_bytes = oracle_bytes[name][slot, :, written]
+            diff = cache[slot, :, written].int() != want_bytes.int()
+            print(f"  {name}: {int(diff.sum())} of {diff.numel()} written bytes differ", flush=True)
+            assert float(diff.float().mean()) <= 0.01, name
+            assert bool((((cache[slot, :, written].int() - want_bytes.int()).abs() == 1))[diff].all()), name
+        else:
+            err = row_rel(cache[slot, :, written].transpose(0, 1), st[name][slot, :, written].transpose(0, 1))
+            print(f"  {name}: written positions within {err:.3g}", flush=True)
+            assert err <= 1e-2, name
+        assert torch.equal(cache[slot, :, keep], before[name][slot, :, keep]), name
+        assert torch.equal(cache[0], before[name][0]), name

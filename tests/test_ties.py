@@ -72,3 +72,47 @@ def test_generic_errors_and_far_flips_are_not_explained():
     gpu, _ = ties.layer_tail(w, eps, x[t], o_in[t], ("o", big, far))
     assert ties.rel(gpu, base) > ties.TOL  # large enough to need explaining
     assert ties.explain(w, eps, x[t], o_in[t], gpu) is None
+
+
+def test_swiglu_enumeration_finds_planted_ties_and_rejects_other_values():
+    """`layerwise.swiglu_ties` (the down-projection input's exact tie enumeration): with a gate sum planted exactly on a
+    bf16 rounding boundary, the e5m2 input computed from either rounding of it is explained, and so is every value the
+    oracle's own SwiGLU gives; a value an e5m2 step or more from every candidate is not."""
+    from layerwise import swiglu_ties
+
+    g = torch.Generator().manual_seed(3)
+    k = 256
+    x = om.fp8_round(torch.randn(2, k, generator=g).to(torch.bfloat16))
+    wg = quant_pair(torch.randn(4, k, generator=g) * 0.05)
+    wu = quant_pair(torch.randn(4, k, generator=g) * 0.05)
+    gate, up = om.FP8Weight(*wg), om.FP8Weight(*wu)
+    rows, cols = torch.tensor([0, 0, 1, 1]), torch.tensor([0, 1, 2, 3])
+    pre = om.silu(om.linear_fp8(x, gate)) * om.linear_fp8(x, up)
+    own = om.fp8_round(pre).float()[rows, cols]
+    assert bool(swiglu_ties(x, gate, up, rows, cols, own, 8.0).all())
+    # Plant a tie: move one weight so that the gate sum of (0, 0) is a bf16 midpoint (exactly representable).
+    exact = float((x[0].double() * gate.dense()[0].double()).sum())
+    step = 2.0 ** (float(torch.floor(torch.log2(torch.tensor(abs(exact))))) - 7)
+    midpoint = (float(torch.floor(torch.tensor(exact / step))) + 0.5) * step
+    need = midpoint - exact
+    j = int(x[0].abs().argmax())
+    dense = gate.dense().clone()
+    dense[0, j] += need / float(x[0, j])
+    # The moved weight need not be e4m3; the enumeration only reads the dense values.
+    planted = om.FP8Weight(gate.coded, gate.scales, dense.T.contiguous())
+    total = float((x[0].double() * planted.dense()[0].double()).sum())
+    for rounded in (torch.tensor(total - step / 4).to(torch.bfloat16), torch.tensor(total + step / 4).to(torch.bfloat16)):
+        s = torch.sigmoid(rounded.float()).to(torch.bfloat16)
+        act = (rounded.float() * s.float()).to(torch.bfloat16)
+        u = om.linear_fp8(x[:1], up)[0, 0]
+        h = om.fp8_round((act.float() * u.float()).to(torch.bfloat16))
+        assert bool(swiglu_ties(x, planted, up, rows[:1], cols[:1], h.float().reshape(1), 8.0)[0])
+    far = own.clone()
+    far[0] = own[0] * 4 + torch.sign(own[0]) * 0.5
+    assert not bool(swiglu_ties(x, gate, up, rows[:1], cols[:1], far[:1], 8.0)[0])
+
+
+def quant_pair(w):
+    from qwen38_amd.quant import quantize_e4m3
+
+    return quantize_e4m3(w)

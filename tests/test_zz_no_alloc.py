@@ -38,3 +38,32 @@ def test_noalloc_projection_refuses_sizes_beyond_its_array(gpu):
         ext.fp8_linear_noalloc(torch.zeros(65, 1024, dtype=torch.bfloat16, device="cuda"), tiles, words, 256)
     with pytest.raises(RuntimeError, match="K <= 32768"):
         ext.fp8_linear_noalloc(torch.zeros(64, 33024, dtype=torch.bfloat16, device="cuda"), tiles, words, 256)
+
+
+@pytest.mark.gpu
+def test_noalloc_projection_captured_in_a_graph_replays_like_the_scratch_argument_one(gpu):
+    """The callers this entry point is for capture it: two calls of different shapes captured into one
+    torch.cuda.CUDAGraph (no allocation and no memset inside: its counters are cleared by a kernel), replayed twice
+    with eager work between the replays, each replay's outputs equal to q38_fp8_linear's bit for bit."""
+    calls = []
+    for rows, k, n, seed in [(64, 5120, 16384, 4), (9, 1024, 768, 5)]:
+        tiles, words, x = packed(n, k, seed)
+        x = x[:rows].contiguous()
+        calls.append((x, tiles, words, n, torch.empty(rows, n, dtype=torch.bfloat16, device="cuda"),
+                      ext.fp8_linear(x, tiles, words, n)))
+    for x, tiles, words, n, out, _ in calls:  # eager first calls: the array's address is resolved before capture
+        ext.fp8_linear_noalloc(x, tiles, words, n, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for x, tiles, words, n, out, _ in calls:
+            ext.fp8_linear_noalloc(x, tiles, words, n, out=out)
+    for replay in range(2):
+        for call in calls:
+            call[4].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = torch.ones(1024, device="cuda").sum().item()  # eager work between replays
+        for x, tiles, words, n, out, want in calls:
+            assert torch.equal(out.view(torch.int16), want.view(torch.int16)), (replay, x.shape[0], n)
