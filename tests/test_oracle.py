@@ -550,3 +550,37 @@ def _e4m3_half_step(v: torch.Tensor) -> torch.Tensor:
     """Half the spacing of e4m3 values around |v| (subnormal spacing 2^-9)."""
     e = torch.floor(torch.log2(v.abs().clamp_min(2.0**-6)))
     return torch.pow(2.0, e - 3) / 2
+
+
+def test_oracle_matches_the_reference_at_the_27b_widths_bit_for_bit():
+    """tests/golden/slice_27b.*: two verify steps of one gated-delta and one attention layer (each with its MLP) at the
+    27B widths (H 5120; 16 key heads repeated three-fold over 48 value heads; 24 query heads over 4 KV heads, six-fold
+    GQA; SwiGLU 17408), B = 2, from the reference's own CPU path: the hidden states of both steps and every state buffer
+    after the second, bit for bit. Pins the value-head repeat and the GQA grouping at their 27B factors, which the
+    config 0 goldens (two-fold and four-fold) do not."""
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden_27b_slice as gs
+
+    meta = json.loads((GOLDEN / "slice_27b.json").read_text())
+    gold = load_file(GOLDEN / "slice_27b.safetensors")
+    assert {k: meta[k] for k in gs.SLICE} == gs.SLICE
+    cfg = gs.slice_config()
+    assert (cfg.linear_key_repeat, cfg.num_attention_heads // cfg.num_key_value_heads) == (3, 6)
+    values = dict((sp.name, v) for sp, v in synth.make_all(synth.model_specs(cfg, mtp=False, head=False), gs.SLICE["seed"]))
+    layers, _, _ = oracle_weights(values, cfg)
+    states = gs.slice_states(cfg)
+    x = gs.slice_inputs(cfg)
+    b, k, s = gs.SLICE["batch"], gs.SLICE["tokens"], gs.SLICE["max_seq_len"]
+    in1 = verify_inputs(cfg, gs.SLICE["context"], k, s, torch.bfloat16, [True] * b, [0] * b)
+    assert torch.equal(in1["cos"], gold["cos1"]) and torch.equal(in1["sin"], gold["sin1"])
+    h1 = om.step_verify(cfg, layers, states, x[0], in1["cos"], in1["sin"], in1["position"], in1["active"], in1["accepted"])
+    assert torch.equal(h1, gold["hidden1"])
+    in2 = verify_inputs(cfg, meta["positions_2"], k, s, torch.bfloat16, [True] * b, gs.SLICE["accepted_2"])
+    h2 = om.step_verify(cfg, layers, states, x[1], in2["cos"], in2["sin"], in2["position"], in2["active"], in2["accepted"])
+    assert torch.equal(h2, gold["hidden2"])
+    for i, (kind, st) in enumerate(zip(cfg.layer_types, states)):
+        owner = "linear_attn" if kind == "linear_attention" else "self_attn"
+        for key, value in st.items():
+            assert _digest(value) == meta["state_sha256"][f"layers.{i}.{owner}.{key}"], (i, key)
