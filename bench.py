@@ -627,6 +627,61 @@ def cpu_block_baseline(cfg, batch: int, tokens: int, max_seq_len: int, context: 
     }
 
 
+def vendor_gemm_main(args) -> dict:
+    """This build's GEMMs beside the vendor library's at the verify step's shapes: torch's bf16 matmul and FP8
+    `_scaled_mm` (hipBLASLt on ROCm) against `q38_mlp_up` (the gate/up pair with SwiGLU, FP8 e4m3 weights widened to
+    bf16 for the bf16 MFMA) and `q38_fp8_linear` (bf16 output) at 256 tokens, each averaged over 100 back-to-back
+    launches after 10 warm-up ones. A reference point for the MFMA fractions: at 256 tokens neither reaches the dense
+    peak."""
+    import torch
+
+    from qwen38_amd import ext
+    from qwen38_amd.quant import quantize_e4m3
+
+    def timeit(fn, iters=100):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / iters * 1000.0
+
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    rows, rows_out = 256, []
+    for name, k, n in (("gate/up (SwiGLU)", 5120, 2 * 17408), ("qkvz", 5120, 16384), ("o_proj", 6144, 5120), ("down", 17408, 5120)):
+        a = torch.randn(rows, k, generator=g, device="cuda").to(torch.bfloat16)
+        b = torch.randn(n, k, generator=g, device="cuda").to(torch.bfloat16)
+        bf = timeit(lambda: a @ b.T)
+        one = torch.ones((), device="cuda")
+        a8, b8 = a.to(torch.float8_e4m3fn), b.to(torch.float8_e4m3fn)
+        f8 = timeit(lambda: torch._scaled_mm(a8, b8.T, scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
+        flop = 2.0 * rows * k * n
+        entry = {"gemm": name, "tokens": rows, "k": k, "n": n, "hipblaslt_bf16_us": round(bf, 1),
+                 "hipblaslt_fp8_us": round(f8, 1), "hipblaslt_bf16_tflops": round(flop / bf / 1e6, 1)}
+        if name.startswith("gate") or name == "qkvz":
+            coded, scales = quantize_e4m3(b.float() * 0.02)
+            tiles, tscales = ext.pack_weight(coded, scales)
+            scratch = ext.linear_scratch(rows, k)
+            if name.startswith("gate"):
+                out = torch.empty(ext.library().q38_tiles_size(rows, n // 2), dtype=torch.uint8, device="cuda")
+                ext.mlp_up(a, rows, k, tiles, tscales, n // 2, scratch=scratch, out=out)
+                ours = timeit(lambda: ext.mlp_up(None, rows, k, tiles, tscales, n // 2, scratch=scratch, out=out))
+            else:
+                ours = timeit(lambda: ext.fp8_linear(a, tiles, tscales, n, scratch=scratch))
+            entry.update(this_build_us=round(ours, 1), this_build_tflops=round(flop / ours / 1e6, 1))
+        rows_out.append(entry)
+        log(f"{entry}")
+        del a, b, a8, b8
+    return {"metric": "GEMM time at the verify step's shapes, this build against hipBLASLt (torch)", "unit": "us",
+            "n_gpus": 1, "data": "synthetic", "gemms": rows_out,
+            "note": "this build's qkvz time includes the e5m2 activation tiles kernel; its o_proj and down projections run "
+                    "split-K inside the step (see profiles/spec_step_27b_b64_k4_kernel_trace.md), not as standalone calls"}
+
+
 def weight_dtype(args) -> str:
     kv = ", fp8 e4m3 KV cache" if args.kv_fp8 else ""
     if args.mxfp4:
@@ -654,6 +709,8 @@ def main() -> int:
     ap.add_argument("--kv-fp8", action="store_true", help="KV caches as e4m3 bytes with per-layer scales")
     ap.add_argument("--config", type=int, choices=(3, 4), default=None,
                     help="time BASELINE config 3 (long context) or 4 (high batch, 8 tokens) at block level instead")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time the step's GEMM shapes on hipBLASLt (torch bf16 and FP8) beside this build's GEMMs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain elementwise copy (bitwise_not) of MIB MiB, for counter calibration")
     args = ap.parse_args()
@@ -679,6 +736,9 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy probe: {args.copy_probe} MiB read and written by one bitwise_not kernel")
         del src, dst
+    if args.vendor_gemm:
+        print(json.dumps(vendor_gemm_main(args)), flush=True)
+        return 0
     if args.config is not None:
         result = block_main(args, args.config)
         engine, shape = result.pop("_engine"), result.pop("_shape")
