@@ -62,6 +62,7 @@ for _p in (ROOT, ROOT / "qwen38-27b-aws_amd"):
 
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
 
 
 def log(msg: str) -> None:
@@ -111,7 +112,8 @@ def decode_bytes(cfg, batch: int, context: int, mxfp4: bool = False, kv8: bool =
     return b["weights"] + b["state"] + b["kv"] + b["io"]
 
 
-def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, mxfp4: bool = False, kv8: bool = False):
+def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: int, mxfp4: bool = False, kv8: bool = False,
+          mfma: str = "bf16"):
     import torch
 
     from qwen38_amd import synth
@@ -120,7 +122,7 @@ def build(cfg, batch: int, tokens: int, max_seq_len: int, context: int, seed: in
 
     dev = "cuda"
     engine = Engine(cfg, batch, tokens, max_seq_len, mtp=True, device=dev, weight_format="mxfp4" if mxfp4 else "e4m3",
-                    kv_cache_format="fp8" if kv8 else "bf16")
+                    kv_cache_format="fp8" if kv8 else "bf16", projection_mfma=mfma)
 
     def set_kv(layer, name):
         kv = synth.kv_states(cfg, batch, max_seq_len, ctx, seed, name, dev)
@@ -684,9 +686,11 @@ def vendor_gemm_main(args) -> dict:
 
 def weight_dtype(args) -> str:
     kv = ", fp8 e4m3 KV cache" if args.kv_fp8 else ""
+    mfma = (", scaled fp8 MFMA (e4m3 x e5m2) for the projections, bf16 MFMA for the head" if getattr(args, "mfma", "bf16") == "fp8"
+            else ", bf16 MFMA (fp32 accumulate)")
     if args.mxfp4:
-        return "mxfp4 (e2m1 + e8m0) decoder weights, fp8 e4m3 mtp/head weights" + kv + ", bf16 MFMA (fp32 accumulate)"
-    return "fp8 e4m3 weights" + kv + ", bf16 MFMA (fp32 accumulate)"
+        return "mxfp4 (e2m1 + e8m0) decoder weights, fp8 e4m3 mtp/head weights" + kv + mfma
+    return "fp8 e4m3 weights" + kv + mfma
 
 
 def variant(args) -> str:
@@ -709,6 +713,10 @@ def main() -> int:
     ap.add_argument("--kv-fp8", action="store_true", help="KV caches as e4m3 bytes with per-layer scales")
     ap.add_argument("--config", type=int, choices=(3, 4), default=None,
                     help="time BASELINE config 3 (long context) or 4 (high batch, 8 tokens) at block level instead")
+    ap.add_argument("--mfma", choices=("bf16", "fp8"), default="bf16",
+                    help="the projections' MFMA: bf16 (default, float32-grade sums) or the scaled FP8 MFMA")
+    ap.add_argument("--no-alternatives", action="store_true",
+                    help="skip the extra timing of the same step with the other projection MFMA")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="time the step's GEMM shapes on hipBLASLt (torch bf16 and FP8) beside this build's GEMMs")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -757,7 +765,7 @@ def main() -> int:
             result["cpu_baseline"] = cpu_prefill_baseline(qwen38_27b_config(1), 1024, 512, seed, 16)
         print(json.dumps(result), flush=True)
         return 0
-    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4, args.kv_fp8)
+    engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4, args.kv_fp8, args.mfma)
     if args.decode:
         result = decode_main(args, cfg, engine, batch, context, max_seq_len)
         if not args.no_cpu_baseline:
@@ -813,6 +821,7 @@ def main() -> int:
     log(f"gate/up GEMM inside the steps: {launches} launches, {kernel_ms * 1000:.1f} us each")
     flops = 2.0 * batch * tokens * 2 * cfg.intermediate_size * cfg.hidden_size
     achieved = flops / (kernel_ms / 1000.0) / 1e12
+    peak = FP8_PEAK_TFLOPS if args.mfma == "fp8" else BF16_PEAK_TFLOPS
     alg = algorithmic_bytes(cfg, batch, tokens, context, args.mxfp4, args.kv_fp8)
     step_gbs = alg["total"] / (ms / 1000.0) / 1e9
     result = {
@@ -839,11 +848,11 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": f"gemm_kernel<2,4,2,2,e5m2,3,SWIGLU,{'e2m1' if args.mxfp4 else 'e4m3'},bf16 MFMA,KU=2> (MLP gate/up, 256 x 34816 x 5120)",
+            "kernel": f"gemm_kernel<2,4,2,2,e5m2,3,SWIGLU,{'e2m1' if args.mxfp4 else 'e4m3'},{args.mfma} MFMA,KU=2> (MLP gate/up, 256 x 34816 x 5120)",
             "achieved": round(achieved, 1),
-            "peak": BF16_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": profiled_traffic(),
             "avg_ms": round(kernel_ms, 4),
             "launches_timed": launches,
@@ -858,6 +867,23 @@ def main() -> int:
         },
         "accepted_per_step": accepted / args.steps,
     }
+    if not args.no_alternatives and not args.decode:
+        # The same step with the other projection MFMA, timed the same way on a second engine (reported beside the
+        # line, not as its value: the FP8 MFMA's sums are not float32-grade).
+        other = "fp8" if args.mfma == "bf16" else "bf16"
+        del engine
+        torch.cuda.empty_cache()
+        engine, st = build(cfg, batch, tokens, max_seq_len, context, seed, args.mxfp4, args.kv_fp8, other)
+        for _ in range(args.warmup):
+            step(graph=False)
+        for _ in range(2):
+            step(graph=True)
+        ms_other, acc_other = timed(graph=True)
+        engine.handle.raise_step_errors()
+        log(f"with the {other} MFMA: {ms_other:.3f} ms/step")
+        result["alternative"] = {"projection_mfma": other, "ms_per_step": round(ms_other, 4),
+                                 "value": round(acc_other / (ms_other * args.steps / 1000.0), 2),
+                                 "step_hbm_frac": round(alg["total"] / (ms_other / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)}
     if not args.no_cpu_baseline:
         from qwen38_amd.config import qwen38_27b_config as big
 
