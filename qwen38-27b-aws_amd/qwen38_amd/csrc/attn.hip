@@ -14,10 +14,12 @@
 // launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the other path
 // takes):
 //   attn_scores (chunk of 512 cached positions, KV head, row): q norm + RoPE, the chunk's scores by MFMA (sixteen
-//       waves, one block of 32 positions each), the chunk's per-row max m_c, probabilities e = exp(s - m_c) (stored as float32) and
-//       their sum s_c. Chunk 0 also normalises and rotates the step's own keys and scores them.
+//       waves, one block of 32 positions each), the chunk's per-row max m_c, the sum s_c of e = exp(s - m_c), and the
+//       scores s themselves (stored as bf16: each is bf16 / 16, so two bytes hold it exactly). Chunk 0 also normalises
+//       and rotates the step's own keys and scores them.
 //   attn_out (quarter of the 256 dims, KV head, row): the row's max M and sum S = sum_c s_c e^(m_c - M) (chunk order)
-//       + own terms; bf16 weights bf16(e * (e^(m_c - M) / S)) formed in registers and multiplied with V by MFMA over
+//       + own terms; e = exp(s - m_c) again from the stored scores (the same float32 values attn_scores summed);
+//       bf16 weights bf16(e * (e^(m_c - M) / S)) formed in registers and multiplied with V by MFMA over
 //       all visible positions (four waves, added in wave order); the own part, the gate, e5m2 activation tiles for
 //       o_proj; then the step's keys and values into the cache. The weights differ from the reference's
 //       bf16(e^(s - M) / S) by a few float32 ulps before the bf16 rounding (the product of two exponentials).
@@ -487,9 +489,11 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     }
     __syncthreads();
 
-    // Phase C: the chunk's probabilities e = exp(s - m_c) (stored as float32) and their sums.
+    // Phase C: the sums of the chunk's e = exp(s - m_c), and the scores themselves for attn_out, which forms the same
+    // e from them. A score is bf16(acc) / 16 (score_block), so 16 s is a bf16 value and its upper half keeps it whole:
+    // two bytes a score instead of the four of e.
     float lsum[QT];
-    float* pr = a.probs + head * ATTN_QMAX * S;
+    bf16_t* sr = a.scores + head * ATTN_QMAX * S;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         lsum[qt] = 0.0f;
@@ -498,10 +502,13 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
         const float m = mrow[q];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const v4f e = {expf(sacc[qt][g * 4] - m), expf(sacc[qt][g * 4 + 1] - m), expf(sacc[qt][g * 4 + 2] - m),
-                           expf(sacc[qt][g * 4 + 3] - m)};
-            lsum[qt] += (e[0] + e[1]) + (e[2] + e[3]);
-            *(v4f*)(pr + (size_t)q * S + blk * 32 + g * 8 + (lane >> 5) * 4) = e;
+            const float s[4] = {sacc[qt][g * 4], sacc[qt][g * 4 + 1], sacc[qt][g * 4 + 2], sacc[qt][g * 4 + 3]};
+            lsum[qt] += (expf(s[0] - m) + expf(s[1] - m)) + (expf(s[2] - m) + expf(s[3] - m));
+            uint32_t hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hi[i] = __float_as_uint(s[i] * 16.0f) >> 16;
+            *(uint2*)(sr + (size_t)q * S + blk * 32 + g * 8 + (lane >> 5) * 4) =
+                make_uint2(hi[0] | hi[1] << 16, hi[2] | hi[3] << 16);
         }
     }
 #pragma unroll
@@ -521,7 +528,8 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
 }
 
 template <int QT, bool KV8>
-__global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
+// One 32-row tile fits three waves per SIMD in registers without spilling; two tiles keep two.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attn_out_kernel(const AttnArgs a) {
     constexpr int PF = QT == 1 ? 4 : 2;  // blocks of 32 positions whose loads one wave keeps in flight
     __shared__ float mx[QT * 32], inv[QT * 32];
     __shared__ float wown[QT * 32][ATTN_KMAX];
@@ -540,50 +548,50 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
         hh = bid >> 2;
     }
     const int b = hh / a.Hkv, kvh = hh % a.Hkv;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index as a uniform value, so that the position loop branches on scalars.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b), nblk = (npos + 31) >> 5;
     if (npos <= a.fused_max) return;  // attn_fused takes this row
     const size_t head = (size_t)hh;
     const int dq = quarter * 64;
-    const float* pr = a.probs + head * ATTN_QMAX * S;
+    const bf16_t* sr = a.scores + head * ATTN_QMAX * S;
     const float* cmax = a.stats + head * a.nchunks * ATTN_QMAX * 2;
     const size_t vc = head * S * 256;
     const float vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
 
-    // V and probability loads of the wave's first blocks (w, w + 4, ...). Lane l: V dims dq + 32 dt + l % 32, positions
-    // 16 (l / 32) .. + 15 of the block; probabilities of query row l % 32 of each tile at the same positions, and that
-    // row's chunk max.
+    // V and score loads, PF blocks in flight per wave: slot j holds block w + 4j of each group of 4 PF blocks, and is
+    // refilled with its block of the next group as soon as its MFMAs are issued. Lane l: V dims dq + 32 dt + l % 32,
+    // positions 16 (l / 32) .. + 15 of the block; scores (times 16) of query row l % 32 of each tile at the same
+    // positions, and that row's chunk max. Slots past the last block load the last block again (never used), so that
+    // every load is unconditional.
     v8bf vf[PF][2][2];
     uint4 vr[PF][2];  // KV8: the raw bytes, widened at their MFMAs
-    v4f ef[PF][QT][4];
+    uint4 sb[PF][QT][2];
     float mc[PF][QT];
-    auto issue = [&](int blk0) {
+    auto issue = [&](int j, int blk) {
+        blk = min(blk, nblk - 1);
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int blk = blk0 + 4 * j;
-            if (blk >= nblk) break;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-                const size_t vo = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
-                if constexpr (KV8) {
-                    vr[j][dt] = *(const uint4*)((const uint8_t*)a.v_cache + vo);
-                } else {
-                    vf[j][dt][0] = load8(a.v_cache + vo);
-                    vf[j][dt][1] = load8(a.v_cache + vo + 8);
-                }
-            }
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                const int q = qt * 32 + (lane & 31);
-                const float* pp = pr + (size_t)q * S + blk * 32 + (lane >> 5) * 16;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) ef[j][qt][g] = *(const v4f*)(pp + 4 * g);
-                mc[j][qt] = cmax[((blk / SW) * ATTN_QMAX + q) * 2];
+        for (int dt = 0; dt < 2; ++dt) {
+            const size_t vo = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
+            if constexpr (KV8) {
+                vr[j][dt] = *(const uint4*)((const uint8_t*)a.v_cache + vo);
+            } else {
+                vf[j][dt][0] = load8(a.v_cache + vo);
+                vf[j][dt][1] = load8(a.v_cache + vo + 8);
             }
         }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const int q = qt * 32 + (lane & 31);
+            const bf16_t* sp = sr + (size_t)q * S + blk * 32 + (lane >> 5) * 16;
+            sb[j][qt][0] = *(const uint4*)sp;
+            sb[j][qt][1] = *(const uint4*)(sp + 8);
+            mc[j][qt] = cmax[((blk / SW) * ATTN_QMAX + q) * 2];
+        }
     };
-    issue(wave);
+#pragma unroll
+    for (int j = 0; j < PF; ++j) issue(j, wave + 4 * j);
 
     // Row statistics, own weights, own keys and values of this quarter, and the gates.
     if (tid < QT * 32) {
@@ -642,37 +650,49 @@ __global__ __launch_bounds__(256) void attn_out_kernel(const AttnArgs a) {
         qm[qt] = mx[qt * 32 + (lane & 31)];
         qi[qt] = inv[qt * 32 + (lane & 31)];
     }
-    for (int blk0 = wave; blk0 < nblk; blk0 += 4 * PF) {
-        if (blk0 != wave) issue(blk0);
+    // Block `blk` from slot j: its weights, times V into the accumulators.
+    auto consume = [&](int j) {
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            if (blk0 + 4 * j >= nblk) break;
+        for (int qt = 0; qt < QT; ++qt) {
+            // bf16(e^(s - m_c) e^(m_c - M) / S): the chunk's probabilities, as attn_scores summed them, rescaled
+            // to the row's softmax.
+            const float f = expf(mc[j][qt] - qm[qt]) * qi[qt], m = mc[j][qt];
+            const u4t lo = __builtin_bit_cast(u4t, sb[j][qt][0]), hi = __builtin_bit_cast(u4t, sb[j][qt][1]);
+            uint32_t wbits[8];
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                // bf16(e^(s - m_c) e^(m_c - M) / S): the chunk's probabilities rescaled to the row's softmax.
-                const float f = expf(mc[j][qt] - qm[qt]) * qi[qt];
-                uint32_t wbits[8];
+            for (int w = 0; w < 8; ++w) {
+                const uint32_t pair = w < 4 ? lo[w] : hi[w - 4];
+                const float s0 = bf2f(pair & 0xffff) * 0.0625f, s1 = bf2f(pair >> 16) * 0.0625f;
+                wbits[w] = pk_bf16(expf(s0 - m) * f, expf(s1 - m) * f);
+            }
+            const v8bf w0 = __builtin_bit_cast(v8bf, (u4t){wbits[0], wbits[1], wbits[2], wbits[3]});
+            const v8bf w1 = __builtin_bit_cast(v8bf, (u4t){wbits[4], wbits[5], wbits[6], wbits[7]});
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    wbits[2 * g] = pk_bf16(ef[j][qt][g][0] * f, ef[j][qt][g][1] * f);
-                    wbits[2 * g + 1] = pk_bf16(ef[j][qt][g][2] * f, ef[j][qt][g][3] * f);
-                }
-                const v8bf w0 = __builtin_bit_cast(v8bf, (u4t){wbits[0], wbits[1], wbits[2], wbits[3]});
-                const v8bf w1 = __builtin_bit_cast(v8bf, (u4t){wbits[4], wbits[5], wbits[6], wbits[7]});
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    if constexpr (KV8) {
-                        if (qt == 0) {
-                            vf[j][dt][0] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].x, vr[j][dt].y, vsc));
-                            vf[j][dt][1] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].z, vr[j][dt].w, vsc));
-                        }
+            for (int dt = 0; dt < 2; ++dt) {
+                if constexpr (KV8) {
+                    if (qt == 0) {
+                        vf[j][dt][0] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].x, vr[j][dt].y, vsc));
+                        vf[j][dt][1] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].z, vr[j][dt].w, vsc));
                     }
-                    acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, vf[j][dt][0], acc[qt][dt], 0, 0, 0);
-                    acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, vf[j][dt][1], acc[qt][dt], 0, 0, 0);
                 }
+                acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, vf[j][dt][0], acc[qt][dt], 0, 0, 0);
+                acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, vf[j][dt][1], acc[qt][dt], 0, 0, 0);
             }
         }
+    };
+    // Whole groups of PF blocks, each slot refilled after its MFMAs (the loop has no other exit, so the waits at
+    // its top count only the oldest slot's loads), then the last, partial group.
+    int blk0 = wave;
+    for (; blk0 + 4 * (PF - 1) < nblk; blk0 += 4 * PF) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            consume(j);
+            issue(j, blk0 + 4 * PF + 4 * j);
+        }
     }
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j)
+        if (blk0 + 4 * j < nblk) consume(j);
 
     // Per 32-row tile: the four waves' sums through LDS (lane l holds dim column l % 32 of each 32-dim half and rows
     // acc_row(i, l)), then own part, gate and e5m2 bytes, four dims per thread.

@@ -518,7 +518,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         a.k_scale = ks;
         a.v_scale = vs;
         a.nchunks = h->attn_nchunks;
-        a.probs = (float*)h->ws(h->off_scores);
+        a.scores = (bf16_t*)h->ws(h->off_scores);
         a.stats = (float*)h->ws(h->off_astats);
         a.own = (float*)h->ws(h->off_aown);
         a.kv_own = (float*)h->ws(h->off_akv);
@@ -696,7 +696,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     h->off_gates = take((size_t)h->gate_groups * Tp * 2 * h->Hv * 4);
     const size_t heads = (size_t)h->B * h->Hkv;
     h->attn_nchunks = (h->S + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    h->off_scores = take(heads * ATTN_QMAX * h->S * 4);
+    h->off_scores = take(heads * ATTN_QMAX * h->S * 2);
     h->off_astats = take(heads * h->attn_nchunks * ATTN_QMAX * 2 * 4);
     h->off_aown = take(heads * ATTN_QMAX * ATTN_KMAX * 4);
     h->off_akv = take(heads * 2 * ATTN_KMAX * 256 * 4);

@@ -48,6 +48,13 @@ __device__ __forceinline__ void wait_and_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// The same, after this wave's LDS reads have also returned: for a schedule whose reads of a stage are not all consumed
+// by MFMAs before the barrier that frees the stage for loading.
+template <int N>
+__device__ __forceinline__ void wait_all_and_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Direct global -> LDS load of BYTES per lane: lane l's bytes land at LDS address dst + l * BYTES (dst wave-uniform).
 // Issued as inline assembly, so the compiler neither waits for it before unrelated LDS reads (it cannot tell ring
 // stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the compiler's waits for its own loads only
@@ -117,6 +124,9 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
                   "weight stage splits evenly over the waves, each load inside one tile");
     static_assert(SC_CHUNKS >= 1 && NW % SC_CHUNKS == 0, "scale stage splits evenly over the waves");
     static_assert(OPS * (S - 2) <= 63 && S >= 2, "vmcnt range");
+    // The pipelined schedule (bf16 MFMA, units of an even number of K-steps) waits with up to S - 1 stages in flight.
+    constexpr bool PIPE = !F8 && KU % 2 == 0;
+    static_assert(!PIPE || OPS * (S - 1) <= 63, "vmcnt range");
     static_assert(EPI != EPI_SWIGLU || FR % 2 == 0, "gate and up tiles pair up");
     static_assert(!F8 || (A8 && !W4), "the FP8 MFMA takes e4m3 weight tiles and e5m2 activation tiles");
     constexpr int SLOT = FR * TR * 16 * NTH;  // floats of one stream-K partial
@@ -287,6 +297,63 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     auto compute = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < KU; ++j) compute_sub(st, j);
+    };
+
+    // The same K-step split in two for the pipelined schedule: prep reads and widens all of a K-step's operands into
+    // registers, mma runs its MFMAs (in compute_sub's order, so the same sums).
+    struct Ops {
+        v8bf w[4][FR];
+        v8bf x[4][TR];
+    };
+    auto prep = [&](int st, int j, Ops& o) __attribute__((always_inline)) {
+        const uint8_t* sb = lds + st * STAGE + j * SUB;
+        const uint8_t* wl = sb + ACT_B + (wf * FR) * WTB + lane * (WTB / 256);
+        const uint8_t* sl = sb + ACT_B + W_B + (wf * FR) * 64 + (lane & 31) * 2;
+#pragma unroll
+        for (int f = 0; f < FR; ++f) {
+            const uint32_t sc = *(const uint16_t*)(sl + f * 64);
+            const float s0 = __uint_as_float((sc & 0xffu) << 23), s1 = __uint_as_float((sc >> 8) << 23);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                if constexpr (W4) {
+                    o.w[m][f] = widen_e2m1(*(const uint32_t*)(wl + f * 1024 + m * 256), m < 2 ? s0 : s1);
+                } else {
+                    const u2 r = *(const u2*)(wl + f * 2048 + m * 512);
+                    o.w[m][f] = widen_e4m3(r[0], r[1], m < 2 ? s0 : s1);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TR; ++t)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                if constexpr (A8) {
+                    const u2 r = *(const u2*)(sb + (wt * TR + t) * 2048 + m * 512 + lane * 8);
+                    o.x[m][t] = widen_e5m2(r[0], r[1]);
+                } else {
+                    o.x[m][t] = *(const v8bf*)(sb + (wt * TR + t) * 4096 + m * 1024 + lane * 16);
+                }
+            }
+    };
+    // Makes the widened operands of `o` exist at this point: keeps the compiler from sinking a prep's conversions past
+    // the tile-end branch, away from the MFMAs they are meant to run beside.
+    auto pin = [&](Ops& o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int f = 0; f < FR; ++f) asm volatile("" : "+v"(o.w[m][f]));
+#pragma unroll
+            for (int t = 0; t < TR; ++t) asm volatile("" : "+v"(o.x[m][t]));
+        }
+    };
+    auto mma = [&](const Ops& o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int t = 0; t < TR; ++t)
+#pragma unroll
+                for (int f = 0; f < FR; ++f)
+                    acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.w[m][f], o.x[m][t], acc[f][t], 0, 0, 0);
     };
 
     // Accumulator layout of a 32x32 MFMA: lane l holds token column l % 32 and feature rows
@@ -469,26 +536,8 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
     int cfb = ifb, ck = ik;
     bool partial_start = ik != 0;  // the current tile segment began inside the tile
     int later0 = -1, later1 = -1;  // tiles to finish by recomputation (at most the range's first and last)
-#pragma unroll
-    for (int i = 0; i < S - 1; ++i)
-        if (i < n) {
-            issue(ifb, ik, i);
-            if (++ik == KS) ik = 0, ifb += fstep;
-        }
-    zero();
-    int st = 0, ist = S - 1;  // stage computed now, stage loaded next
-    for (int i = 0; i < n; ++i) {
-        if (i + S - 2 < n)
-            wait_and_barrier<OPS*(S - 2)>();
-        else
-            wait_and_barrier<0>();
-        if (i + S - 1 < n) {
-            issue(ifb, ik, ist);
-            if (++ik == KS) ik = 0, ifb += fstep;
-            if (++ist == S) ist = 0;
-        }
-        compute(st);
-        if (++st == S) st = 0;
+    // After the last K-step of unit i: the tile's epilogue or stream-K fixup when the unit ends a tile or the range.
+    auto after_unit = [&](int i) __attribute__((always_inline)) {
         if (ck == KS - 1 || i == n - 1) {
             if (EPI == EPI_PARTIAL || (!partial_start && ck == KS - 1))
                 epilogue(cfb);
@@ -498,10 +547,76 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             partial_start = false;
         }
         if (++ck == KS) ck = 0, cfb += fstep;
+    };
+    if constexpr (PIPE) {
+        // Pipelined: every stage loaded up front; each K-step's operands are read and widened while the previous
+        // K-step's MFMAs run. Unit i's last K-step waits for unit i + 1's stage (and the barrier after which every
+        // wave has read all of unit i), refills unit i's stage with unit i + S, and preps unit i + 1's first K-step
+        // beside its own MFMAs. KU is even, so K-step j of every unit uses operand set j % 2. The loop body has no
+        // branch but the tile ends, so that the preps and MFMAs schedule together: past the range's last unit the
+        // loads repeat that unit into stages no longer read (S - 1 extra units per range, from L2) and the last prep
+        // reads a stage it never uses; every load has landed before the workgroup leaves its LDS.
+        Ops ops[2];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            issue(ifb, ik, i);
+            if (i + 1 < n && ++ik == KS) ik = 0, ifb += fstep;
+        }
+        zero();
+        wait_all_and_barrier<OPS*(S - 1)>();
+        prep(0, 0, ops[0]);
+        int st = 0;
+        for (int i = 0; i < n; ++i) {
+            const int nst = st + 1 == S ? 0 : st + 1;
+#pragma unroll
+            for (int j = 0; j < KU; ++j) {
+                if (j + 1 < KU) {
+                    prep(st, j + 1, ops[(j + 1) & 1]);
+                    mma(ops[j & 1]);
+                    pin(ops[(j + 1) & 1]);
+                } else {
+                    wait_all_and_barrier<OPS*(S - 2)>();  // loads issued after unit i + 1's: units i + 2 .. i + S - 1
+                    issue(ifb, ik, st);                   // unit i + S, or the range's last unit again
+                    // The cursor moves on while units remain (selects, not a branch).
+                    const int nk = ik + (i + S + 1 < n ? 1 : 0);
+                    ifb += nk == KS ? fstep : 0;
+                    ik = nk == KS ? 0 : nk;
+                    prep(nst, 0, ops[0]);
+                    mma(ops[j & 1]);
+                    pin(ops[0]);
+                }
+            }
+            st = nst;
+            after_unit(i);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+#pragma unroll
+        for (int i = 0; i < S - 1; ++i)
+            if (i < n) {
+                issue(ifb, ik, i);
+                if (++ik == KS) ik = 0, ifb += fstep;
+            }
+        zero();
+        int st = 0, ist = S - 1;  // stage computed now, stage loaded next
+        for (int i = 0; i < n; ++i) {
+            if (i + S - 2 < n)
+                wait_and_barrier<OPS*(S - 2)>();
+            else
+                wait_and_barrier<0>();
+            if (i + S - 1 < n) {
+                issue(ifb, ik, ist);
+                if (++ik == KS) ik = 0, ifb += fstep;
+                if (++ist == S) ist = 0;
+            }
+            compute(st);
+            if (++st == S) st = 0;
+            after_unit(i);
+        }
     }
     if constexpr (EPI != EPI_PARTIAL) {
         if (later0 >= 0) {
-            wait_and_barrier<0>();  // every wave is done with the ring
+            wait_all_and_barrier<0>();  // every wave is done with the ring
 #pragma unroll 1
             for (int d = 0; d < 2; ++d) {
                 const int fb = d ? later1 : later0;

@@ -154,7 +154,7 @@ struct AttnArgs {
     bf16_t* k_cache;
     bf16_t* v_cache;
     int nchunks;            // chunks of ATTN_CHUNK cached positions over S
-    float* probs;           // [B*Hkv][ATTN_QMAX][S]: exp(score - chunk max)
+    bf16_t* scores;         // [B*Hkv][ATTN_QMAX][S]: the scores times 16 (bf16-exact); attn_out forms exp(s - chunk max)
     float* stats;           // [B*Hkv][nchunks][ATTN_QMAX][2]: per chunk, max and sum of exp(score - max)
     float* own;             // [B*Hkv][ATTN_QMAX][ATTN_KMAX]: scores of the step's own keys (-inf where masked)
     float* kv_own;          // [B*Hkv][2][ATTN_KMAX][256]: the step's keys (normed, rotated) and values
