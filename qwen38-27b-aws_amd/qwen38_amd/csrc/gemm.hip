@@ -55,25 +55,32 @@ __device__ __forceinline__ void wait_all_and_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Direct global -> LDS load of BYTES per lane: lane l's bytes land at LDS address dst + l * BYTES (dst wave-uniform).
-// Issued as inline assembly, so the compiler neither waits for it before unrelated LDS reads (it cannot tell ring
-// stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the compiler's waits for its own loads only
-// get longer. NT marks the load non-temporal. The head's weight and scale streams (1.31 GB, read once per launch) use
-// it: L2 then keeps the activation tiles every workgroup rereads (the 256-row head's HBM reads fall from 2.2 GB to
-// 1.43 GB per launch). So does the SwiGLU pair at 64 tokens (the decode step: 45.4 against 50.1 us). The other
-// decoder projections do not: at 256 tokens it changed no GEMM's time or slowed it, and the attention kernel that
-// follows them ran 55 instead of 46 us.
+// Direct global -> LDS load of BYTES per lane: lane l's bytes come from base + voff (base wave-uniform, held in SGPRs,
+// voff a 32-bit per-lane offset) and land at LDS address dst + l * BYTES (dst wave-uniform). The scalar base keeps the
+// per-load address arithmetic on the scalar unit (the 256-token speculative step 21.13 against 21.46 ms with 64-bit
+// per-lane addresses, A/B on one box). Issued as inline assembly, so the compiler neither waits for it before unrelated
+// LDS reads (it cannot tell ring stages apart) nor counts it; the main loop's own vmcnt waits cover it, and the
+// compiler's waits for its own loads only get longer. NT marks the load non-temporal. The head's weight and scale
+// streams (1.31 GB, read once per launch) use it: L2 then keeps the activation tiles every workgroup rereads (the
+// 256-row head's HBM reads fall from 2.2 GB to 1.43 GB per launch). So does the SwiGLU pair at 64 tokens (the decode
+// step: 45.4 against 50.1 us). The other decoder projections do not: at 256 tokens it changed no GEMM's time or slowed
+// it, and the attention kernel that follows them ran 55 instead of 46 us.
 template <int BYTES, bool NT = false>
-__device__ __forceinline__ void lds_load(const void* src, uint32_t dst) {
+__device__ __forceinline__ void lds_load(const void* base, uint32_t voff, uint32_t dst) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(dst);
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    // readfirstlane returns a signed int: each word goes through uint32_t so that neither is sign-extended.
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
     if constexpr (BYTES == 16 && NT)
-        asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
+        asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sb), "{m0}"(m0) : "memory");
     else if constexpr (BYTES == 16)
-        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+        asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "{m0}"(m0) : "memory");
     else if constexpr (NT)
-        asm volatile("global_load_lds_dword %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
+        asm volatile("global_load_lds_dword %0, %1 nt" ::"v"(voff), "s"(sb), "{m0}"(m0) : "memory");
     else
-        asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+        asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(sb), "{m0}"(m0) : "memory");
 }
 
 __device__ __forceinline__ uint32_t bits(v2bf v) { return __builtin_bit_cast(uint32_t, v); }
@@ -191,16 +198,16 @@ __global__ __launch_bounds__(WF * WT * 64, 1) void gemm_kernel(const GemmArgs a)
             for (int i = 0; i < N_ACT; ++i) {
                 const int off = (i * NW + wave) * (64 * ACT_DMA);
                 const uint8_t* g = act_base + ((size_t)(off / AT) * KS64 + k64) * AT + off % AT;
-                lds_load<ACT_DMA>(g + lane * ACT_DMA, sb + off);
+                lds_load<ACT_DMA>(g, lane * ACT_DMA, sb + off);
             }
 #pragma unroll
             for (int i = 0; i < N_W; ++i) {
                 const int off = (i * NW + wave) * (64 * W_DMA);
                 const uint8_t* g = a.w + ((size_t)(fb * FT + off / WTB) * KS64 + k64) * WTB + off % WTB;
-                lds_load<W_DMA, NT_W>(g + lane * W_DMA, sb + ACT_B + off);
+                lds_load<W_DMA, NT_W>(g, lane * W_DMA, sb + ACT_B + off);
             }
             const uint8_t* g = a.ws + ((size_t)(fb * FT + sc_c * 4) * KS64 + k64) * 64;
-            lds_load<4, NT_W>(g + sc_lane, sb + ACT_B + W_B + sc_c * 256);
+            lds_load<4, NT_W>(g, sc_lane, sb + ACT_B + W_B + sc_c * 256);
         }
     };
 
