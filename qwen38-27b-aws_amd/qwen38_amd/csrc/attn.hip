@@ -251,8 +251,21 @@ __global__ __launch_bounds__(SW * 64) void attn_fused_kernel(const AttnArgs a) {
     const int kvh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
     const int npos = visible(a, b);
-    if (npos > NB * ATTN_CHUNK) return;  // the chunked kernels take this row
     const size_t head = (size_t)b * a.Hkv + kvh;
+    if (npos > NB * ATTN_CHUNK) {
+        // The chunked kernels take this row: here only its rows, once for all of its chunks — the query rows normed
+        // and rotated into qprep, the step's own keys (normed, rotated) and values into kv_own.
+        RowLoads<QT, SW, KV8> rows;
+        rows.load(a, b, kvh, wave, lane, true);
+        rows.finish(a, wave, lane, true, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
+        __syncthreads();
+        bf16_t* dst = a.qprep + head * ATTN_QMAX * 256;
+        for (int i = tid; i < QT * 32 * 32; i += SW * 64) {  // 16-byte pieces: row i / 32, dims 8 (i % 32) + [0, 8)
+            const int r = i >> 5, d = (i & 31) * 8;
+            *(uint4*)(dst + r * 256 + d) = *(const uint4*)(qb + r * QPITCH + d);
+        }
+        return;
+    }
     auto scored = [&](int nb) { return (nb * SW + wave) * 32 < npos; };
     const int dcol = wave * 16 + (lane & 15);  // output dim of this lane
 
@@ -453,16 +466,31 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     const int blk = (p_lo >> 5) + wave;  // this wave's 32 positions
     const bool scored = blk * 32 < p_hi;
 
-    // The step's rows first, then the cache keys (clamped into the cache for waves past the chunk's positions, whose
-    // scores are never formed), so that the row work waits for its own loads only.
-    RowLoads<QT, SW, KV8> rows;
-    rows.load(a, b, kvh, wave, lane, first);
+    // The query rows as attn_fused prepared them (normed, rotated; chunk 0 also the step's own keys) first, then the
+    // cache keys (clamped into the cache for waves past the chunk's positions, whose scores are never formed), so that
+    // the copy into LDS waits for its own loads only.
+    constexpr int QP = QT * 32 * 32 / (SW * 64);  // 16-byte pieces of the query rows per thread
+    const bf16_t* qsrc = a.qprep + head * ATTN_QMAX * 256;
+    uint4 qv[QP];
+#pragma unroll
+    for (int u = 0; u < QP; ++u) qv[u] = *(const uint4*)(qsrc + (tid + u * SW * 64) * 8);
+    const float* ksrc = a.kv_own + head * 2 * ATTN_KMAX * 256;
+    float4 kv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // own keys: 4 of K x 256 per thread (chunk 0)
+    if (first && tid * 4 < K * 256) kv = *(const float4*)(ksrc + tid * 4);
     asm volatile("" ::: "memory");
     v8bf kf[16];
     load_keys<KV8>(a, head, min(blk * 32, S - 32), lane, kf);
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);  // nor may the row arithmetic (and its waits) be scheduled above the key loads
-    rows.finish(a, wave, lane, first, qb, kb, a.kv_own + head * 2 * ATTN_KMAX * 256, nullptr);
+    __builtin_amdgcn_sched_barrier(0);  // nor may the copies (and their waits) be scheduled above the key loads
+#pragma unroll
+    for (int u = 0; u < QP; ++u) {
+        const int i = tid + u * SW * 64, r = i >> 5, d = (i & 31) * 8;
+        *(uint4*)(qb + r * QPITCH + d) = qv[u];
+    }
+    if (first && tid * 4 < K * 256) {
+        const int t = (tid * 4) >> 8, d = (tid * 4) & 255;
+        *(uint2*)(kb + t * QPITCH + d) = make_uint2(pk_bf16(kv.x, kv.y), pk_bf16(kv.z, kv.w));
+    }
     __syncthreads();
 
     // The wave's block of scores, kept in registers; chunk 0's last wave also scores the own keys.

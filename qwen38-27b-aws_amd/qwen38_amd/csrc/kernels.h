@@ -158,6 +158,7 @@ struct AttnArgs {
     float* stats;           // [B*Hkv][nchunks][ATTN_QMAX][2]: per chunk, max and sum of exp(score - max)
     float* own;             // [B*Hkv][ATTN_QMAX][ATTN_KMAX]: scores of the step's own keys (-inf where masked)
     float* kv_own;          // [B*Hkv][2][ATTN_KMAX][256]: the step's keys (normed, rotated) and values
+    bf16_t* qprep;          // [B*Hkv][ATTN_QMAX][256]: query rows normed and rotated, for the rows attn_scores takes
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
     int fused_max;          // set by the launcher: rows with at most this many visible positions take attn_fused
