@@ -11,12 +11,13 @@
 // Rows whose visible context is at most NB * 512 positions take one launch, attn_fused (KV head, row): sixteen
 // waves score NB blocks of 32 positions each, the softmax completes in the workgroup, and each wave then multiplies
 // the weights with 16 dims of V (NB = 2 for up to 32 query rows per KV head, else 1). Longer contexts take two
-// launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the other path
-// takes):
-//   attn_scores (chunk of 512 cached positions, KV head, row): q norm + RoPE, the chunk's scores by MFMA (sixteen
-//       waves, one block of 32 positions each), the chunk's per-row max m_c, the sum s_c of e = exp(s - m_c), and the
-//       scores s themselves (stored as bf16: each is bf16 / 16, so two bytes hold it exactly). Chunk 0 also normalises
-//       and rotates the step's own keys and scores them.
+// more launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the other
+// path takes); for them attn_fused only prepares the row once: its query rows normed and rotated (qprep) and the
+// step's own keys, normed and rotated, and values (kv_own).
+//   attn_scores (chunk of 512 cached positions, KV head, row): the prepared query rows, the chunk's scores by MFMA
+//       (sixteen waves, one block of 32 positions each), the chunk's per-row max m_c, the sum s_c of e = exp(s - m_c),
+//       and the scores s themselves (stored as bf16: each is bf16 / 16, so two bytes hold it exactly). Chunk 0 also
+//       scores the step's own keys.
 //   attn_out (quarter of the 256 dims, KV head, row): the row's max M and sum S = sum_c s_c e^(m_c - M) (chunk order)
 //       + own terms; e = exp(s - m_c) again from the stored scores (the same float32 values attn_scores summed);
 //       bf16 weights bf16(e * (e^(m_c - M) / S)) formed in registers and multiplied with V by MFMA over
