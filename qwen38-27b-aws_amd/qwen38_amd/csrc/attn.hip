@@ -37,13 +37,16 @@
 // The cache loads of a workgroup are issued first, so their latency overlaps the row-statistics work; loads are issued
 // before global stores (the pointers may alias as far as the compiler knows, and a load issued after a store waits
 // for it).
+#include <algorithm>
+#include <type_traits>
+
 #include "kernels.h"
 
 #define QPITCH 264  // bf16 elements per query row in LDS (256 + 8: rows start 4 banks apart)
-#define RPITCH 68   // floats per row of the cross-wave sums in attn_out
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef uint32_t u4t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2t __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -536,8 +539,9 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
             uint32_t hi[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) hi[i] = __float_as_uint(s[i] * 16.0f) >> 16;
-            *(uint2*)(sr + (size_t)q * S + blk * 32 + g * 8 + (lane >> 5) * 4) =
-                make_uint2(hi[0] | hi[1] << 16, hi[2] | hi[3] << 16);
+            if (q < NQ)  // rows past NQ are never read
+                *(uint2*)(sr + (size_t)q * S + blk * 32 + g * 8 + (lane >> 5) * 4) =
+                    make_uint2(hi[0] | hi[1] << 16, hi[2] | hi[3] << 16);
         }
     }
 #pragma unroll
@@ -556,223 +560,295 @@ __global__ __launch_bounds__(SW * 64) void attn_scores_kernel(const AttnArgs a) 
     }
 }
 
-template <int QT, bool KV8>
-// One 32-row tile fits three waves per SIMD in registers without spilling; two tiles keep two.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attn_out_kernel(const AttnArgs a) {
-    constexpr int PF = QT == 1 ? 4 : 2;  // blocks of 32 positions whose loads one wave keeps in flight
-    __shared__ float mx[QT * 32], inv[QT * 32];
-    __shared__ float wown[QT * 32][ATTN_KMAX];
-    __shared__ float kq[ATTN_KMAX][64], vq[ATTN_KMAX][64];
-    __shared__ __attribute__((aligned(16))) float red[4][32 * RPITCH];
+constexpr int PV_GP = 64;          // positions per group of attn_pv: one LDS weight tile and one barrier
+constexpr int PV_WP = PV_GP + 8;    // bf16 per weight row in LDS (rows start 4 banks apart)
+constexpr int PV_RP = 256 + 4;      // floats per row of the output tile in LDS
+constexpr int PV_SPLIT_MAX = 16;
 
-    // Block -> (quarter, head): the four quarters of one head run on one XCD (they share its probabilities in L2).
-    const int nheads = a.B * a.Hkv, bid = blockIdx.x;
-    int quarter, hh;
-    if (nheads % 8 == 0) {
-        const int l = bid >> 3;
-        quarter = l & 3;
-        hh = (l >> 2) * 8 + (bid & 7);
-    } else {
-        quarter = bid & 3;
-        hh = bid >> 2;
-    }
-    const int b = hh / a.Hkv, kvh = hh % a.Hkv;
-    // The wave index as a uniform value, so that the position loop branches on scalars.
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S;
-    const int npos = visible(a, b), nblk = (npos + 31) >> 5;
-    if (npos <= a.fused_max) return;  // attn_fused takes this row
-    const size_t head = (size_t)hh;
-    const int dq = quarter * 64;
-    const bf16_t* sr = a.scores + head * ATTN_QMAX * S;
-    const float* cmax = a.stats + head * a.nchunks * ATTN_QMAX * 2;
-    const size_t vc = head * S * 256;
-    const float vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
-
-    // V and score loads, PF blocks in flight per wave: slot j holds block w + 4j of each group of 4 PF blocks, and is
-    // refilled with its block of the next group as soon as its MFMAs are issued. Lane l: V dims dq + 32 dt + l % 32,
-    // positions 16 (l / 32) .. + 15 of the block; scores (times 16) of query row l % 32 of each tile at the same
-    // positions, and that row's chunk max. Slots past the last block load the last block again (never used), so that
-    // every load is unconditional.
-    v8bf vf[PF][2][2];
-    uint4 vr[PF][2];  // KV8: the raw bytes, widened at their MFMAs
-    uint4 sb[PF][QT][2];
-    float mc[PF][QT];
-    auto issue = [&](int j, int blk) {
-        blk = min(blk, nblk - 1);
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-            const size_t vo = vc + (size_t)blk * 8192 + (dq + dt * 32 + (lane & 31)) * 32 + (lane >> 5) * 16;
-            if constexpr (KV8) {
-                vr[j][dt] = *(const uint4*)((const uint8_t*)a.v_cache + vo);
-            } else {
-                vf[j][dt][0] = load8(a.v_cache + vo);
-                vf[j][dt][1] = load8(a.v_cache + vo + 8);
-            }
-        }
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const int q = qt * 32 + (lane & 31);
-            const bf16_t* sp = sr + (size_t)q * S + blk * 32 + (lane >> 5) * 16;
-            sb[j][qt][0] = *(const uint4*)sp;
-            sb[j][qt][1] = *(const uint4*)(sp + 8);
-            mc[j][qt] = cmax[((blk / SW) * ATTN_QMAX + q) * 2];
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < PF; ++j) issue(j, wave + 4 * j);
-
-    // Row statistics, own weights, own keys and values of this quarter, and the gates.
-    if (tid < QT * 32) {
-        const int nch = (npos + ATTN_CHUNK - 1) / ATTN_CHUNK;
-        const float* st = a.stats + head * a.nchunks * ATTN_QMAX * 2 + tid * 2;
+// The row statistics of the chunked path, by all 512 threads (a barrier inside): the row's max M over its chunks'
+// maxima and own scores, 1 / S with S = sum_c s_c e^(m_c - M) + its own terms e^(s - M), and its own weights
+// bf16(e^(s - M) / S). Each row's chunks are split in P contiguous parts, one thread each; the parts' sums are added
+// in part order, so the result is fixed. red holds 512 floats.
+template <int QT>
+__device__ __forceinline__ void pv_row_stats(const AttnArgs& a, size_t head, int npos, int tid, float* mx, float* inv,
+                                             float (*wown)[ATTN_KMAX], float* red) {
+    constexpr int R = QT * 32, P = 512 / R;
+    const int K = a.K, NQ = a.Hq / a.Hkv * K;
+    const int r = tid % R, p = tid / R;
+    const int nch = (npos + ATTN_CHUNK - 1) / ATTN_CHUNK, c0 = p * nch / P, c1 = (p + 1) * nch / P;
+    const float* st = a.stats + head * a.nchunks * ATTN_QMAX * 2 + r * 2;
+    float m = -INFINITY;
+    for (int c = c0; c < c1; ++c) m = fmaxf(m, st[c * ATTN_QMAX * 2]);
+    red[tid] = m;
+    __syncthreads();
+    float so[ATTN_KMAX];
+    if (tid < R) {
         const float* own = a.own + (head * ATTN_QMAX + tid) * ATTN_KMAX;
-        float so[ATTN_KMAX];
 #pragma unroll
         for (int tp = 0; tp < ATTN_KMAX; ++tp) so[tp] = tp < K && tid < NQ ? own[tp] : -INFINITY;
-        float m = -INFINITY;
-        for (int c = 0; c < nch; ++c) m = fmaxf(m, st[c * ATTN_QMAX * 2]);
+        float mm = red[tid];
 #pragma unroll
-        for (int tp = 0; tp < ATTN_KMAX; ++tp) m = fmaxf(m, so[tp]);
-        float s = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-            const float sc_ = st[c * ATTN_QMAX * 2 + 1];
-            if (sc_ > 0.0f) s += sc_ * expf(st[c * ATTN_QMAX * 2] - m);
-        }
+        for (int q = 1; q < P; ++q) mm = fmaxf(mm, red[q * R + tid]);
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) mm = fmaxf(mm, so[tp]);
+        mx[tid] = mm;
+    }
+    __syncthreads();
+    const float M = mx[r];
+    float s = 0.0f;
+    for (int c = c0; c < c1; ++c) {
+        const float sc_ = st[c * ATTN_QMAX * 2 + 1];
+        if (sc_ > 0.0f) s += sc_ * expf(st[c * ATTN_QMAX * 2] - M);
+    }
+    red[tid] = s;
+    __syncthreads();
+    if (tid < R) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int q = 0; q < P; ++q) ss += red[q * R + tid];
 #pragma unroll
         for (int tp = 0; tp < ATTN_KMAX; ++tp)
-            if (so[tp] > -INFINITY) s += expf(so[tp] - m);
-        const float iv = s > 0.0f ? 1.0f / s : 0.0f;
-        mx[tid] = m;
+            if (so[tp] > -INFINITY) ss += expf(so[tp] - M);
+        const float iv = ss > 0.0f ? 1.0f / ss : 0.0f;
         inv[tid] = iv;
 #pragma unroll
-        for (int tp = 0; tp < ATTN_KMAX; ++tp) wown[tid][tp] = so[tp] > -INFINITY ? rbf(expf(so[tp] - m) * iv) : 0.0f;
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) wown[tid][tp] = so[tp] > -INFINITY ? rbf(expf(so[tp] - M) * iv) : 0.0f;
     }
-    const float* kv_own = a.kv_own + head * 2 * ATTN_KMAX * 256 + dq;
-    for (int i = tid; i < K * 64; i += 256) {
-        kq[i >> 6][i & 63] = kv_own[(i >> 6) * 256 + (i & 63)];
-        vq[i >> 6][i & 63] = kv_own[(ATTN_KMAX + (i >> 6)) * 256 + (i & 63)];
-    }
-    const int dg = tid & 15;  // finish phase: dims dq + 4 dg .. + 3, rows (tid >> 4) + 16 it of each 32-row tile
-    uint2 gate[QT][2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int q = min(qt * 32 + (tid >> 4) + 16 * it, NQ - 1);
-            gate[qt][it] = *(const uint2*)(a.qkv + (size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 +
-                                           dq + 4 * dg);
-        }
-    __syncthreads();
+}
 
-    // Weights x V over the visible positions.
-    v16f acc[QT][2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[qt][dt][i] = 0.0f;
-    float qm[QT], qi[QT];
+// The step's own values (float32) into LDS, for the own part of the output.
+__device__ __forceinline__ void pv_own_values(const AttnArgs& a, size_t head, int tid, float (*vown)[256]) {
+    const float* src = a.kv_own + (head * 2 + 1) * ATTN_KMAX * 256;
+    for (int i = tid * 4; i < a.K * 256; i += 512 * 4) *(v4f*)&vown[i >> 8][i & 255] = *(const v4f*)(src + i);
+}
+
+// The output of one (row, KV head) from the weights x V sums in acc (wave w: dims 32w + l % 32 of its lane l, query
+// rows acc_row(i, l) of each 32-row tile): own part, gate and e5m2 activation bytes, as the reference adds them
+// (cache part and own part as separate bf16 matmuls added in bf16, then times bf16 sigmoid(gate)); then the step's
+// own keys and values into the cache (model.py:603-608, 653-654; inactive rows write the tail). Every wave has
+// consumed its V loads before the first barrier here, so the cache writes come after every read of this row's V in
+// the workgroup.
+template <int QT, bool KV8>
+__device__ __forceinline__ void pv_finish(const AttnArgs& a, int b, int kvh, size_t head, v16f (&acc)[QT], float* red,
+                                          const float (*wown)[ATTN_KMAX], const float (*vown)[256], int tid, int lane,
+                                          int wave) {
+    const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S, act_k = a.Hq * 256;
+    const int fr = tid >> 4, d0 = (tid & 15) * 16;  // this thread: row fr of each tile, dims d0 .. d0 + 15
+    u4t gate[QT][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        qm[qt] = mx[qt * 32 + (lane & 31)];
-        qi[qt] = inv[qt * 32 + (lane & 31)];
+        const int q = min(qt * 32 + fr, NQ - 1);
+        const bf16_t* gp = a.qkv + (size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + d0;
+        gate[qt][0] = *(const u4t*)gp;
+        gate[qt][1] = *(const u4t*)(gp + 8);
     }
-    // Block `blk` from slot j: its weights, times V into the accumulators.
-    auto consume = [&](int j) {
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            // bf16(e^(s - m_c) e^(m_c - M) / S): the chunk's probabilities, as attn_scores summed them, rescaled
-            // to the row's softmax.
-            const float f = expf(mc[j][qt] - qm[qt]) * qi[qt], m = mc[j][qt];
-            const u4t lo = __builtin_bit_cast(u4t, sb[j][qt][0]), hi = __builtin_bit_cast(u4t, sb[j][qt][1]);
-            uint32_t wbits[8];
+    for (int qt = 0; qt < QT; ++qt) {
+        __syncthreads();  // the weight tiles' last reads (or the previous tile's) are done
 #pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                const uint32_t pair = w < 4 ? lo[w] : hi[w - 4];
-                const float s0 = bf2f(pair & 0xffff) * 0.0625f, s1 = bf2f(pair >> 16) * 0.0625f;
-                wbits[w] = pk_bf16(expf(s0 - m) * f, expf(s1 - m) * f);
-            }
-            const v8bf w0 = __builtin_bit_cast(v8bf, (u4t){wbits[0], wbits[1], wbits[2], wbits[3]});
-            const v8bf w1 = __builtin_bit_cast(v8bf, (u4t){wbits[4], wbits[5], wbits[6], wbits[7]});
+        for (int i = 0; i < 16; ++i) red[acc_row(i, lane) * PV_RP + wave * 32 + (lane & 31)] = acc[qt][i];
+        __syncthreads();
+        const int q = qt * 32 + fr;
+        if (q < NQ) {
+            uint32_t bytes[4];
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-                if constexpr (KV8) {
-                    if (qt == 0) {
-                        vf[j][dt][0] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].x, vr[j][dt].y, vsc));
-                        vf[j][dt][1] = __builtin_bit_cast(v8bf, kv_widen8(vr[j][dt].z, vr[j][dt].w, vsc));
-                    }
+            for (int h = 0; h < 4; ++h) {
+                const v4f cache = *(const v4f*)&red[fr * PV_RP + d0 + 4 * h];
+                const u4t gw = gate[qt][h >> 1];
+                float gt[4], o[4];
+                unpack4(make_uint2(gw[(h & 1) * 2], gw[(h & 1) * 2 + 1]), gt);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float own = 0.0f;
+                    for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vown[tp][d0 + 4 * h + e];
+                    o[e] = rbf(rbf(cache[e]) + rbf(own));
+                    o[e] = rbf(o[e] * rbf(sigmoidf_(gt[e])));
                 }
-                acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, vf[j][dt][0], acc[qt][dt], 0, 0, 0);
-                acc[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, vf[j][dt][1], acc[qt][dt], 0, 0, 0);
+                bytes[h] = pk_e5m2(o[0], o[1], o[2], o[3]);
             }
+            const int t = q % K, col = (kvh * G + q / K) * 256 + d0;
+            *(uint2*)(a.act + act_offset(b * K + t, col, act_k)) = make_uint2(bytes[0], bytes[1]);
+            *(uint2*)(a.act + act_offset(b * K + t, col + 8, act_k)) = make_uint2(bytes[2], bytes[3]);
+        }
+    }
+
+    const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
+    const float* kown = a.kv_own + head * 2 * ATTN_KMAX * 256;
+    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f, vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
+    for (int i = tid; i < K * 256; i += 512) {
+        const int t = i >> 8, d = i & 255, p = base + t;
+        if (p < 0 || p >= S) continue;
+        const size_t ko = (head * S + p) * 256 + d, vo = head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31);
+        if constexpr (KV8) {
+            ((uint8_t*)a.k_cache)[ko] = (uint8_t)kv_code(kown[t * 256 + d], ksc);
+            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vown[t][d], vsc);
+        } else {
+            a.k_cache[ko] = f2bf(kown[t * 256 + d]);
+            a.v_cache[vo] = f2bf(vown[t][d]);
+        }
+    }
+}
+
+// Weights x V of the chunked path over one split of a (row, KV head)'s positions (blockIdx.x of pv_splits, whole
+// groups of 64 positions), eight waves, all 256 dims: per group, the 512 threads form the group's bf16 weights
+// bf16(e^(s - m_c) * (e^(m_c - M) / S)) once each, from the scores and chunk maxima attn_scores stored (the float32
+// values it summed), into an LDS tile; wave w multiplies the tile with dims 32w .. 32w + 31 of V by MFMA
+// (A = 32 query rows x 16 positions from LDS, B = 16 positions x 32 dims from registers), adding the groups in
+// position order. Loads run PF groups ahead (slot j of each round of PF; past the range they load the last
+// group again, never used, so that every load is unconditional). With one split the workgroup finishes the row;
+// with more, each stores its sums and attn_pv_finish adds them in split order.
+template <int QT, bool KV8>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attn_pv_kernel(const AttnArgs a) {
+    constexpr int WPT = QT * 32 * PV_GP / 512;  // weights formed per thread per group (4 or 8)
+    // Groups whose loads a wave keeps in flight: four, or three where two query tiles of bf16 V would not fit
+    // 128 VGPRs (two workgroups per CU) with four.
+    constexpr int PF = QT == 2 && !KV8 ? 3 : 4;
+    constexpr int NT = PF % 2 == 0 ? 2 : PF;    // LDS weight tiles (slot j writes tile j % NT)
+    constexpr int TILE = QT * 32 * PV_WP;       // bf16 per LDS weight tile
+    constexpr int SMEM = NT * TILE * 2 > 32 * PV_RP * 4 ? NT * TILE * 2 : 32 * PV_RP * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];  // the weight tiles; after the loop, red
+    __shared__ float mx[QT * 32], inv[QT * 32], wown[QT * 32][ATTN_KMAX], sred[512];
+    __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX][256];
+    bf16_t* wt = (bf16_t*)smem;
+
+    const int z = blockIdx.x, hh = blockIdx.y, b = hh / a.Hkv, kvh = hh % a.Hkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int npos = visible(a, b), S = a.S, ns = a.pv_splits;
+    if (npos <= a.fused_max) return;  // attn_fused takes this row
+    const size_t head = (size_t)hh;
+    const int ngrp = (npos + PV_GP - 1) / PV_GP, g_lo = z * ngrp / ns, g_hi = (z + 1) * ngrp / ns;
+    const bf16_t* sr = a.scores + head * ATTN_QMAX * S;
+    const float* cst = a.stats + head * a.nchunks * ATTN_QMAX * 2;
+    const size_t vc = head * S * 256 + (size_t)(wave * 32 + (lane & 31)) * 32 + (lane >> 5) * 8;
+    const float vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
+    const int fr = tid / (PV_GP / WPT), fc = tid % (PV_GP / WPT) * WPT;  // weights formed: row fr, positions + fc
+    const int NQ = a.Hq / a.Hkv * a.K, lr = min(fr, NQ - 1);              // rows past NQ load a real row, weigh 0
+
+    // Slot loads: V of this wave's dims over the group's 64 positions (lane half h: positions 16 kk + 8 h .. + 7 of
+    // MFMA step kk), the scores of the weights this thread forms and their chunk's max.
+    typedef typename std::conditional<KV8, uint2, v8bf>::type VSlot;
+    typedef typename std::conditional<WPT == 8, u4t, u2t>::type SSlot;
+    VSlot vs[PF][4];
+    SSlot ss[PF];
+    float mc[PF];
+    auto issue = [&](int j, int g) {
+        g = min(g, max(g_hi - 1, g_lo));
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const size_t vo = vc + (size_t)min(2 * g + (kk >> 1), S / 32 - 1) * 8192 + (kk & 1) * 16;
+            if constexpr (KV8)
+                vs[j][kk] = *(const uint2*)((const uint8_t*)a.v_cache + vo);
+            else
+                vs[j][kk] = load8(a.v_cache + vo);
+        }
+        ss[j] = *(const SSlot*)(sr + (size_t)lr * S + min(g * PV_GP + fc, S - WPT));
+        mc[j] = cst[((g * PV_GP / ATTN_CHUNK) * ATTN_QMAX + lr) * 2];
+    };
+#pragma unroll
+    for (int j = 0; j < PF; ++j) issue(j, g_lo + j);
+
+    pv_row_stats<QT>(a, head, npos, tid, mx, inv, wown, sred);
+    if (ns == 1) pv_own_values(a, head, tid, vown);
+    __syncthreads();
+
+    v16f acc[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[qt][i] = 0.0f;
+    const float fm = mx[lr], fi = inv[lr];
+    // Group g from slot j: its weights into tile w (positions at or past npos, and rows past NQ, weigh zero).
+    const int nlim = fr < NQ ? npos : 0;
+    auto form = [&](int j, int g, bf16_t* w) {
+        const float m = mc[j], f = expf(m - fm) * fi;
+        const int p0 = g * PV_GP + fc;
+        uint32_t words[WPT / 2];
+#pragma unroll
+        for (int e = 0; e < WPT / 2; ++e) {
+            const uint32_t pair = ss[j][e];
+            const float s0 = bf2f(pair & 0xffff) * 0.0625f, s1 = bf2f(pair >> 16) * 0.0625f;
+            words[e] = pk_bf16(p0 + 2 * e < nlim ? expf(s0 - m) * f : 0.0f, p0 + 2 * e + 1 < nlim ? expf(s1 - m) * f : 0.0f);
+        }
+        if constexpr (WPT == 8)
+            *(uint4*)(w + fr * PV_WP + fc) = make_uint4(words[0], words[1], words[2], words[3]);
+        else
+            *(uint2*)(w + fr * PV_WP + fc) = make_uint2(words[0], words[1]);
+    };
+    auto mfma = [&](int j, const bf16_t* w) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            v8bf vb;
+            if constexpr (KV8)
+                vb = __builtin_bit_cast(v8bf, kv_widen8(vs[j][kk].x, vs[j][kk].y, vsc));
+            else
+                vb = vs[j][kk];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+                acc[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    load8(w + (qt * 32 + (lane & 31)) * PV_WP + kk * 16 + (lane >> 5) * 8), vb, acc[qt], 0, 0, 0);
         }
     };
-    // Whole groups of PF blocks, each slot refilled after its MFMAs (the loop has no other exit, so the waits at
-    // its top count only the oldest slot's loads), then the last, partial group.
-    int blk0 = wave;
-    for (; blk0 + 4 * (PF - 1) < nblk; blk0 += 4 * PF) {
+    // Whole rounds of PF groups, each slot refilled after its MFMAs (the loop has no other exit, so the waits at
+    // its top count only the oldest slot's loads), then the last, partial round. Tile j % NT was last read NT
+    // groups earlier, before the barrier of the group after it.
+    int g = g_lo;
+    for (; g + PF <= g_hi; g += PF) {
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
-            consume(j);
-            issue(j, blk0 + 4 * PF + 4 * j);
+            bf16_t* w = wt + (j % NT) * TILE;
+            form(j, g + j, w);
+            __syncthreads();
+            mfma(j, w);
+            issue(j, g + j + PF);
         }
     }
 #pragma unroll
     for (int j = 0; j < PF - 1; ++j)
-        if (blk0 + 4 * j < nblk) consume(j);
-
-    // Per 32-row tile: the four waves' sums through LDS (lane l holds dim column l % 32 of each 32-dim half and rows
-    // acc_row(i, l)), then own part, gate and e5m2 bytes, four dims per thread.
-    const int act_k = a.Hq * 256;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) red[wave][acc_row(i, lane) * RPITCH + dt * 32 + (lane & 31)] = acc[qt][dt][i];
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int row = (tid >> 4) + 16 * it, q = qt * 32 + row;
-            if (q < NQ) {
-                v4f cache = *(const v4f*)&red[0][row * RPITCH + 4 * dg];
-#pragma unroll
-                for (int w = 1; w < 4; ++w) cache += *(const v4f*)&red[w][row * RPITCH + 4 * dg];
-                float gt[4];
-                unpack4(gate[qt][it], gt);
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float own = 0.0f;
-                    for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vq[tp][4 * dg + e];
-                    o[e] = rbf(rbf(cache[e]) + rbf(own));
-                    o[e] = rbf(o[e] * rbf(sigmoidf_(gt[e])));
-                }
-                const uint32_t bytes = pk_e5m2(o[0], o[1], o[2], o[3]);
-                const int g = q / K, t = q % K;
-                *(uint32_t*)(a.act + act_offset(b * K + t, (kvh * G + g) * 256 + dq + 4 * dg, act_k)) = bytes;
-            }
+        if (g + j < g_hi) {
+            bf16_t* w = wt + (j % NT) * TILE;
+            form(j, g + j, w);
+            __syncthreads();
+            mfma(j, w);
         }
-        __syncthreads();
-    }
 
-    // The step's own keys and values into the cache (model.py:603-608, 653-654); inactive rows write the tail.
-    const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
-    const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f;
-    for (int i = tid; i < K * 64; i += 256) {
-        const int t = i >> 6, d = dq + (i & 63), p = base + t;
-        if (p < 0 || p >= S) continue;
-        const size_t ko = (head * S + p) * 256 + d, vo = head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31);
-        if constexpr (KV8) {
-            ((uint8_t*)a.k_cache)[ko] = (uint8_t)kv_code(kq[t][i & 63], ksc);
-            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vq[t][i & 63], vsc);
-        } else {
-            a.k_cache[ko] = f2bf(kq[t][i & 63]);
-            a.v_cache[vo] = f2bf(vq[t][i & 63]);
-        }
+    if (ns == 1) {
+        pv_finish<QT, KV8>(a, b, kvh, head, acc, (float*)smem, wown, vown, tid, lane, wave);
+        return;
     }
+    // This split's sums, [pair][split][tile][wave][i][lane] (each store 256 contiguous bytes).
+    float* part = a.pv_part + ((size_t)hh * ns + z) * QT * 8192 + wave * 1024 + lane;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part[qt * 8192 + i * 64] = acc[qt][i];
+}
+
+// The splits' sums of one (row, KV head) added in split order, then the row finished as attn_pv finishes it.
+template <int QT, bool KV8>
+__global__ __launch_bounds__(512) void attn_pv_finish_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float red[32 * PV_RP];
+    __shared__ float mx[QT * 32], inv[QT * 32], wown[QT * 32][ATTN_KMAX], sred[512];
+    __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX][256];
+    const int hh = blockIdx.x, b = hh / a.Hkv, kvh = hh % a.Hkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int npos = visible(a, b), ns = a.pv_splits;
+    if (npos <= a.fused_max) return;
+    const size_t head = (size_t)hh;
+    const float* part = a.pv_part + (size_t)hh * ns * QT * 8192 + wave * 1024 + lane;
+    v16f acc[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[qt][i] = part[qt * 8192 + i * 64];
+#pragma unroll 4
+    for (int z = 1; z < ns; ++z)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[qt][i] += part[((size_t)z * QT + qt) * 8192 + i * 64];
+    pv_row_stats<QT>(a, head, npos, tid, mx, inv, wown, sred);
+    pv_own_values(a, head, tid, vown);
+    pv_finish<QT, KV8>(a, b, kvh, head, acc, red, wown, vown, tid, lane, wave);
 }
 
 template <int QT, int NB, bool KV8>
@@ -780,8 +856,15 @@ hipError_t launch_attn(AttnArgs a, hipStream_t stream) {
     a.fused_max = NB * ATTN_CHUNK;
     hipLaunchKernelGGL((attn_fused_kernel<QT, NB, KV8>), dim3(a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
     if (a.S > a.fused_max) {
+        // Splits of each (row, KV head)'s positions for attn_pv: about two workgroups per CU in all, as many as the
+        // partial buffer holds.
+        const long pairs = (long)a.B * a.Hkv;
+        int ns = pairs >= 2L * a.cus ? 1 : (int)std::min<long>(PV_SPLIT_MAX, std::max<long>(1, 2L * a.cus / pairs));
+        while (ns > 1 && (size_t)pairs * ns * QT * 8192 > a.pv_part_floats) --ns;
+        a.pv_splits = ns;
         hipLaunchKernelGGL((attn_scores_kernel<QT, KV8>), dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
-        hipLaunchKernelGGL((attn_out_kernel<QT, KV8>), dim3(4 * a.B * a.Hkv), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((attn_pv_kernel<QT, KV8>), dim3(ns, pairs), dim3(512), 0, stream, a);
+        if (ns > 1) hipLaunchKernelGGL((attn_pv_finish_kernel<QT, KV8>), dim3(pairs), dim3(512), 0, stream, a);
     }
     return hipGetLastError();
 }

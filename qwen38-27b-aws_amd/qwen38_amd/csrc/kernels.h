@@ -154,11 +154,15 @@ struct AttnArgs {
     bf16_t* k_cache;
     bf16_t* v_cache;
     int nchunks;            // chunks of ATTN_CHUNK cached positions over S
-    bf16_t* scores;         // [B*Hkv][ATTN_QMAX][S]: the scores times 16 (bf16-exact); attn_out forms exp(s - chunk max)
+    bf16_t* scores;         // [B*Hkv][ATTN_QMAX][S]: the scores times 16 (bf16-exact); attn_pv forms exp(s - chunk max)
     float* stats;           // [B*Hkv][nchunks][ATTN_QMAX][2]: per chunk, max and sum of exp(score - max)
     float* own;             // [B*Hkv][ATTN_QMAX][ATTN_KMAX]: scores of the step's own keys (-inf where masked)
     float* kv_own;          // [B*Hkv][2][ATTN_KMAX][256]: the step's keys (normed, rotated) and values
     bf16_t* qprep;          // [B*Hkv][ATTN_QMAX][256]: query rows normed and rotated, for the rows attn_scores takes
+    float* pv_part;         // attn_pv's split sums, [B*Hkv][pv_splits][query tiles][8192]
+    size_t pv_part_floats;  // its capacity (splits are capped to fit)
+    int pv_splits;          // set by the launcher
+    int cus;                // compute units of the device
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
     float eps;
     int fused_max;          // set by the launcher: rows with at most this many visible positions take attn_fused
