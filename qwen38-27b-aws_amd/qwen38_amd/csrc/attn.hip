@@ -10,20 +10,24 @@
 //
 // Rows whose visible context is at most NB * 512 positions take one launch, attn_fused (KV head, row): sixteen
 // waves score NB blocks of 32 positions each, the softmax completes in the workgroup, and each wave then multiplies
-// the weights with 16 dims of V (NB = 2 for up to 32 query rows per KV head, else 1). Longer contexts take two
-// more launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the other
-// path takes); for them attn_fused only prepares the row once: its query rows normed and rotated (qprep) and the
-// step's own keys, normed and rotated, and values (kv_own).
+// the weights with 16 dims of V (NB = 2 for up to 32 query rows per KV head, else 1). Longer contexts take two or
+// three more launches, so that every (row, KV head) spreads over several workgroups (each kernel skips the rows the
+// other path takes); for them attn_fused only prepares the row once: its query rows normed and rotated (qprep) and
+// the step's own keys, normed and rotated, and values (kv_own).
 //   attn_scores (chunk of 512 cached positions, KV head, row): the prepared query rows, the chunk's scores by MFMA
 //       (sixteen waves, one block of 32 positions each), the chunk's per-row max m_c, the sum s_c of e = exp(s - m_c),
-//       and the scores s themselves (stored as bf16: each is bf16 / 16, so two bytes hold it exactly). Chunk 0 also
-//       scores the step's own keys.
-//   attn_out (quarter of the 256 dims, KV head, row): the row's max M and sum S = sum_c s_c e^(m_c - M) (chunk order)
-//       + own terms; e = exp(s - m_c) again from the stored scores (the same float32 values attn_scores summed);
-//       bf16 weights bf16(e * (e^(m_c - M) / S)) formed in registers and multiplied with V by MFMA over
-//       all visible positions (four waves, added in wave order); the own part, the gate, e5m2 activation tiles for
-//       o_proj; then the step's keys and values into the cache. The weights differ from the reference's
-//       bf16(e^(s - M) / S) by a few float32 ulps before the bf16 rounding (the product of two exponentials).
+//       and the scores s themselves (stored as bf16: each is bf16 / 16, so two bytes hold it exactly; rows past the
+//       real query rows are not stored). Chunk 0 also scores the step's own keys.
+//   attn_pv (split of the row's positions, KV head, row; eight waves, all 256 dims): the row's max M and sum
+//       S = sum_c s_c e^(m_c - M) + own terms; per group of 64 positions, each bf16 weight bf16(e * (e^(m_c - M) / S))
+//       formed once from the stored scores (e = exp(s - m_c), the same float32 values attn_scores summed) into LDS,
+//       and multiplied with V by MFMA, each wave 32 dims, groups added in position order. With one split per row it
+//       finishes the row (below); with more, it stores its sums.
+//   attn_pv_finish (quarter of the dims, KV head, row; only with several splits): the splits' sums added in split
+//       order, then the row finished: the own part, the gate, e5m2 activation tiles for o_proj, the step's keys and
+//       values into the cache.
+//   The weights differ from the reference's bf16(e^(s - M) / S) by a few float32 ulps before the bf16 rounding (the
+//   product of two exponentials).
 //
 // FP8 KV cache (KV8; the reference's kv_cache_format "fp8", model.py:557-601 with its CPU path's _store / _load /
 // _round_trip): the same layouts with one e4m3 byte of value / scale per element. Cached keys and values widen to
@@ -616,29 +620,34 @@ __device__ __forceinline__ void pv_row_stats(const AttnArgs& a, size_t head, int
     }
 }
 
-// The step's own values (float32) into LDS, for the own part of the output.
-__device__ __forceinline__ void pv_own_values(const AttnArgs& a, size_t head, int tid, float (*vown)[256]) {
-    const float* src = a.kv_own + (head * 2 + 1) * ATTN_KMAX * 256;
-    for (int i = tid * 4; i < a.K * 256; i += 512 * 4) *(v4f*)&vown[i >> 8][i & 255] = *(const v4f*)(src + i);
+// The step's own values (float32), dims dbase .. dbase + 32 NW - 1, into LDS ([K][32 NW]), for the own part of the
+// output; NW * 64 threads.
+template <int NW>
+__device__ __forceinline__ void pv_own_values(const AttnArgs& a, size_t head, int dbase, int tid, float* vown) {
+    constexpr int D = 32 * NW;
+    const float* src = a.kv_own + (head * 2 + 1) * ATTN_KMAX * 256 + dbase;
+    for (int i = tid * 4; i < a.K * D; i += NW * 64 * 4) *(v4f*)&vown[i] = *(const v4f*)(src + (i / D) * 256 + i % D);
 }
 
-// The output of one (row, KV head) from the weights x V sums in acc (wave w: dims 32w + l % 32 of its lane l, query
-// rows acc_row(i, l) of each 32-row tile): own part, gate and e5m2 activation bytes, as the reference adds them
-// (cache part and own part as separate bf16 matmuls added in bf16, then times bf16 sigmoid(gate)); then the step's
-// own keys and values into the cache (model.py:603-608, 653-654; inactive rows write the tail). Every wave has
-// consumed its V loads before the first barrier here, so the cache writes come after every read of this row's V in
-// the workgroup.
-template <int QT, bool KV8>
-__device__ __forceinline__ void pv_finish(const AttnArgs& a, int b, int kvh, size_t head, v16f (&acc)[QT], float* red,
-                                          const float (*wown)[ATTN_KMAX], const float (*vown)[256], int tid, int lane,
+// The output of one (row, KV head) from the weights x V sums in acc (NW waves; wave w: dims dbase + 32w + l % 32 of
+// its lane l, query rows acc_row(i, l) of each 32-row tile): own part, gate and e5m2 activation bytes, as the
+// reference adds them (cache part and own part as separate bf16 matmuls added in bf16, then times bf16
+// sigmoid(gate)); then the step's own keys and values of these dims into the cache (model.py:603-608, 653-654;
+// inactive rows write the tail). Every wave has consumed its V loads before the first barrier here, so the cache
+// writes come after every read of this row's V in the workgroup. red holds 32 x (32 NW + 4) floats, vown the own
+// values of these dims ([K][32 NW]).
+template <int QT, bool KV8, int NW>
+__device__ __forceinline__ void pv_finish(const AttnArgs& a, int b, int kvh, size_t head, int dbase, v16f (&acc)[QT],
+                                          float* red, const float (*wown)[ATTN_KMAX], const float* vown, int tid, int lane,
                                           int wave) {
+    constexpr int D = 32 * NW, RP = D + 4, TPR = 2 * NW;  // dims, LDS row pitch, threads per row
     const int K = a.K, G = a.Hq / a.Hkv, NQ = G * K, S = a.S, act_k = a.Hq * 256;
-    const int fr = tid >> 4, d0 = (tid & 15) * 16;  // this thread: row fr of each tile, dims d0 .. d0 + 15
+    const int fr = tid / TPR, dl = (tid % TPR) * 16;  // this thread: row fr of each tile, dims dbase + dl .. + 15
     u4t gate[QT][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const int q = min(qt * 32 + fr, NQ - 1);
-        const bf16_t* gp = a.qkv + (size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + d0;
+        const bf16_t* gp = a.qkv + (size_t)(b * K + q % K) * a.ld + (size_t)(kvh * G + q / K) * 512 + 256 + dbase + dl;
         gate[qt][0] = *(const u4t*)gp;
         gate[qt][1] = *(const u4t*)(gp + 8);
     }
@@ -646,45 +655,46 @@ __device__ __forceinline__ void pv_finish(const AttnArgs& a, int b, int kvh, siz
     for (int qt = 0; qt < QT; ++qt) {
         __syncthreads();  // the weight tiles' last reads (or the previous tile's) are done
 #pragma unroll
-        for (int i = 0; i < 16; ++i) red[acc_row(i, lane) * PV_RP + wave * 32 + (lane & 31)] = acc[qt][i];
+        for (int i = 0; i < 16; ++i) red[acc_row(i, lane) * RP + wave * 32 + (lane & 31)] = acc[qt][i];
         __syncthreads();
         const int q = qt * 32 + fr;
         if (q < NQ) {
             uint32_t bytes[4];
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
-                const v4f cache = *(const v4f*)&red[fr * PV_RP + d0 + 4 * h];
+                const v4f cache = *(const v4f*)&red[fr * RP + dl + 4 * h];
                 const u4t gw = gate[qt][h >> 1];
                 float gt[4], o[4];
                 unpack4(make_uint2(gw[(h & 1) * 2], gw[(h & 1) * 2 + 1]), gt);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float own = 0.0f;
-                    for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vown[tp][d0 + 4 * h + e];
+                    for (int tp = 0; tp < K; ++tp) own += wown[q][tp] * vown[tp * D + dl + 4 * h + e];
                     o[e] = rbf(rbf(cache[e]) + rbf(own));
                     o[e] = rbf(o[e] * rbf(sigmoidf_(gt[e])));
                 }
                 bytes[h] = pk_e5m2(o[0], o[1], o[2], o[3]);
             }
-            const int t = q % K, col = (kvh * G + q / K) * 256 + d0;
+            const int t = q % K, col = (kvh * G + q / K) * 256 + dbase + dl;
             *(uint2*)(a.act + act_offset(b * K + t, col, act_k)) = make_uint2(bytes[0], bytes[1]);
             *(uint2*)(a.act + act_offset(b * K + t, col + 8, act_k)) = make_uint2(bytes[2], bytes[3]);
         }
     }
 
     const int base = a.active[b] > 0.5f ? a.position[b] : S - K;
-    const float* kown = a.kv_own + head * 2 * ATTN_KMAX * 256;
+    const float* kown = a.kv_own + head * 2 * ATTN_KMAX * 256 + dbase;
     const float ksc = KV8 ? bf2f(*a.k_scale) : 0.0f, vsc = KV8 ? bf2f(*a.v_scale) : 0.0f;
-    for (int i = tid; i < K * 256; i += 512) {
-        const int t = i >> 8, d = i & 255, p = base + t;
+    for (int i = tid; i < K * D; i += NW * 64) {
+        const int t = i / D, d = i % D, p = base + t;
         if (p < 0 || p >= S) continue;
-        const size_t ko = (head * S + p) * 256 + d, vo = head * S * 256 + (size_t)(p >> 5) * 8192 + d * 32 + (p & 31);
+        const size_t ko = (head * S + p) * 256 + dbase + d,
+                     vo = head * S * 256 + (size_t)(p >> 5) * 8192 + (dbase + d) * 32 + (p & 31);
         if constexpr (KV8) {
             ((uint8_t*)a.k_cache)[ko] = (uint8_t)kv_code(kown[t * 256 + d], ksc);
-            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vown[t][d], vsc);
+            ((uint8_t*)a.v_cache)[vo] = (uint8_t)kv_code(vown[t * D + d], vsc);
         } else {
             a.k_cache[ko] = f2bf(kown[t * 256 + d]);
-            a.v_cache[vo] = f2bf(vown[t][d]);
+            a.v_cache[vo] = f2bf(vown[t * D + d]);
         }
     }
 }
@@ -748,7 +758,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     for (int j = 0; j < PF; ++j) issue(j, g_lo + j);
 
     pv_row_stats<QT>(a, head, npos, tid, mx, inv, wown, sred);
-    if (ns == 1) pv_own_values(a, head, tid, vown);
+    if (ns == 1) pv_own_values<8>(a, head, 0, tid, &vown[0][0]);
     __syncthreads();
 
     v16f acc[QT];
@@ -812,8 +822,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         }
 
     if (ns == 1) {
-        pv_finish<QT, KV8>(a, b, kvh, head, acc, (float*)smem, wown, vown, tid, lane, wave);
+        pv_finish<QT, KV8, 8>(a, b, kvh, head, 0, acc, (float*)smem, wown, &vown[0][0], tid, lane, wave);
         return;
+    }
+    if (z == 0 && tid < QT * 32) {  // the row statistics attn_pv_finish needs
+        float* rs = a.pv_rows + (head * ATTN_QMAX + tid) * (2 + ATTN_KMAX);
+        rs[0] = mx[tid];
+        rs[1] = inv[tid];
+#pragma unroll
+        for (int tp = 0; tp < ATTN_KMAX; ++tp) rs[2 + tp] = wown[tid][tp];
     }
     // This split's sums, [pair][split][tile][wave][i][lane] (each store 256 contiguous bytes).
     float* part = a.pv_part + ((size_t)hh * ns + z) * QT * 8192 + wave * 1024 + lane;
@@ -823,18 +840,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         for (int i = 0; i < 16; ++i) part[qt * 8192 + i * 64] = acc[qt][i];
 }
 
-// The splits' sums of one (row, KV head) added in split order, then the row finished as attn_pv finishes it.
+// The splits' sums of one (row, KV head) added in split order, then the row finished as attn_pv finishes it; one
+// workgroup of two waves per quarter of the 256 dims (blockIdx.x), with the row statistics split 0 stored.
 template <int QT, bool KV8>
-__global__ __launch_bounds__(512) void attn_pv_finish_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float red[32 * PV_RP];
-    __shared__ float mx[QT * 32], inv[QT * 32], wown[QT * 32][ATTN_KMAX], sred[512];
-    __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX][256];
-    const int hh = blockIdx.x, b = hh / a.Hkv, kvh = hh % a.Hkv;
+__global__ __launch_bounds__(128) void attn_pv_finish_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float red[32 * 68];
+    __shared__ float wown[QT * 32][ATTN_KMAX];
+    __shared__ __attribute__((aligned(16))) float vown[ATTN_KMAX * 64];
+    const int quarter = blockIdx.x, hh = blockIdx.y, b = hh / a.Hkv, kvh = hh % a.Hkv;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int npos = visible(a, b), ns = a.pv_splits;
     if (npos <= a.fused_max) return;
     const size_t head = (size_t)hh;
-    const float* part = a.pv_part + (size_t)hh * ns * QT * 8192 + wave * 1024 + lane;
+    const float* part = a.pv_part + (size_t)hh * ns * QT * 8192 + (quarter * 2 + wave) * 1024 + lane;
     v16f acc[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
@@ -846,9 +864,10 @@ __global__ __launch_bounds__(512) void attn_pv_finish_kernel(const AttnArgs a) {
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[qt][i] += part[((size_t)z * QT + qt) * 8192 + i * 64];
-    pv_row_stats<QT>(a, head, npos, tid, mx, inv, wown, sred);
-    pv_own_values(a, head, tid, vown);
-    pv_finish<QT, KV8>(a, b, kvh, head, acc, red, wown, vown, tid, lane, wave);
+    for (int i = tid; i < QT * 32 * ATTN_KMAX; i += 128)
+        wown[i / ATTN_KMAX][i % ATTN_KMAX] = a.pv_rows[(head * ATTN_QMAX + i / ATTN_KMAX) * (2 + ATTN_KMAX) + 2 + i % ATTN_KMAX];
+    pv_own_values<2>(a, head, quarter * 64, tid, vown);
+    pv_finish<QT, KV8, 2>(a, b, kvh, head, quarter * 64, acc, red, wown, vown, tid, lane, wave);
 }
 
 template <int QT, int NB, bool KV8>
@@ -864,7 +883,7 @@ hipError_t launch_attn(AttnArgs a, hipStream_t stream) {
         a.pv_splits = ns;
         hipLaunchKernelGGL((attn_scores_kernel<QT, KV8>), dim3(a.nchunks, a.Hkv, a.B), dim3(SW * 64), 0, stream, a);
         hipLaunchKernelGGL((attn_pv_kernel<QT, KV8>), dim3(ns, pairs), dim3(512), 0, stream, a);
-        if (ns > 1) hipLaunchKernelGGL((attn_pv_finish_kernel<QT, KV8>), dim3(pairs), dim3(512), 0, stream, a);
+        if (ns > 1) hipLaunchKernelGGL((attn_pv_finish_kernel<QT, KV8>), dim3(4, pairs), dim3(128), 0, stream, a);
     }
     return hipGetLastError();
 }

@@ -89,7 +89,7 @@ struct q38_handle {
     int parity = 0;
     // workspace carve-up
     size_t off_x, off_hbf, off_tmp, off_act_h, off_act_mid, off_act_ffn, off_z, off_qkv, off_part,
-        off_scores, off_astats, off_aown, off_akv, off_aq, off_apv, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos,
+        off_scores, off_astats, off_aown, off_akv, off_aq, off_apv, off_apr, off_htiles, off_x32, off_maxima, off_sp_embeds, off_sp_cos,
         off_sp_sin, off_sp_states, off_sp_out, off_sp_current, off_sp_ids, off_sp_at, off_sp_draft, off_gemm, off_gates, off_status,
         workspace_bytes;
     // prefill scratch (with a prefill chunk in the config)
@@ -526,6 +526,7 @@ int run_mixer(q38_handle* h, int li, const StepIO& io, int rd, int wr, hipStream
         a.qprep = (bf16_t*)h->ws(h->off_aq);
         a.pv_part = (float*)h->ws(h->off_apv);
         a.pv_part_floats = h->attn_pv_floats;
+        a.pv_rows = (float*)h->ws(h->off_apr);
         a.cus = device_cus();
         a.act = act_mid;
         a.eps = h->cfg.rms_norm_eps;
@@ -709,6 +710,7 @@ int q38_create(const q38_config* cfg, q38_handle** out) {
     // attn_pv's split sums: at most about two workgroups per CU of 64 query rows x 256 dims each.
     h->attn_pv_floats = h->attn_nchunks > 1 ? (size_t)2 * device_cus() * ATTN_QMAX * 256 : 0;
     h->off_apv = take(h->attn_pv_floats * 4);
+    h->off_apr = take(heads * ATTN_QMAX * (2 + ATTN_KMAX) * 4);
     h->off_htiles = take(Tv * H * 2);
     h->off_x32 = take(Tv * H * 4);
     h->off_maxima = take(Tv * (h->V / 32) * 4);

@@ -161,6 +161,7 @@ struct AttnArgs {
     bf16_t* qprep;          // [B*Hkv][ATTN_QMAX][256]: query rows normed and rotated, for the rows attn_scores takes
     float* pv_part;         // attn_pv's split sums, [B*Hkv][pv_splits][query tiles][8192]
     size_t pv_part_floats;  // its capacity (splits are capped to fit)
+    float* pv_rows;         // [B*Hkv][ATTN_QMAX][2 + ATTN_KMAX]: per query row M, 1 / S and the own weights, for attn_pv_finish
     int pv_splits;          // set by the launcher
     int cus;                // compute units of the device
     uint8_t* act;           // e5m2 activation tiles of width Hq*256 for o_proj
