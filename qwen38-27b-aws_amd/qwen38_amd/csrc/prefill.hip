@@ -6,7 +6,8 @@
 //   gdn_prefill_prep   (token, key head): conv over the chunk with the row's conv history (bf16 tap products summed
 //                      by bf16 additions, model.py:514), SiLU, l2 norms of q and k, the gates times `valid`
 //   gdn_prefill_scan   (value head, 32 state columns): the gated delta rule token by token in float32 from the row's
-//                      state (times `start > 0`), the state kept in registers; per token S = e^g S, delta = (v - S^T
+//                      state (times `start > 0`), the state kept in registers, the tokens' k, q, v, beta and g staged
+//                      through LDS a round ahead; per token S = e^g S, delta = (v - S^T
 //                      k) beta, S += k delta^T, o = S^T q. The reference runs the same rule in pieces of 128 tokens
 //                      (chunked_gated_delta, model.py:88-124); both are the same sums in float32, in another order.
 //   gdn_prefill_finish (token, 4 value heads): o to bf16, gated RMS norm times SiLU(z), e5m2 tiles for out_proj
@@ -90,11 +91,13 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(const PrefillGdnA
     }
 }
 
-// Grid (value head, group of 32 state columns); thread (column c = tid / 8, rows 16 (tid % 8) + [0, 16)).
+// Grid (value head, group of 32 state columns); thread (column c = tid / 8, rows 16 (tid % 8) + [0, 16)). Tokens are
+// staged through LDS 16 at a time in two buffers: each round's loads are issued into registers before the round
+// before it runs, so their latency hides behind its 16 token steps.
 __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(const PrefillGdnArgs a) {
     constexpr int D = 128, TB = 16;  // tokens staged per round
-    __shared__ __attribute__((aligned(16))) float sk[TB][D], sq[TB][D];
-    __shared__ float sv[TB][32], sb[TB], sg[TB];
+    __shared__ __attribute__((aligned(16))) float sk[2][TB][D], sq[2][TB][D];
+    __shared__ float sv[2][TB][32], sb[2][TB], sg[2][TB];
     const int h = blockIdx.x, grp = blockIdx.y, tid = threadIdx.x;
     const int Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
     const int c = tid >> 3, r = tid & 7, j = grp * 32 + c, i0 = r * 16;
@@ -106,32 +109,48 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(const PrefillGdnA
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = bf2f(st[(size_t)(i0 + e) * D + j]) * keep;
 
-    for (int t0 = 0; t0 < a.L; t0 += TB) {
-        __syncthreads();  // the last round's reads are done
-        const int nt = min(TB, a.L - t0);
-        for (int e = tid; e < TB * D / 4; e += 256) {
-            const int tt = e / (D / 4), d = (e % (D / 4)) * 4;
-            if (tt < nt) {
-                *(float4*)&sk[tt][d] = *(const float4*)(a.kn + ((size_t)(t0 + tt) * Hk + kh) * D + d);
-                *(float4*)&sq[tt][d] = *(const float4*)(a.qn + ((size_t)(t0 + tt) * Hk + kh) * D + d);
-            }
+    // One round's loads: 2 float4 of k and of q, 2 values of v, and beta and g for threads 0 .. TB - 1; tokens past
+    // the chunk load its last token (never used).
+    static_assert(TB * D / 4 == 2 * 256 && TB * 32 == 2 * 256, "two pieces per thread");
+    float4 rk[2], rq[2];
+    float rv[2], rb = 0.0f, rg = 0.0f;
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = tid + 256 * u, t = min(t0 + e / (D / 4), a.L - 1), d = (e % (D / 4)) * 4;
+            rk[u] = *(const float4*)(a.kn + ((size_t)t * Hk + kh) * D + d);
+            rq[u] = *(const float4*)(a.qn + ((size_t)t * Hk + kh) * D + d);
+            const int tv = min(t0 + e / 32, a.L - 1);
+            rv[u] = a.v[((size_t)tv * Hv + h) * D + grp * 32 + e % 32];
         }
-        for (int e = tid; e < TB * 32; e += 256) {
-            const int tt = e / 32;
-            if (tt < nt) sv[tt][e % 32] = a.v[((size_t)(t0 + tt) * Hv + h) * D + grp * 32 + e % 32];
+        const int tb = min(t0 + (tid & (TB - 1)), a.L - 1);
+        rb = a.beta[(size_t)tb * Hv + h];
+        rg = a.g[(size_t)tb * Hv + h];
+    };
+    load(0);
+    for (int t0 = 0, buf = 0; t0 < a.L; t0 += TB, buf ^= 1) {
+        // Buffer buf was last read two rounds ago, before every thread passed the last round's barrier.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = tid + 256 * u, tt = e / (D / 4), d = (e % (D / 4)) * 4;
+            *(float4*)&sk[buf][tt][d] = rk[u];
+            *(float4*)&sq[buf][tt][d] = rq[u];
+            sv[buf][e / 32][e % 32] = rv[u];
         }
-        if (tid < TB && tid < nt) {
-            sb[tid] = a.beta[(size_t)(t0 + tid) * Hv + h];
-            sg[tid] = a.g[(size_t)(t0 + tid) * Hv + h];
+        if (tid < TB) {
+            sb[buf][tid] = rb;
+            sg[buf][tid] = rg;
         }
         __syncthreads();
+        if (t0 + TB < a.L) load(t0 + TB);
+        const int nt = min(TB, a.L - t0);
         for (int tt = 0; tt < nt; ++tt) {
-            const float e = expf(sg[tt]);
+            const float e = expf(sg[buf][tt]);
             float kv[16], qv[16];
 #pragma unroll
             for (int q = 0; q < 16; q += 4) {
-                *(float4*)&kv[q] = *(const float4*)&sk[tt][i0 + q];
-                *(float4*)&qv[q] = *(const float4*)&sq[tt][i0 + q];
+                *(float4*)&kv[q] = *(const float4*)&sk[buf][tt][i0 + q];
+                *(float4*)&qv[q] = *(const float4*)&sq[buf][tt][i0 + q];
             }
             float ks = 0.0f;
 #pragma unroll
@@ -140,7 +159,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(const PrefillGdnA
                 ks += s[q] * kv[q];
             }
             ks = group8_sum(ks);
-            const float delta = (sv[tt][c] - ks) * sb[tt];
+            const float delta = (sv[buf][tt][c] - ks) * sb[buf][tt];
             float os = 0.0f;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
