@@ -3,7 +3,8 @@
 The golden scenario's contexts are short; these cases spread each (row, KV head) over many chunks (the tiny block at
 2048 positions, with 4 tokens per row and with 1 as in decode), take the one-launch path with one and with two blocks
 of 512 positions per wave, take the 64-query-row path (16 query heads over 2 KV heads, 8 tokens), run 512 (row, KV
-head) pairs (each row's weights x V in one workgroup, at 32 and 64 query rows), and include an empty cache and
+head) pairs (each row's weights x V in one workgroup, at 32 and 64 query rows), run a cache whose length is not a
+whole number of 64-position groups (contexts ending at its edge), and include an empty cache and
 inactive rows (which write the cache tail), each with a bf16 cache and with an FP8 one (e4m3 bytes with the layer's
 scales). Checked: the
 MTP output (one layer, held to the north-star 2e-2 per row), the positions the step writes in
@@ -35,6 +36,9 @@ CASES = {
     "fused-two-blocks": (8, 4, 4, 1024, [1019, 513, 767, 1000], [True, True, True, False]),
     # one token per row, as the decode step runs it, over many chunks
     "one-token-2048": (8, 4, 1, 2048, [2000, 1025, 0, 600], [True, True, True, False]),
+    # a cache of 49 blocks of 32 positions (not whole groups of 64): the last group's second block lies past the
+    # cache, rows' contexts end inside and at the edge of it
+    "ragged-1568": (8, 4, 4, 1568, [1563, 1100, 1539, 1201], [True, True, True, False]),
     # 512 (row, KV head) pairs: the weights x V pass takes each row's positions in one workgroup, which then finishes
     # the row itself (fewer pairs split the positions and finish in a second kernel), with 32 and with 64 query rows
     "512-pairs-1536": (8, 256, 4, 1536, [1025 + (37 * r) % 507 for r in range(256)], [r % 17 != 5 for r in range(256)]),
