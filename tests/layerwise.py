@@ -32,6 +32,7 @@ import torch
 from oracle import model as om
 from qwen38_amd import synth
 from qwen38_amd.config import LINEAR, with_layers
+from qwen38_amd.quant import decode_kv, encode_kv
 from qwen38_amd.steps import Engine, VerifyStep
 
 HIDDEN_TOL, STATE_TOL = 2e-2, 1e-2
@@ -65,36 +66,52 @@ def gdn_state_from(engine: Engine, cfg) -> dict:
     return st
 
 
-def kv_state_from(engine: Engine) -> dict:
+def kv_state_from(engine: Engine, scales=None) -> dict:
+    """The layer's caches on the host; with an FP8 cache (``scales`` = (k_scale, v_scale)) the bytes and the scales, as
+    the oracle's attention takes them."""
     kc, vc = engine.get_kv(0)
-    return {"k_cache": kc.cpu(), "v_cache": vc.cpu()}
+    st = {"k_cache": kc.cpu(), "v_cache": vc.cpu()}
+    if scales is not None:
+        st["k_scale"], st["v_scale"] = scales
+    return st
 
 
-def seeded_states(cfg, batch: int, tokens: int, max_seq_len: int, context, seed: int, device="cuda"):
+def seeded_states(cfg, batch: int, tokens: int, max_seq_len: int, context, seed: int, device="cuda", kv: str = "bf16"):
     """Per-layer starting states: unit-RMS gated-delta and conv states with empty snapshots, caches filled below each
-    row's context (synth.gdn_states / synth.kv_states), made one layer at a time."""
+    row's context (synth.gdn_states / synth.kv_states), made one layer at a time; with ``kv`` "fp8" the caches as
+    e4m3 bytes of the layer's scales (synth.kv_scales), with the scales."""
     for i, kind in enumerate(cfg.layer_types):
         one = with_layers(cfg, (kind,))
         if kind == LINEAR:
             yield synth.gdn_states(one, batch, tokens, seed, f"layers.{i}", device=device)
         else:
-            yield synth.kv_states(one, batch, max_seq_len, context, seed, f"layers.{i}", device=device)
+            st = synth.kv_states(one, batch, max_seq_len, context, seed, f"layers.{i}", device=device)
+            if kv == "fp8":
+                ks, vs = synth.kv_scales(one, seed, f"layers.{i}")
+                st = {"k_cache": encode_kv(st["k_cache"], ks.to(device)), "v_cache": encode_kv(st["v_cache"], vs.to(device)),
+                      "k_scale": ks, "v_scale": vs}
+            yield st
 
 
 class LayerStack:
     """One one-layer engine per decoder layer of ``cfg``, loaded with ``values`` and the per-layer ``states``
     (reference shapes; consumed layer by layer so a caller can pass a generator), each with its probe bound."""
 
-    def __init__(self, cfg, values: dict, batch: int, tokens: int, max_seq_len: int, states, projection_mfma: str = "bf16"):
+    def __init__(self, cfg, values: dict, batch: int, tokens: int, max_seq_len: int, states, projection_mfma: str = "bf16",
+                 kv_cache_format: str = "bf16"):
         self.cfg, self.batch, self.tokens, self.max_seq_len = cfg, batch, tokens, max_seq_len
-        self.engines, self.weights = [], []
+        self.engines, self.weights, self.kv_scales = [], [], {}
         for i, (kind, st) in enumerate(zip(cfg.layer_types, states)):
-            engine = Engine(with_layers(cfg, (kind,)), batch, tokens, max_seq_len, mtp=False, projection_mfma=projection_mfma)
+            engine = Engine(with_layers(cfg, (kind,)), batch, tokens, max_seq_len, mtp=False, projection_mfma=projection_mfma,
+                            kv_cache_format=kv_cache_format)
             engine.load(layer_values(values, i).items())
             engine.enable_probe(0)
             if kind == LINEAR:
                 engine.set_gdn(0, st)
             else:
+                if "k_scale" in st:
+                    self.kv_scales[i] = (st["k_scale"].cpu(), st["v_scale"].cpu())
+                    engine.set_kv_scales(0, st["k_scale"].cuda(), st["v_scale"].cuda())
                 engine.set_kv(0, st["k_cache"], st["v_cache"])
             del st
             self.engines.append(engine)
@@ -109,7 +126,7 @@ class LayerStack:
         args = (cpu_inputs["cos"], cpu_inputs["sin"], cpu_inputs["position"], cpu_inputs["active"], cpu_inputs["accepted"])
         for i, (kind, engine, w) in enumerate(zip(cfg.layer_types, self.engines, self.weights)):
             one = with_layers(cfg, (kind,))
-            before = gdn_state_from(engine, one) if kind == LINEAR else kv_state_from(engine)
+            before = gdn_state_from(engine, one) if kind == LINEAR else kv_state_from(engine, self.kv_scales.get(i))
             y = VerifyStep(engine)(inputs_embeds=x, **inputs)
             torch.cuda.synchronize()
             probe = {name: t.cpu().clone() for name, t in engine.probe(0).items()}
@@ -117,7 +134,7 @@ class LayerStack:
                 errs = gdn_layer_errors(one, w, x.cpu(), y.cpu(), probe, gdn_state_from(engine, one), before, args,
                                         MODE_TOL[engine.projection_mfma])
             else:
-                errs = attention_layer_errors(self, one, w, x.cpu(), y.cpu(), probe, kv_state_from(engine), before, args,
+                errs = attention_layer_errors(self, one, w, x.cpu(), y.cpu(), probe, kv_state_from(engine, self.kv_scales.get(i)), before, args,
                                               cpu_inputs, i, MODE_TOL[engine.projection_mfma])
             for name, e in errs.items():
                 if name.startswith("_"):
@@ -295,19 +312,33 @@ def mixer_output_stage(cfg, x, probe: dict, pre_mid, out_weight, notes: list, to
 
 
 def kv_errors(stack, got: dict, before: dict, want: dict, cpu_inputs: dict, layer: int) -> dict:
-    """The step's own cache positions against the oracle; every other position must be untouched."""
+    """The step's own cache positions against the oracle; every other position must be untouched. A bf16 cache: the
+    relative error of each written (head, token) row. An FP8 cache: the share of written bytes that differ from the
+    oracle's per batch row (``k_cache``, ``v_cache``) and the relative error of each written row decoded
+    (``k_cache_decoded``, ``v_cache_decoded``). The layer's keys and values come from the oracle's own projection of the
+    GPU's input, so a near-tie e5m2 input rounded the other way moves a row by a little; its bytes then differ now and
+    then, and a value near zero can move by several of e4m3's fine codes, so single bytes are not held to one code."""
     pos, k, s = cpu_inputs["position"].long(), stack.tokens, stack.max_seq_len
     on = cpu_inputs["active"] > 0.5
+    fp8 = "k_scale" in want
     out = {}
     for name in ("k_cache", "v_cache"):
-        written = []
+        written, decoded = [], []
         for b in range(stack.batch):
             at = slice(int(pos[b]), int(pos[b]) + k) if on[b] else slice(s - k, s)
-            written.append(rel_rows(got[name][b, :, at], want[name][b, :, at], stack.cfg.head_dim))
+            if fp8:
+                g, w = got[name][b, :, at], want[name][b, :, at]
+                written.append((g != w).float().mean().reshape(1))
+                sc = want["k_scale" if name == "k_cache" else "v_scale"]
+                decoded.append(rel_rows(decode_kv(g, sc), decode_kv(w, sc), stack.cfg.head_dim))
+            else:
+                written.append(rel_rows(got[name][b, :, at], want[name][b, :, at], stack.cfg.head_dim))
             keep = torch.ones(s, dtype=torch.bool)
             keep[at] = False
             assert torch.equal(got[name][b][:, keep], before[name][b][:, keep]), f"layer {layer}: {name} row {b} changed elsewhere"
         out[name] = torch.cat(written)
+        if fp8:
+            out[name + "_decoded"] = torch.cat(decoded)
     return out
 
 
